@@ -1,0 +1,298 @@
+// attention.hip - causal self-attention straight from the packed qkv rows.
+//
+// The reference (fast.c:267-298) computes, per (sequence, head), the full
+// T x T score plane S = (1/sqrt(hs)) Q K^T with cblas_sgemm, sets the upper
+// triangle to -1e9 (ops.c:488-493), applies a three-pass row softmax
+// (ops.c:424-482) and multiplies by V. exp(-1e9 - max) is exactly 0 in fp32,
+// so skipping masked keys gives the same probabilities; no score plane is
+// ever written here.
+//
+// k_attn_causal: one workgroup = 4 wavefronts = 128 queries of one
+// (sequence, head). K/V tiles of 64 keys are double-buffered in LDS. Each
+// wavefront computes S^T = K Q^T for its 32 queries with
+// v_mfma_f32_32x32x2f32, so a lane holds one query column: the row max and
+// row sum need one cross-half shuffle, and the probabilities feed the
+// O^T += V^T P^T product directly from the accumulator registers (the key
+// order of the S^T output layout is used as the k order of that product).
+// The softmax is the online (running max / running sum) form.
+//
+// k_attn_row: one query row per (sequence, head) against keys 0..t: the
+// last-position pass (fast.c:287-297) and one decode step.
+#include "common.h"
+#include "kernels.h"
+
+namespace {
+
+constexpr int KT = 64;  // keys per LDS tile
+
+template <int HS>
+__global__ void __launch_bounds__(256, 2)
+    k_attn_causal(const float* __restrict__ qkv, long seq_stride, float* __restrict__ out, int B,
+                  int T, int C, int H, int nqb, float scale) {
+    constexpr int HALF = HS / 2;            // d values per lane half in Q K^T
+    constexpr int F4 = HS / 4;              // float4 per head row
+    constexpr int ROW = HS + 4;             // padded LDS row
+    constexpr int NDB = (HS + 31) / 32;     // 32-row blocks of O^T
+    constexpr int LITERS = (KT * F4 + 255) / 256;
+    __shared__ float Ks[2][KT * ROW];
+    __shared__ float Vs[2][KT * ROW];
+
+    const int BH = B * H;
+    const int qb = nqb - 1 - (int)(blockIdx.x / BH);  // longest query blocks first
+    const int bh = blockIdx.x % BH;
+    const int b = bh / H, h = bh % H;
+    const long C3 = 3L * C;
+    const float* base = qkv + (long)b * seq_stride * C3;
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int lr = lane & 31, lh = lane >> 5;
+    const int q0 = qb * 128 + wave * 32;  // first query of this wavefront
+    const int qi = q0 + lr;                // this lane's query
+    const int q_last_wg = min(qb * 128 + 127, T - 1);
+    const int ntiles = q_last_wg / KT + 1;
+
+    // Q row of this lane's query, d in [lh*HALF, lh*HALF + HALF).
+    float qreg[HALF];
+    {
+        const float* qp = base + (long)min(qi, T - 1) * C3 + h * HS + lh * HALF;
+#pragma unroll
+        for (int s = 0; s < HALF; s += 4) {
+            f32x4 v = *(const f32x4*)(qp + s);
+            qreg[s] = v.x; qreg[s + 1] = v.y; qreg[s + 2] = v.z; qreg[s + 3] = v.w;
+        }
+    }
+
+    f32x4 rk[LITERS], rv[LITERS];
+    auto gload = [&](int kt) {
+#pragma unroll
+        for (int i = 0; i < LITERS; i++) {
+            int idx = tid + 256 * i;
+            if (idx < KT * F4) {
+                int key = min(kt * KT + idx / F4, T - 1);
+                const float* rp = base + (long)key * C3 + h * HS + (idx % F4) * 4;
+                rk[i] = *(const f32x4*)(rp + C);
+                rv[i] = *(const f32x4*)(rp + 2 * C);
+            }
+        }
+    };
+    auto lstore = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < LITERS; i++) {
+            int idx = tid + 256 * i;
+            if (idx < KT * F4) {
+                int o = (idx / F4) * ROW + (idx % F4) * 4;
+                *(f32x4*)&Ks[buf][o] = rk[i];
+                *(f32x4*)&Vs[buf][o] = rv[i];
+            }
+        }
+    };
+
+    f32x16 o[NDB];
+#pragma unroll
+    for (int d = 0; d < NDB; d++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) o[d][r] = 0.f;
+    float m_run = -INFINITY, l_run = 0.f;
+
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    for (int kt = 0; kt < ntiles; kt++) {
+        const int cur = kt & 1;
+        if (kt + 1 < ntiles) gload(kt + 1);
+        // Wave-uniform: skip tiles entirely above this wavefront's queries.
+        if (q0 < T && kt * KT <= q0 + 31) {
+            const float* ks = &Ks[cur][0];
+            const float* vs = &Vs[cur][0];
+            f32x16 s[2];
+#pragma unroll
+            for (int kb = 0; kb < 2; kb++) {
+#pragma unroll
+                for (int r = 0; r < 16; r++) s[kb][r] = 0.f;
+#pragma unroll
+                for (int d = 0; d < HALF; d += 4) {
+                    f32x4 kv = *(const f32x4*)&ks[(kb * 32 + lr) * ROW + lh * HALF + d];
+                    s[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.x, qreg[d], s[kb], 0, 0, 0);
+                    s[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.y, qreg[d + 1], s[kb], 0, 0, 0);
+                    s[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.z, qreg[d + 2], s[kb], 0, 0, 0);
+                    s[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.w, qreg[d + 3], s[kb], 0, 0, 0);
+                }
+            }
+            // s[kb][r] = score of key kt*64 + 32kb + 8(r/4) + 4lh + r%4 for query qi.
+            float mt = -INFINITY;
+#pragma unroll
+            for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    int key = kt * KT + kb * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                    float v = s[kb][r] * scale;
+                    v = (key > qi) ? -INFINITY : v;
+                    s[kb][r] = v;
+                    mt = fmaxf(mt, v);
+                }
+            mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+            const float m_new = fmaxf(m_run, mt);
+            const float alpha = expf(m_run - m_new);
+            float ps = 0.f;
+#pragma unroll
+            for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    float p = expf(s[kb][r] - m_new);
+                    s[kb][r] = p;
+                    ps += p;
+                }
+            ps += __shfl_xor(ps, 32, 64);
+            l_run = l_run * alpha + ps;
+            m_run = m_new;
+#pragma unroll
+            for (int d = 0; d < NDB; d++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) o[d][r] *= alpha;
+            // O^T[d][q] += sum_key V[key][d] * P[q][key]
+#pragma unroll
+            for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int key = kb * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+#pragma unroll
+                    for (int d = 0; d < NDB; d++) {
+                        const int dd = d * 32 + lr;
+                        float va = (HS >= 32 || dd < HS) ? vs[key * ROW + dd] : 0.f;
+                        o[d] = __builtin_amdgcn_mfma_f32_32x32x2f32(va, s[kb][r], o[d], 0, 0, 0);
+                    }
+                }
+        }
+        if (kt + 1 < ntiles) lstore(cur ^ 1);
+        __syncthreads();
+    }
+
+    if (qi < T) {
+        const float inv = 1.0f / l_run;
+        float* op = out + ((long)b * T + qi) * C + h * HS;
+#pragma unroll
+        for (int d = 0; d < NDB; d++)
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const int dd = d * 32 + 8 * g + 4 * lh;  // rows 4g..4g+3 of the block
+                if (dd < HS) {
+                    f32x4 v = {o[d][4 * g] * inv, o[d][4 * g + 1] * inv, o[d][4 * g + 2] * inv,
+                               o[d][4 * g + 3] * inv};
+                    *(f32x4*)(op + dd) = v;
+                }
+            }
+    }
+}
+
+// One workgroup per (sequence, head); query at position t against keys 0..t.
+template <int HS>
+__global__ void __launch_bounds__(256)
+    k_attn_row(const float* __restrict__ qkv, long seq_stride, float* __restrict__ out, int q_pos,
+               const int* __restrict__ pos_dev, int C, int H, float scale) {
+    extern __shared__ float sm[];  // [HS] query, [4] reductions, [t+1] scores
+    float* qs = sm;
+    float* red = sm + HS;
+    float* sc = sm + HS + 8;
+    __shared__ float part[256];
+
+    const int bh = blockIdx.x, b = bh / H, h = bh % H;
+    const int t = pos_dev ? *pos_dev : q_pos;
+    const int nk = t + 1;
+    const long C3 = 3L * C;
+    const float* base = qkv + (long)b * seq_stride * C3 + h * HS;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+    for (int d = tid; d < HS; d += 256) qs[d] = base[(long)t * C3 + d];
+    __syncthreads();
+
+    float mx = -INFINITY;
+    for (int j = tid; j < nk; j += 256) {
+        const float* kp = base + (long)j * C3 + C;
+        float acc = 0.f;
+#pragma unroll
+        for (int d = 0; d < HS; d += 4) {
+            f32x4 kv = *(const f32x4*)(kp + d);
+            acc += (kv.x * qs[d] + kv.y * qs[d + 1]) + (kv.z * qs[d + 2] + kv.w * qs[d + 3]);
+        }
+        acc *= scale;
+        sc[j] = acc;
+        mx = fmaxf(mx, acc);
+    }
+    mx = wave_max(mx);
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float sum = 0.f;
+    for (int j = tid; j < nk; j += 256) {
+        float p = expf(sc[j] - mx);
+        sc[j] = p;
+        sum += p;
+    }
+    sum = wave_sum(sum);
+    __syncthreads();  // everyone has read red[] (max) before it is reused
+    if (lane == 0) red[4 + wave] = sum;
+    __syncthreads();
+    sum = (red[4] + red[5]) + (red[6] + red[7]);
+
+    // out[d] = sum_j p_j V[j][d]: thread = (d, slice of keys).
+    constexpr int NS = 256 / HS;
+    const int d = tid % HS, sl = tid / HS;
+    float acc = 0.f;
+    if (sl < NS)
+        for (int j = sl; j < nk; j += NS) acc += sc[j] * base[(long)j * C3 + 2 * C + d];
+    part[tid] = acc;
+    __syncthreads();
+    if (tid < HS) {
+        float s = 0.f;
+        for (int k = 0; k < NS; k++) s += part[k * HS + tid];
+        out[(long)b * C + h * HS + tid] = s * (1.0f / sum);
+    }
+}
+
+template <int HS>
+hipError_t causal_hs(const float* qkv, long seq_stride, float* out, int B, int T, int C, int H,
+                     hipStream_t s) {
+    const int nqb = (T + 127) / 128;
+    const float scale = 1.0f / sqrtf((float)HS);
+    k_attn_causal<HS><<<nqb * B * H, 256, 0, s>>>(qkv, seq_stride, out, B, T, C, H, nqb, scale);
+    return hipGetLastError();
+}
+
+template <int HS>
+hipError_t row_hs(const float* qkv, long seq_stride, float* out, int B, int q_pos,
+                  const int* pos_dev, int max_keys, int C, int H, hipStream_t s) {
+    const float scale = 1.0f / sqrtf((float)HS);
+    size_t lds = (size_t)(HS + 8 + max_keys) * sizeof(float);
+    k_attn_row<HS><<<B * H, 256, lds, s>>>(qkv, seq_stride, out, q_pos, pos_dev, C, H, scale);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_attention_causal(const float* qkv, long seq_stride, float* out, int B, int T,
+                                   int C, int H, hipStream_t s) {
+    if (B <= 0 || T <= 0) return hipSuccess;
+    switch (C / H) {
+        case 8: return causal_hs<8>(qkv, seq_stride, out, B, T, C, H, s);
+        case 16: return causal_hs<16>(qkv, seq_stride, out, B, T, C, H, s);
+        case 32: return causal_hs<32>(qkv, seq_stride, out, B, T, C, H, s);
+        case 64: return causal_hs<64>(qkv, seq_stride, out, B, T, C, H, s);
+        case 128: return causal_hs<128>(qkv, seq_stride, out, B, T, C, H, s);
+    }
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_attention_row(const float* qkv, long seq_stride, float* out, int B, int q_pos,
+                                const int* pos_dev, int max_keys, int C, int H, hipStream_t s) {
+    if (B <= 0) return hipSuccess;
+    if (max_keys <= 0 || (size_t)(max_keys + 136) * sizeof(float) > 64 * 1024)
+        return hipErrorInvalidValue;
+    switch (C / H) {
+        case 8: return row_hs<8>(qkv, seq_stride, out, B, q_pos, pos_dev, max_keys, C, H, s);
+        case 16: return row_hs<16>(qkv, seq_stride, out, B, q_pos, pos_dev, max_keys, C, H, s);
+        case 32: return row_hs<32>(qkv, seq_stride, out, B, q_pos, pos_dev, max_keys, C, H, s);
+        case 64: return row_hs<64>(qkv, seq_stride, out, B, q_pos, pos_dev, max_keys, C, H, s);
+        case 128: return row_hs<128>(qkv, seq_stride, out, B, q_pos, pos_dev, max_keys, C, H, s);
+    }
+    return hipErrorInvalidValue;
+}

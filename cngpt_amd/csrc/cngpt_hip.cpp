@@ -1,0 +1,650 @@
+// cngpt_hip.cpp - the C ABI (include/cngpt_hip.h): device memory, the kernel
+// sequence of the forward pass, incremental decode and timing counters.
+//
+// Kernel sequence of one forward (reference fast.c:227-333):
+//   embed -> per layer { LN1 -> QKV product (+b) -> causal attention
+//   -> c_proj product (x += . + b) -> LN2 -> fc product (+b, GELU)
+//   -> proj product (x += . + b) } -> LN_f -> lm_head product (wte^T).
+// In LAST mode the last layer runs attention for the final query row only
+// and the rest of that layer on the B gathered rows (fast.c:287-311).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <vector>
+
+#include "../../include/cngpt_hip.h"
+#include "common.h"
+#include "kernels.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return -1;
+}
+
+#define HIP_TRY(expr)                                                                   \
+    do {                                                                                \
+        hipError_t e_ = (expr);                                                         \
+        if (e_ != hipSuccess)                                                           \
+            return fail("%s failed: %s (%s:%d)", #expr, hipGetErrorString(e_), __FILE__, \
+                        __LINE__);                                                      \
+    } while (0)
+
+struct LayerW {
+    const float *ln1_w, *ln1_b, *attn_w, *attn_b, *proj_w, *proj_b;
+    const float *ln2_w, *ln2_b, *fc_w, *fc_b, *mlp_w, *mlp_b;
+};
+
+struct ProfRec {
+    int cls;
+    hipEvent_t a, b;
+    double flops, bytes;
+};
+
+constexpr size_t ALIGN = 256;
+size_t align_up(size_t n) { return (n + ALIGN - 1) & ~(ALIGN - 1); }
+
+}  // namespace
+
+struct cngpt_hip_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+
+    cngpt_hip_config cfg{};
+    bool have_params = false;
+    float* d_params = nullptr;
+    long n_params = 0;
+    const float *wte = nullptr, *wpe = nullptr, *lnf_w = nullptr, *lnf_b = nullptr;
+    std::vector<LayerW> layers;
+
+    // activation arena: one allocation, carved below
+    char* d_act = nullptr;
+    size_t act_bytes = 0;
+    int capB = 0, capT = 0, capAll = 0, capKV = 0;
+    int* tok = nullptr;
+    int* dev_err = nullptr;
+    int* pos = nullptr;      // decode position (device)
+    int* next_tok = nullptr; // [B] decode tokens (device)
+    float *x = nullptr, *ln = nullptr, *qkv = nullptr, *aout = nullptr, *hid = nullptr;
+    float *logits = nullptr;
+    float *xc = nullptr, *lnc = nullptr, *aoutc = nullptr, *hidc = nullptr;
+
+    // state of the last forward / decode
+    int curB = 0, curT = 0, curMode = CNGPT_LAST;
+    size_t logits_count = 0;
+    int kvB = 0, kvLen = 0;  // sequences and positions held in the KV cache
+
+    // timing
+    bool prof = false;
+    std::vector<ProfRec> recs;
+    std::vector<hipEvent_t> pool;
+    size_t pool_used = 0;
+};
+
+namespace {
+
+bool valid_cfg(const cngpt_hip_config* c) {
+    return c && c->n_layer > 0 && c->n_head > 0 && c->n_embd > 0 && c->vocab_size > 0 &&
+           c->block_size > 0 && c->n_embd % c->n_head == 0;
+}
+
+// ---------------------------------------------------------------- timing
+
+hipEvent_t pool_event(cngpt_hip_ctx* h) {
+    if (h->pool_used == h->pool.size()) {
+        hipEvent_t e;
+        if (hipEventCreate(&e) != hipSuccess) return nullptr;
+        h->pool.push_back(e);
+    }
+    return h->pool[h->pool_used++];
+}
+
+struct Timed {
+    cngpt_hip_ctx* h;
+    ProfRec rec{};
+    bool on;
+    Timed(cngpt_hip_ctx* h_, int cls, double flops, double bytes) : h(h_), on(h_->prof) {
+        if (!on) return;
+        rec.cls = cls;
+        rec.flops = flops;
+        rec.bytes = bytes;
+        rec.a = pool_event(h);
+        rec.b = pool_event(h);
+        if (!rec.a || !rec.b) { on = false; return; }
+        (void)hipEventRecord(rec.a, h->stream);
+    }
+    ~Timed() {
+        if (!on) return;
+        (void)hipEventRecord(rec.b, h->stream);
+        h->recs.push_back(rec);
+    }
+};
+
+// ---------------------------------------------------------------- launches
+
+int run_gemm(cngpt_hip_ctx* h, const float* X, const float* W, const float* bias, float* Y, int M,
+             int N, int K, int epi, int seg = 0, long seg_stride = 0, long ldy = -1,
+             int row_off = 0, const int* row_off_dev = nullptr) {
+    GemmArgs a{};
+    a.X = X; a.W = W; a.bias = bias; a.Y = Y;
+    a.M = M; a.N = N; a.K = K;
+    a.ldy = ldy < 0 ? N : ldy;
+    a.seg = seg; a.seg_stride = seg_stride;
+    a.row_off = row_off; a.row_off_dev = row_off_dev;
+    a.epi = epi;
+    const bool skinny = M <= 8;
+    double flops = 2.0 * M * N * K;
+    double bytes = 4.0 * ((double)M * K + (double)N * K + (double)M * N * (epi == EPI_RESID ? 2 : 1));
+    Timed t(h, skinny ? CNGPT_K_GEMV : CNGPT_K_GEMM, flops, bytes);
+    HIP_TRY(skinny ? launch_gemv(a, h->stream) : launch_gemm(a, h->stream));
+    return 0;
+}
+
+int run_ln(cngpt_hip_ctx* h, const float* x, long in_stride, const float* w, const float* b,
+           float* out, int rows) {
+    const int C = h->cfg.n_embd;
+    Timed t(h, CNGPT_K_LAYERNORM, 0.0, 8.0 * C * rows);
+    HIP_TRY(launch_layernorm(x, in_stride, w, b, out, C, rows, C, h->stream));
+    return 0;
+}
+
+// ---------------------------------------------------------------- arena
+
+// The arena grows in every dimension and never shrinks (one allocation,
+// re-carved on growth; growth drops the decode KV cache). The KV cache of
+// layer l, sequence b, position t is row (l*B + b)*capKV + t of the qkv
+// region, so any B <= capB and capacity <= capKV fit without moving.
+int ensure_arena(cngpt_hip_ctx* h, int B, int T, int all, int kv) {
+    if (h->d_act && B <= h->capB && T <= h->capT && (!all || h->capAll) && kv <= h->capKV)
+        return 0;
+    const cngpt_hip_config& c = h->cfg;
+    const int nB = std::max(B, h->capB);
+    const int nT = std::max(T, h->capT);
+    const int nAll = (all || h->capAll) ? 1 : 0;
+    const int nKV = std::max(kv, h->capKV);
+    const size_t C = c.n_embd, V = c.vocab_size, L = c.n_layer;
+    const size_t rows = (size_t)nB * nT;
+    const size_t qkv_rows = std::max(rows, L * nB * (size_t)nKV);
+    size_t sz[16], total = 0;
+    int n = 0;
+    sz[n++] = rows * sizeof(int);             // tok
+    sz[n++] = 4 * sizeof(int);                // dev_err, pos
+    sz[n++] = (size_t)nB * sizeof(int);       // next_tok
+    sz[n++] = rows * C * 4;                   // x
+    sz[n++] = rows * C * 4;                   // ln
+    sz[n++] = qkv_rows * 3 * C * 4;           // qkv / KV cache
+    sz[n++] = rows * C * 4;                   // aout
+    sz[n++] = rows * 4 * C * 4;               // hid
+    sz[n++] = (nAll ? rows : (size_t)nB) * V * 4;  // logits
+    sz[n++] = nB * C * 4;                     // xc
+    sz[n++] = nB * C * 4;                     // lnc
+    sz[n++] = nB * C * 4;                     // aoutc
+    sz[n++] = nB * 4 * C * 4;                 // hidc
+    for (int i = 0; i < n; i++) total += align_up(sz[i]);
+
+    if (h->d_act) {
+        HIP_TRY(hipStreamSynchronize(h->stream));
+        HIP_TRY(hipFree(h->d_act));
+        h->d_act = nullptr;
+        h->act_bytes = 0;
+        h->capB = h->capT = h->capAll = h->capKV = 0;
+        h->kvB = h->kvLen = 0;
+    }
+    char* p = nullptr;
+    if (hipMalloc(&p, total) != hipSuccess) {
+        (void)hipGetLastError();
+        return fail("activation allocation of %zu bytes failed (B=%d T=%d all=%d kv=%d)", total,
+                    nB, nT, nAll, nKV);
+    }
+    h->d_act = p;
+    h->act_bytes = total;
+    char* q = p;
+    auto take = [&](size_t bytes) { char* r = q; q += align_up(bytes); return r; };
+    n = 0;
+    h->tok = (int*)take(sz[n++]);
+    h->dev_err = (int*)take(sz[n++]);
+    h->pos = h->dev_err + 1;
+    h->next_tok = (int*)take(sz[n++]);
+    h->x = (float*)take(sz[n++]);
+    h->ln = (float*)take(sz[n++]);
+    h->qkv = (float*)take(sz[n++]);
+    h->aout = (float*)take(sz[n++]);
+    h->hid = (float*)take(sz[n++]);
+    h->logits = (float*)take(sz[n++]);
+    h->xc = (float*)take(sz[n++]);
+    h->lnc = (float*)take(sz[n++]);
+    h->aoutc = (float*)take(sz[n++]);
+    h->hidc = (float*)take(sz[n++]);
+    h->capB = nB; h->capT = nT; h->capAll = nAll; h->capKV = nKV;
+    HIP_TRY(hipMemsetAsync(h->dev_err, 0, 4 * sizeof(int), h->stream));
+    return 0;
+}
+
+int check_tokens(const cngpt_hip_ctx* h, const int* tokens, long n) {
+    for (long i = 0; i < n; i++)
+        if (tokens[i] < 0 || tokens[i] >= h->cfg.vocab_size)
+            return fail("token %d at index %ld outside [0, %d)", tokens[i], i, h->cfg.vocab_size);
+    return 0;
+}
+
+// Enqueue one forward over h->tok [B, T]. kv: QKV rows go to the per-layer
+// KV cache (capacity h->capKV per sequence) instead of the reused buffer.
+int enqueue_forward(cngpt_hip_ctx* h, int B, int T, int mode, bool kv) {
+    const cngpt_hip_config& c = h->cfg;
+    const int C = c.n_embd, V = c.vocab_size, L = c.n_layer, H = c.n_head;
+    const long rows = (long)B * T;
+    const long seq_stride = kv ? h->capKV : T;
+    {
+        Timed t(h, CNGPT_K_EMBED, 0.0, 12.0 * C * rows);
+        HIP_TRY(launch_embed(h->tok, h->wte, h->wpe, h->x, rows, T, C, V, 0, nullptr, h->dev_err,
+                             h->stream));
+    }
+    for (int l = 0; l < L; l++) {
+        const LayerW& w = h->layers[l];
+        const bool last = (mode == CNGPT_LAST) && (l == L - 1);
+        float* qkv = kv ? h->qkv + (size_t)l * B * h->capKV * 3 * C : h->qkv;
+        if (run_ln(h, h->x, C, w.ln1_w, w.ln1_b, h->ln, (int)rows)) return -1;
+        if (run_gemm(h, h->ln, w.attn_w, w.attn_b, qkv, (int)rows, 3 * C, C, EPI_BIAS,
+                     kv ? T : 0, seq_stride, 3L * C))
+            return -1;
+        if (!last) {
+            {
+                double fl = 2.0 * C * (double)T * (T + 1) * B;
+                double by = 4.0 * rows * C * 4;  // q,k,v read + out written
+                Timed t(h, CNGPT_K_ATTN, fl, by);
+                HIP_TRY(launch_attention_causal(qkv, seq_stride, h->aout, B, T, C, H, h->stream));
+            }
+            if (run_gemm(h, h->aout, w.proj_w, w.proj_b, h->x, (int)rows, C, C, EPI_RESID)) return -1;
+            if (run_ln(h, h->x, C, w.ln2_w, w.ln2_b, h->ln, (int)rows)) return -1;
+            if (run_gemm(h, h->ln, w.fc_w, w.fc_b, h->hid, (int)rows, 4 * C, C, EPI_BIAS_GELU))
+                return -1;
+            if (run_gemm(h, h->hid, w.mlp_w, w.mlp_b, h->x, (int)rows, C, 4 * C, EPI_RESID))
+                return -1;
+        } else {
+            {
+                double fl = 4.0 * C * (double)T * B;
+                double by = 4.0 * ((double)B * T * 2 * C + 2.0 * B * C);
+                Timed t(h, CNGPT_K_ATTN_ROW, fl, by);
+                HIP_TRY(launch_attention_row(qkv, seq_stride, h->aoutc, B, T - 1, nullptr, T, C, H,
+                                             h->stream));
+            }
+            {
+                Timed t(h, CNGPT_K_GATHER, 0.0, 8.0 * B * C);
+                HIP_TRY(launch_gather_rows(h->x + (size_t)(T - 1) * C, (long)T * C, h->xc, B, C,
+                                           h->stream));
+            }
+            if (run_gemm(h, h->aoutc, w.proj_w, w.proj_b, h->xc, B, C, C, EPI_RESID)) return -1;
+            if (run_ln(h, h->xc, C, w.ln2_w, w.ln2_b, h->lnc, B)) return -1;
+            if (run_gemm(h, h->lnc, w.fc_w, w.fc_b, h->hidc, B, 4 * C, C, EPI_BIAS_GELU)) return -1;
+            if (run_gemm(h, h->hidc, w.mlp_w, w.mlp_b, h->xc, B, C, 4 * C, EPI_RESID)) return -1;
+        }
+    }
+    if (mode == CNGPT_ALL) {
+        if (run_ln(h, h->x, C, h->lnf_w, h->lnf_b, h->ln, (int)rows)) return -1;
+        if (run_gemm(h, h->ln, h->wte, nullptr, h->logits, (int)rows, V, C, EPI_STORE)) return -1;
+        h->logits_count = (size_t)rows * V;
+    } else {
+        if (run_ln(h, h->xc, C, h->lnf_w, h->lnf_b, h->lnc, B)) return -1;
+        if (run_gemm(h, h->lnc, h->wte, nullptr, h->logits, B, V, C, EPI_STORE)) return -1;
+        h->logits_count = (size_t)B * V;
+    }
+    h->curB = B; h->curT = T; h->curMode = mode;
+    return 0;
+}
+
+// One decode step over h->next_tok [B] at position h->kvLen.
+int enqueue_decode_step(cngpt_hip_ctx* h) {
+    const cngpt_hip_config& c = h->cfg;
+    const int C = c.n_embd, V = c.vocab_size, L = c.n_layer, H = c.n_head;
+    const int B = h->kvB, p = h->kvLen;
+    const long cap = h->capKV;
+    {
+        Timed t(h, CNGPT_K_EMBED, 0.0, 12.0 * C * B);
+        HIP_TRY(launch_embed(h->next_tok, h->wte, h->wpe, h->xc, B, 1, C, V, p, nullptr,
+                             h->dev_err, h->stream));
+    }
+    for (int l = 0; l < L; l++) {
+        const LayerW& w = h->layers[l];
+        float* kvl = h->qkv + (size_t)l * B * cap * 3 * C;
+        if (run_ln(h, h->xc, C, w.ln1_w, w.ln1_b, h->lnc, B)) return -1;
+        if (run_gemm(h, h->lnc, w.attn_w, w.attn_b, kvl, B, 3 * C, C, EPI_BIAS, 1, cap, 3L * C, p))
+            return -1;
+        {
+            double fl = 4.0 * C * (double)(p + 1) * B;
+            double by = 4.0 * ((double)B * (p + 1) * 2 * C + 2.0 * B * C);
+            Timed t(h, CNGPT_K_ATTN_ROW, fl, by);
+            HIP_TRY(launch_attention_row(kvl, cap, h->aoutc, B, p, nullptr, (int)cap, C, H,
+                                         h->stream));
+        }
+        if (run_gemm(h, h->aoutc, w.proj_w, w.proj_b, h->xc, B, C, C, EPI_RESID)) return -1;
+        if (run_ln(h, h->xc, C, w.ln2_w, w.ln2_b, h->lnc, B)) return -1;
+        if (run_gemm(h, h->lnc, w.fc_w, w.fc_b, h->hidc, B, 4 * C, C, EPI_BIAS_GELU)) return -1;
+        if (run_gemm(h, h->hidc, w.mlp_w, w.mlp_b, h->xc, B, C, 4 * C, EPI_RESID)) return -1;
+    }
+    if (run_ln(h, h->xc, C, h->lnf_w, h->lnf_b, h->lnc, B)) return -1;
+    if (run_gemm(h, h->lnc, h->wte, nullptr, h->logits, B, V, C, EPI_STORE)) return -1;
+    h->logits_count = (size_t)B * V;
+    h->curB = B; h->curT = 1; h->curMode = CNGPT_LAST;
+    h->kvLen = p + 1;
+    return 0;
+}
+
+int need_params(const cngpt_hip_ctx* h) {
+    if (!h) return fail("null handle");
+    if (!h->have_params) return fail("no parameters loaded (cngpt_hip_load_params)");
+    return 0;
+}
+
+int check_dev_err(cngpt_hip_ctx* h) {
+    int e = 0;
+    HIP_TRY(hipMemcpyAsync(&e, h->dev_err, sizeof(int), hipMemcpyDeviceToHost, h->stream));
+    HIP_TRY(hipStreamSynchronize(h->stream));
+    if (e) {
+        HIP_TRY(hipMemsetAsync(h->dev_err, 0, sizeof(int), h->stream));
+        return fail("device-resident token ids outside [0, %d) were clamped", h->cfg.vocab_size);
+    }
+    return 0;
+}
+
+}  // namespace
+
+// ==================================================================== C ABI
+
+extern "C" {
+
+const char* cngpt_hip_last_error(void) { return g_err; }
+
+long cngpt_hip_num_params(const cngpt_hip_config* c) {
+    if (!valid_cfg(c)) return -1;
+    long C = c->n_embd, V = c->vocab_size, T = c->block_size, L = c->n_layer;
+    long per_layer = 2 * C + 3 * C * C + 3 * C + C * C + C + 2 * C + 4 * C * C + 4 * C +
+                     4 * C * C + C;
+    return V * C + T * C + L * per_layer + 2 * C;
+}
+
+int cngpt_hip_create(int device, cngpt_hip_ctx** out) {
+    if (!out) return fail("null output pointer");
+    *out = nullptr;
+    int n = 0;
+    HIP_TRY(hipGetDeviceCount(&n));
+    if (device < 0 || device >= n) return fail("device %d not present (%d devices)", device, n);
+    HIP_TRY(hipSetDevice(device));
+    cngpt_hip_ctx* h = new cngpt_hip_ctx();
+    h->device = device;
+    if (hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking) != hipSuccess) {
+        delete h;
+        return fail("hipStreamCreate failed");
+    }
+    *out = h;
+    return 0;
+}
+
+void cngpt_hip_destroy(cngpt_hip_ctx* h) {
+    if (!h) return;
+    (void)hipSetDevice(h->device);
+    if (h->stream) (void)hipStreamSynchronize(h->stream);
+    for (hipEvent_t e : h->pool) (void)hipEventDestroy(e);
+    if (h->d_act) (void)hipFree(h->d_act);
+    if (h->d_params) (void)hipFree(h->d_params);
+    if (h->stream) (void)hipStreamDestroy(h->stream);
+    delete h;
+}
+
+int cngpt_hip_load_params(cngpt_hip_ctx* h, const cngpt_hip_config* cfg, const float* params,
+                          long n_params) {
+    if (!h) return fail("null handle");
+    if (!valid_cfg(cfg)) return fail("invalid model shape");
+    if (cfg->n_embd % 4) return fail("n_embd %d must be a multiple of 4", cfg->n_embd);
+    const int hs = cfg->n_embd / cfg->n_head;
+    if (hs != 8 && hs != 16 && hs != 32 && hs != 64 && hs != 128)
+        return fail("head size %d not supported (8, 16, 32, 64, 128)", hs);
+    if (cfg->n_embd > 2048) return fail("n_embd %d above 2048", cfg->n_embd);
+    const long want = cngpt_hip_num_params(cfg);
+    if (!params || n_params != want)
+        return fail("parameter count %ld does not match the shape (%ld)", n_params, want);
+    HIP_TRY(hipSetDevice(h->device));
+    const bool same_shape = h->have_params && memcmp(&h->cfg, cfg, sizeof(*cfg)) == 0;
+    if (!same_shape) {
+        if (h->d_params) {
+            HIP_TRY(hipStreamSynchronize(h->stream));
+            HIP_TRY(hipFree(h->d_params));
+            h->d_params = nullptr;
+        }
+        if (h->d_act) {
+            HIP_TRY(hipFree(h->d_act));
+            h->d_act = nullptr;
+            h->capB = h->capT = h->capAll = h->capKV = 0;
+            h->kvB = h->kvLen = 0;
+        }
+        h->have_params = false;
+        if (hipMalloc(&h->d_params, (size_t)want * sizeof(float)) != hipSuccess) {
+            (void)hipGetLastError();
+            h->d_params = nullptr;
+            return fail("parameter allocation of %ld floats failed", want);
+        }
+    }
+    HIP_TRY(hipMemcpyAsync(h->d_params, params, (size_t)want * sizeof(float),
+                           hipMemcpyHostToDevice, h->stream));
+    HIP_TRY(hipStreamSynchronize(h->stream));
+    h->cfg = *cfg;
+    h->n_params = want;
+    // Carve like assign_weights (src/model.c:54-83).
+    const long C = cfg->n_embd, V = cfg->vocab_size, T = cfg->block_size;
+    const float* p = h->d_params;
+    h->wte = p; p += V * C;
+    h->wpe = p; p += T * C;
+    h->layers.assign(cfg->n_layer, LayerW{});
+    for (int l = 0; l < cfg->n_layer; l++) {
+        LayerW& w = h->layers[l];
+        w.ln1_w = p; p += C;
+        w.ln1_b = p; p += C;
+        w.attn_w = p; p += 3 * C * C;
+        w.attn_b = p; p += 3 * C;
+        w.proj_w = p; p += C * C;
+        w.proj_b = p; p += C;
+        w.ln2_w = p; p += C;
+        w.ln2_b = p; p += C;
+        w.fc_w = p; p += 4 * C * C;
+        w.fc_b = p; p += 4 * C;
+        w.mlp_w = p; p += C * 4 * C;
+        w.mlp_b = p; p += C;
+    }
+    h->lnf_w = p; p += C;
+    h->lnf_b = p;
+    h->have_params = true;
+    return 0;
+}
+
+int cngpt_hip_reserve(cngpt_hip_ctx* h, int B, int T, int mode, int kv_capacity) {
+    if (need_params(h)) return -1;
+    if (B <= 0 || T <= 0) return fail("B=%d T=%d must be positive", B, T);
+    if (T > h->cfg.block_size) return fail("T=%d exceeds block_size %d", T, h->cfg.block_size);
+    if (kv_capacity < 0 || kv_capacity > h->cfg.block_size)
+        return fail("kv capacity %d outside [0, %d]", kv_capacity, h->cfg.block_size);
+    HIP_TRY(hipSetDevice(h->device));
+    return ensure_arena(h, B, T, mode == CNGPT_ALL, kv_capacity);
+}
+
+int cngpt_hip_upload_tokens(cngpt_hip_ctx* h, const int* tokens, int B, int T) {
+    if (need_params(h)) return -1;
+    if (!tokens) return fail("null tokens");
+    if (cngpt_hip_reserve(h, B, T, CNGPT_LAST, 0)) return -1;
+    if (check_tokens(h, tokens, (long)B * T)) return -1;
+    HIP_TRY(hipMemcpyAsync(h->tok, tokens, (size_t)B * T * sizeof(int), hipMemcpyHostToDevice,
+                           h->stream));
+    HIP_TRY(hipStreamSynchronize(h->stream));
+    return 0;
+}
+
+int cngpt_hip_forward_resident(cngpt_hip_ctx* h, int B, int T, int mode) {
+    if (need_params(h)) return -1;
+    if (mode != CNGPT_LAST && mode != CNGPT_ALL) return fail("bad mode %d", mode);
+    if (B > h->capB || T > h->capT || (mode == CNGPT_ALL && !h->capAll))
+        return fail("forward_resident: arena not reserved for B=%d T=%d mode=%d", B, T, mode);
+    HIP_TRY(hipSetDevice(h->device));
+    return enqueue_forward(h, B, T, mode, false);
+}
+
+int cngpt_hip_forward(cngpt_hip_ctx* h, const int* tokens, int B, int T, int mode,
+                      float* logits_out) {
+    if (need_params(h)) return -1;
+    if (mode != CNGPT_LAST && mode != CNGPT_ALL) return fail("bad mode %d", mode);
+    if (!tokens) return fail("null tokens");
+    if (B <= 0 || T <= 0) return fail("B=%d T=%d must be positive", B, T);
+    if (T > h->cfg.block_size) return fail("T=%d exceeds block_size %d", T, h->cfg.block_size);
+    if (check_tokens(h, tokens, (long)B * T)) return -1;
+    HIP_TRY(hipSetDevice(h->device));
+    if (ensure_arena(h, B, T, mode == CNGPT_ALL, 0)) return -1;
+    h->kvB = h->kvLen = 0;
+    HIP_TRY(hipMemcpyAsync(h->tok, tokens, (size_t)B * T * sizeof(int), hipMemcpyHostToDevice,
+                           h->stream));
+    if (enqueue_forward(h, B, T, mode, false)) return -1;
+    if (logits_out)
+        HIP_TRY(hipMemcpyAsync(logits_out, h->logits, h->logits_count * sizeof(float),
+                               hipMemcpyDeviceToHost, h->stream));
+    HIP_TRY(hipStreamSynchronize(h->stream));
+    return 0;
+}
+
+int cngpt_hip_synchronize(cngpt_hip_ctx* h) {
+    if (!h) return fail("null handle");
+    HIP_TRY(hipSetDevice(h->device));
+    HIP_TRY(hipStreamSynchronize(h->stream));
+    return check_dev_err(h);
+}
+
+int cngpt_hip_read_logits(cngpt_hip_ctx* h, size_t offset, size_t count, float* dst) {
+    if (!h || !dst) return fail("null argument");
+    if (!h->logits || offset + count > h->logits_count)
+        return fail("logits range [%zu, %zu) outside the %zu held", offset, offset + count,
+                    h->logits_count);
+    HIP_TRY(hipSetDevice(h->device));
+    HIP_TRY(hipMemcpyAsync(dst, h->logits + offset, count * sizeof(float), hipMemcpyDeviceToHost,
+                           h->stream));
+    HIP_TRY(hipStreamSynchronize(h->stream));
+    return 0;
+}
+
+const float* cngpt_hip_logits_device(cngpt_hip_ctx* h) { return h ? h->logits : nullptr; }
+
+int cngpt_hip_decode_begin(cngpt_hip_ctx* h, const int* prompt, int B, int T, int capacity,
+                           float* logits_out) {
+    if (need_params(h)) return -1;
+    if (!prompt) return fail("null prompt");
+    if (B <= 0 || T <= 0) return fail("B=%d T=%d must be positive", B, T);
+    if (capacity <= T || capacity > h->cfg.block_size)
+        return fail("capacity %d must be in (T=%d, block_size=%d]", capacity, T,
+                    h->cfg.block_size);
+    if (check_tokens(h, prompt, (long)B * T)) return -1;
+    HIP_TRY(hipSetDevice(h->device));
+    if (ensure_arena(h, B, T, 0, capacity)) return -1;
+    HIP_TRY(hipMemcpyAsync(h->tok, prompt, (size_t)B * T * sizeof(int), hipMemcpyHostToDevice,
+                           h->stream));
+    if (enqueue_forward(h, B, T, CNGPT_LAST, true)) return -1;
+    h->kvB = B;
+    h->kvLen = T;
+    if (logits_out)
+        HIP_TRY(hipMemcpyAsync(logits_out, h->logits, (size_t)B * h->cfg.vocab_size * sizeof(float),
+                               hipMemcpyDeviceToHost, h->stream));
+    HIP_TRY(hipStreamSynchronize(h->stream));
+    return 0;
+}
+
+int cngpt_hip_decode_step(cngpt_hip_ctx* h, const int* tokens, float* logits_out) {
+    if (need_params(h)) return -1;
+    if (h->kvB == 0) return fail("decode_step before decode_begin");
+    if (h->kvLen >= h->capKV)
+        return fail("KV cache full (%d positions)", h->capKV);
+    HIP_TRY(hipSetDevice(h->device));
+    const int B = h->kvB;
+    if (tokens) {
+        if (check_tokens(h, tokens, B)) return -1;
+        HIP_TRY(hipMemcpyAsync(h->next_tok, tokens, (size_t)B * sizeof(int),
+                               hipMemcpyHostToDevice, h->stream));
+    } else {
+        Timed t(h, CNGPT_K_ARGMAX, 0.0, 4.0 * B * h->cfg.vocab_size);
+        HIP_TRY(launch_argmax(h->logits, B, h->cfg.vocab_size, h->next_tok, h->stream));
+    }
+    if (enqueue_decode_step(h)) return -1;
+    if (logits_out) {
+        HIP_TRY(hipMemcpyAsync(logits_out, h->logits, (size_t)B * h->cfg.vocab_size * sizeof(float),
+                               hipMemcpyDeviceToHost, h->stream));
+        HIP_TRY(hipStreamSynchronize(h->stream));
+    }
+    return 0;
+}
+
+int cngpt_hip_argmax(cngpt_hip_ctx* h, int* out_tokens) {
+    if (need_params(h)) return -1;
+    if (!out_tokens) return fail("null output");
+    if (!h->logits || h->curB == 0) return fail("no logits yet");
+    if (h->curMode != CNGPT_LAST) return fail("argmax needs last-position logits");
+    HIP_TRY(hipSetDevice(h->device));
+    HIP_TRY(launch_argmax(h->logits, h->curB, h->cfg.vocab_size, h->next_tok, h->stream));
+    HIP_TRY(hipMemcpyAsync(out_tokens, h->next_tok, (size_t)h->curB * sizeof(int),
+                           hipMemcpyDeviceToHost, h->stream));
+    HIP_TRY(hipStreamSynchronize(h->stream));
+    return 0;
+}
+
+int cngpt_hip_decode_length(cngpt_hip_ctx* h) { return h ? h->kvLen : 0; }
+
+void* cngpt_hip_host_alloc(size_t bytes) {
+    void* p = nullptr;
+    if (hipHostMalloc(&p, bytes, hipHostMallocDefault) != hipSuccess) {
+        (void)hipGetLastError();
+        fail("pinned host allocation of %zu bytes failed", bytes);
+        return nullptr;
+    }
+    return p;
+}
+
+void cngpt_hip_host_free(void* p) {
+    if (p) (void)hipHostFree(p);
+}
+
+int cngpt_hip_profile_enable(cngpt_hip_ctx* h, int on) {
+    if (!h) return fail("null handle");
+    h->prof = on != 0;
+    return 0;
+}
+
+int cngpt_hip_profile_reset(cngpt_hip_ctx* h) {
+    if (!h) return fail("null handle");
+    HIP_TRY(hipStreamSynchronize(h->stream));
+    h->recs.clear();
+    h->pool_used = 0;
+    return 0;
+}
+
+int cngpt_hip_profile_read(cngpt_hip_ctx* h, int cls, double* ms, long* launches, double* flops,
+                           double* bytes) {
+    if (!h) return fail("null handle");
+    if (cls < 0 || cls >= CNGPT_K_COUNT) return fail("bad kernel class %d", cls);
+    HIP_TRY(hipStreamSynchronize(h->stream));
+    double t = 0, f = 0, b = 0;
+    long n = 0;
+    for (const ProfRec& r : h->recs) {
+        if (r.cls != cls) continue;
+        float e = 0;
+        HIP_TRY(hipEventElapsedTime(&e, r.a, r.b));
+        t += e; f += r.flops; b += r.bytes; n++;
+    }
+    if (ms) *ms = t;
+    if (launches) *launches = n;
+    if (flops) *flops = f;
+    if (bytes) *bytes = b;
+    return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,47 @@
+// common.h - shared device helpers for the gfx950 kernels of cngpt_amd.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+#define CNGPT_WAVE 64
+
+// Butterfly sum / max over the 64 lanes of a wavefront.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+// GELU, tanh form (the formula of the reference's ops.h:56-58), with the
+// device library's tanhf.
+__device__ __forceinline__ float gelu_tanh(float x) {
+    const float k0 = 0.7978845608028654f;  // sqrt(2/pi)
+    const float k1 = 0.044715f;
+    float x3 = x * x * x;
+    return 0.5f * x * (1.0f + tanhf(k0 * (x + k1 * x3)));
+}
+
+// Epilogues shared by the GEMM and GEMV kernels.
+enum EpiMode : int {
+    EPI_STORE = 0,      // Y = acc
+    EPI_BIAS = 1,       // Y = acc + b
+    EPI_BIAS_GELU = 2,  // Y = gelu(acc + b)
+    EPI_RESID = 3,      // Y = (Y + acc) + b   (residual folded in, beta = 1)
+};
+
+template <int EPI>
+__device__ __forceinline__ float apply_epi(float acc, const float* __restrict__ bias, int col,
+                                           const float* yold) {
+    if (EPI == EPI_STORE) return acc;
+    if (EPI == EPI_BIAS) return acc + bias[col];
+    if (EPI == EPI_BIAS_GELU) return gelu_tanh(acc + bias[col]);
+    return (*yold + acc) + bias[col];
+}

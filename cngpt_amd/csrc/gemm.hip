@@ -1,0 +1,238 @@
+// gemm.hip - fp32 products Y[M,N] = epi(X[M,K] . W[N,K]^T) on gfx950.
+//
+// The reference computes every linear layer as cblas_sgemm(RowMajor,
+// NoTrans, Trans) with a per-row saxpy bias and beta = 1 for the residual
+// (fast.c:175-205). Both operands are K-contiguous, so both tiles are staged
+// in LDS the same way and read back with 16-byte LDS reads.
+//
+// k_gemm: 128x128 output tile per 256-thread workgroup, K in steps of 32,
+// double-buffered LDS (global loads for step k+1 are in flight while step k
+// is multiplied). Each wavefront owns a 64x64 sub-tile = 2x2 blocks of
+// v_mfma_f32_32x32x2f32. Inside a K step, lanes 0-31 feed k = 0..15 and
+// lanes 32-63 feed k = 16..31 of the step, so each lane reads 4 contiguous
+// floats per row per LDS read. The epilogue adds bias / GELU / residual and
+// stores straight from the accumulators (one 128-byte row segment per half
+// wavefront). Ragged M and N edges (e.g. the 50257-wide vocabulary) clamp
+// loads to the last valid row and mask stores.
+//
+// k_gemv: rows M <= 8 (decode and the last-position pass). One wavefront
+// per output column: the weight row streams once with 16-byte loads and is
+// dotted with every input row, then a butterfly reduction.
+#include "common.h"
+#include "kernels.h"
+
+namespace {
+
+constexpr int BM = 128, BN = 128, BK = 32;
+constexpr int LDS_ROW = BK + 4;  // padded row, keeps 16-byte alignment
+constexpr int NTHREADS = 256;
+constexpr int A_ITERS = BM * BK / 4 / NTHREADS;  // float4 loads per thread per tile
+constexpr int B_ITERS = BN * BK / 4 / NTHREADS;
+
+// Workgroups are dispatched round-robin over the 8 XCDs (pid % 8). Renumber
+// them so that each XCD receives a contiguous run of tile ids, then order
+// tiles in groups of 8 M-tiles so neighbours share A rows and W rows in the
+// XCD's L2.
+__device__ __forceinline__ void tile_coords(int pid, int tiles_m, int tiles_n, int& tm, int& tn) {
+    const int nt = tiles_m * tiles_n;
+    const int per = nt / 8, rem = nt % 8;
+    const int xcd = pid % 8, idx = pid / 8;
+    int p = (xcd < rem) ? xcd * (per + 1) + idx : rem * (per + 1) + (xcd - rem) * per + idx;
+    const int GM = 8;
+    const int group = p / (GM * tiles_n);
+    const int first_m = group * GM;
+    const int gsize = min(tiles_m - first_m, GM);
+    const int in_group = p % (GM * tiles_n);
+    tm = first_m + in_group % gsize;
+    tn = in_group / gsize;
+}
+
+template <int EPI>
+__global__ void __launch_bounds__(NTHREADS, 2) k_gemm(GemmArgs a, int tiles_m, int tiles_n) {
+    __shared__ float As[2][BM * LDS_ROW];
+    __shared__ float Bs[2][BN * LDS_ROW];
+
+    int tm, tn;
+    tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int tid = threadIdx.x;
+    const int K = a.K;
+
+    // Global -> register staging: thread covers rows tid/8 + 32*i, float4 kq.
+    const int kq = (tid & 7) * 4;
+    const float* xp[A_ITERS];
+    const float* wp[B_ITERS];
+#pragma unroll
+    for (int i = 0; i < A_ITERS; i++) {
+        int r = m0 + (tid >> 3) + 32 * i;
+        xp[i] = a.X + (long)min(r, a.M - 1) * K + kq;
+    }
+#pragma unroll
+    for (int i = 0; i < B_ITERS; i++) {
+        int r = n0 + (tid >> 3) + 32 * i;
+        wp[i] = a.W + (long)min(r, a.N - 1) * K + kq;
+    }
+    f32x4 ra[A_ITERS], rb[B_ITERS];
+    auto gload = [&](int k0) {
+        const bool ok = (k0 + kq) < K;
+#pragma unroll
+        for (int i = 0; i < A_ITERS; i++)
+            ra[i] = ok ? *(const f32x4*)(xp[i] + k0) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < B_ITERS; i++)
+            rb[i] = ok ? *(const f32x4*)(wp[i] + k0) : f32x4{0.f, 0.f, 0.f, 0.f};
+    };
+    auto lstore = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < A_ITERS; i++)
+            *(f32x4*)&As[buf][((tid >> 3) + 32 * i) * LDS_ROW + kq] = ra[i];
+#pragma unroll
+        for (int i = 0; i < B_ITERS; i++)
+            *(f32x4*)&Bs[buf][((tid >> 3) + 32 * i) * LDS_ROW + kq] = rb[i];
+    };
+
+    const int wave = tid >> 6, lane = tid & 63;
+    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+    const int lr = lane & 31, lh = lane >> 5;
+
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
+
+    const int nk = (K + BK - 1) / BK;
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; kt++) {
+        const int cur = kt & 1;
+        if (kt + 1 < nk) gload((kt + 1) * BK);
+        const float* as = &As[cur][0];
+        const float* bs = &Bs[cur][0];
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            const int kk = lh * 16 + g * 4;
+            f32x4 av[2], bv[2];
+#pragma unroll
+            for (int i = 0; i < 2; i++) av[i] = *(const f32x4*)&as[(wm + i * 32 + lr) * LDS_ROW + kk];
+#pragma unroll
+            for (int j = 0; j < 2; j++) bv[j] = *(const f32x4*)&bs[(wn + j * 32 + lr) * LDS_ROW + kk];
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+#pragma unroll
+                for (int i = 0; i < 2; i++)
+#pragma unroll
+                    for (int j = 0; j < 2; j++)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][e], bv[j][e],
+                                                                          acc[i][j], 0, 0, 0);
+        }
+        if (kt + 1 < nk) lstore(cur ^ 1);
+        __syncthreads();
+    }
+
+    // Epilogue. acc[i][j][r] holds row wm + 32i + 8(r/4) + 4*lh + r%4,
+    // column wn + 32j + lr of the tile.
+    const long roff = a.row_off + (a.row_off_dev ? *a.row_off_dev : 0);
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int col = n0 + wn + j * 32 + lr;
+        if (col >= a.N) continue;
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                if (row >= a.M) continue;
+                long orow = a.seg ? (long)(row / a.seg) * a.seg_stride + row % a.seg : row;
+                orow += roff;
+                float* y = a.Y + orow * a.ldy + col;
+                *y = apply_epi<EPI>(acc[i][j][r], a.bias, col, y);
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------- GEMV
+
+template <int EPI, int MR>
+__global__ void __launch_bounds__(256) k_gemv(GemmArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (n >= a.N) return;
+    const int K = a.K;
+    const float* w = a.W + (long)n * K;
+    float acc[MR];
+#pragma unroll
+    for (int r = 0; r < MR; r++) acc[r] = 0.f;
+    for (int k = lane * 4; k < K; k += 256) {
+        f32x4 wv = *(const f32x4*)(w + k);
+#pragma unroll
+        for (int r = 0; r < MR; r++) {
+            if (r < a.M) {
+                f32x4 xv = *(const f32x4*)(a.X + (long)r * K + k);
+                acc[r] += (wv.x * xv.x + wv.y * xv.y) + (wv.z * xv.z + wv.w * xv.w);
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < MR; r++) {
+        if (r >= a.M) break;
+        float s = wave_sum(acc[r]);
+        if (lane == 0) {
+            long orow = a.seg ? (long)(r / a.seg) * a.seg_stride + r % a.seg : r;
+            orow += a.row_off + (a.row_off_dev ? *a.row_off_dev : 0);
+            float* y = a.Y + orow * a.ldy + n;
+            *y = apply_epi<EPI>(s, a.bias, n, y);
+        }
+    }
+}
+
+template <int EPI>
+hipError_t gemm_epi(const GemmArgs& a, hipStream_t s) {
+    const int tiles_m = (a.M + BM - 1) / BM, tiles_n = (a.N + BN - 1) / BN;
+    k_gemm<EPI><<<tiles_m * tiles_n, NTHREADS, 0, s>>>(a, tiles_m, tiles_n);
+    return hipGetLastError();
+}
+
+template <int EPI>
+hipError_t gemv_epi(const GemmArgs& a, hipStream_t s) {
+    dim3 grid((a.N + 3) / 4), block(256);
+    if (a.M <= 1)
+        k_gemv<EPI, 1><<<grid, block, 0, s>>>(a);
+    else if (a.M <= 2)
+        k_gemv<EPI, 2><<<grid, block, 0, s>>>(a);
+    else if (a.M <= 4)
+        k_gemv<EPI, 4><<<grid, block, 0, s>>>(a);
+    else
+        k_gemv<EPI, 8><<<grid, block, 0, s>>>(a);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
+    if (a.M <= 0 || a.N <= 0) return hipSuccess;
+    if (a.K <= 0 || (a.K & 3)) return hipErrorInvalidValue;
+    switch (a.epi) {
+        case EPI_STORE: return gemm_epi<EPI_STORE>(a, s);
+        case EPI_BIAS: return gemm_epi<EPI_BIAS>(a, s);
+        case EPI_BIAS_GELU: return gemm_epi<EPI_BIAS_GELU>(a, s);
+        case EPI_RESID: return gemm_epi<EPI_RESID>(a, s);
+    }
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_gemv(const GemmArgs& a, hipStream_t s) {
+    if (a.M <= 0 || a.N <= 0) return hipSuccess;
+    if (a.M > 8 || a.K <= 0 || (a.K & 3)) return hipErrorInvalidValue;
+    switch (a.epi) {
+        case EPI_STORE: return gemv_epi<EPI_STORE>(a, s);
+        case EPI_BIAS: return gemv_epi<EPI_BIAS>(a, s);
+        case EPI_BIAS_GELU: return gemv_epi<EPI_BIAS_GELU>(a, s);
+        case EPI_RESID: return gemv_epi<EPI_RESID>(a, s);
+    }
+    return hipErrorInvalidValue;
+}

@@ -1,0 +1,168 @@
+// rowops.hip - bandwidth-bound row kernels: token+position embedding,
+// LayerNorm, row gather and greedy argmax.
+//
+// All are HBM-bound. Each row of C floats is owned by one wavefront and
+// moved with 16-byte loads; reductions stay inside the wavefront (butterfly
+// shuffles), so no LDS or block barrier is needed.
+#include "common.h"
+#include "kernels.h"
+
+// x[i, :] = wte[tok[i], :] + wpe[pos0 + i % T, :]   (reference fast.c:245-254)
+// One thread per float4. pos0 comes from *pos_dev when pos_dev is set, so a
+// captured decode step can advance the position on the device. Token ids
+// outside [0, V) are clamped and reported through *err.
+__global__ void __launch_bounds__(256) k_embed(const int* __restrict__ tok,
+                                               const float* __restrict__ wte,
+                                               const float* __restrict__ wpe, float* __restrict__ x,
+                                               long rows, int T, int C, int V, int pos0,
+                                               const int* __restrict__ pos_dev, int* __restrict__ err) {
+    const int c4 = C >> 2;
+    long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= rows * c4) return;
+    long r = i / c4;
+    int c = (int)(i - r * c4) * 4;
+    int t = (int)(r % T) + (pos_dev ? *pos_dev : pos0);
+    int id = tok[r];
+    if (id < 0 || id >= V) {
+        if (err) atomicOr(err, 1);
+        id = id < 0 ? 0 : V - 1;
+    }
+    f32x4 a = *(const f32x4*)(wte + (long)id * C + c);
+    f32x4 b = *(const f32x4*)(wpe + (long)t * C + c);
+    *(f32x4*)(x + r * C + c) = a + b;
+}
+
+// LayerNorm of one row per wavefront (reference ops.c:191-248): mean, biased
+// variance of (x - mean), rstd = 1/sqrtf(var + 1e-5), out = (x-m)*rstd*w + b.
+// NCH = float4 chunks per lane, so C <= 256 * NCH. Rows are read at stride
+// in_stride and written at stride out_stride (floats), which lets the final
+// LayerNorm of the last-position pass gather rows b*T + T-1.
+template <int NCH>
+__global__ void __launch_bounds__(256) k_layernorm(const float* __restrict__ x, long in_stride,
+                                                   const float* __restrict__ w,
+                                                   const float* __restrict__ b, float* __restrict__ out,
+                                                   long out_stride, int rows, int C) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const float* xr = x + (long)row * in_stride;
+    f32x4 v[NCH];
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < NCH; j++) {
+        int c = (lane + j * 64) * 4;
+        if (c < C) {
+            v[j] = *(const f32x4*)(xr + c);
+            s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
+        } else {
+            v[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+    }
+    const float m = wave_sum(s) / (float)C;
+    float q = 0.f;
+#pragma unroll
+    for (int j = 0; j < NCH; j++) {
+        int c = (lane + j * 64) * 4;
+        if (c < C) {
+            f32x4 d = v[j] - m;
+            q += (d.x * d.x + d.y * d.y) + (d.z * d.z + d.w * d.w);
+        }
+    }
+    const float rs = 1.0f / sqrtf(wave_sum(q) / (float)C + 1e-5f);
+    float* orow = out + (long)row * out_stride;
+#pragma unroll
+    for (int j = 0; j < NCH; j++) {
+        int c = (lane + j * 64) * 4;
+        if (c < C) {
+            f32x4 wv = *(const f32x4*)(w + c);
+            f32x4 bv = *(const f32x4*)(b + c);
+            f32x4 o = (v[j] - m) * rs * wv + bv;
+            *(f32x4*)(orow + c) = o;
+        }
+    }
+}
+
+// dst[r, :] = src[r * src_stride + src_off, :] for r < rows (C floats each).
+__global__ void __launch_bounds__(256) k_gather_rows(const float* __restrict__ src, long src_stride,
+                                                     float* __restrict__ dst, int rows, int C) {
+    const int c4 = C >> 2;
+    long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long)rows * c4) return;
+    int r = (int)(i / c4);
+    int c = (int)(i - (long)r * c4) * 4;
+    *(f32x4*)(dst + (long)r * C + c) = *(const f32x4*)(src + (long)r * src_stride + c);
+}
+
+// out[b] = argmax_v logits[b, v] (first index on ties). One block per row.
+__global__ void __launch_bounds__(256) k_argmax(const float* __restrict__ logits, int V,
+                                                int* __restrict__ out) {
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    const float* row = logits + (long)blockIdx.x * V;
+    float best = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int v = threadIdx.x; v < V; v += blockDim.x) {
+        float x = row[v];
+        if (x > best) { best = x; bi = v; }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        float ob = __shfl_xor(best, o, 64);
+        int oi = __shfl_xor(bi, o, 64);
+        if (ob > best || (ob == best && oi < bi)) { best = ob; bi = oi; }
+    }
+    const int wid = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) { sv[wid] = best; si[wid] = bi; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int k = 1; k < 4; k++)
+            if (sv[k] > best || (sv[k] == best && si[k] < bi)) { best = sv[k]; bi = si[k]; }
+        out[blockIdx.x] = bi;
+    }
+}
+
+// ---------------------------------------------------------------- launchers
+
+hipError_t launch_embed(const int* tok, const float* wte, const float* wpe, float* x, long rows,
+                        int T, int C, int V, int pos0, const int* pos_dev, int* err,
+                        hipStream_t s) {
+    long n = rows * (C / 4);
+    if (n == 0) return hipSuccess;
+    k_embed<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(tok, wte, wpe, x, rows, T, C, V, pos0,
+                                                         pos_dev, err);
+    return hipGetLastError();
+}
+
+hipError_t launch_layernorm(const float* x, long in_stride, const float* w, const float* b,
+                            float* out, long out_stride, int rows, int C, hipStream_t s) {
+    if (rows == 0) return hipSuccess;
+    dim3 grid((rows + 3) / 4), block(256);
+    int nch = (C + 255) / 256;
+    if (nch <= 1)
+        k_layernorm<1><<<grid, block, 0, s>>>(x, in_stride, w, b, out, out_stride, rows, C);
+    else if (nch <= 2)
+        k_layernorm<2><<<grid, block, 0, s>>>(x, in_stride, w, b, out, out_stride, rows, C);
+    else if (nch <= 3)
+        k_layernorm<3><<<grid, block, 0, s>>>(x, in_stride, w, b, out, out_stride, rows, C);
+    else if (nch <= 4)
+        k_layernorm<4><<<grid, block, 0, s>>>(x, in_stride, w, b, out, out_stride, rows, C);
+    else if (nch <= 8)
+        k_layernorm<8><<<grid, block, 0, s>>>(x, in_stride, w, b, out, out_stride, rows, C);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+hipError_t launch_gather_rows(const float* src, long src_stride, float* dst, int rows, int C,
+                              hipStream_t s) {
+    long n = (long)rows * (C / 4);
+    if (n == 0) return hipSuccess;
+    k_gather_rows<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(src, src_stride, dst, rows, C);
+    return hipGetLastError();
+}
+
+hipError_t launch_argmax(const float* logits, int rows, int V, int* out, hipStream_t s) {
+    if (rows == 0) return hipSuccess;
+    k_argmax<<<rows, 256, 0, s>>>(logits, V, out);
+    return hipGetLastError();
+}

@@ -1,0 +1,136 @@
+/*
+ * cngpt_hip.h - C ABI of the MI355X (gfx950) inference forward pass.
+ *
+ * Plain C: opaque handles, plain pointers and sizes, int status codes
+ * (0 = success, -1 = failure with a message from cngpt_hip_last_error()).
+ * One handle owns one HIP stream on one device, one device allocation for
+ * the parameters and one for activations (plus the decode KV cache). Calls on
+ * one handle must come from one host thread at a time, as with the
+ * reference's FastCtx (src/fast.c:114-115 keeps unsynchronised statics).
+ *
+ * The fast.h drop-in (fast_init / gpt_forward_fast, include/fast.h) is
+ * written on top of these entry points; they are exported for callers that
+ * want device-resident inputs, all-position logits or incremental decode.
+ */
+#ifndef CNGPT_HIP_H
+#define CNGPT_HIP_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct cngpt_hip_ctx cngpt_hip_ctx;
+
+/* Model shape: the fields of the weight-file header (src/model.h:22-30). */
+typedef struct {
+    int n_layer;
+    int n_head;
+    int n_embd;
+    int vocab_size;
+    int block_size;
+} cngpt_hip_config;
+
+/* Which positions get logits. LAST: the final position of each sequence,
+ * [B, V] (gpt_forward_fast, src/fast.c:227-333). ALL: every position,
+ * [B, T, V] (the logits gpt_forward keeps, src/model.c:612-614). */
+enum { CNGPT_LAST = 0, CNGPT_ALL = 1 };
+
+/* Kernel classes for the timing counters. */
+enum {
+    CNGPT_K_GEMM = 0,        /* MFMA products (linear layers, lm_head) */
+    CNGPT_K_GEMV = 1,        /* skinny products (<= 8 rows) */
+    CNGPT_K_ATTN = 2,        /* fused causal attention */
+    CNGPT_K_ATTN_ROW = 3,    /* one-query attention (last position, decode) */
+    CNGPT_K_LAYERNORM = 4,
+    CNGPT_K_EMBED = 5,
+    CNGPT_K_GATHER = 6,
+    CNGPT_K_ARGMAX = 7,
+    CNGPT_K_COUNT = 8
+};
+
+/* Last error message of the calling thread ("" if none). */
+const char *cngpt_hip_last_error(void);
+
+/* Handle on HIP device `device`. No reference counterpart: replaces the
+ * zeroed FastCtx of fast_init (src/fast.c:29-32). */
+int  cngpt_hip_create(int device, cngpt_hip_ctx **out);
+/* Frees the handle, its stream and both device allocations
+ * (fast_free, src/fast.c:34-40). NULL is a no-op. */
+void cngpt_hip_destroy(cngpt_hip_ctx *h);
+
+/* Number of floats in the flat parameter buffer for cfg
+ * (gpt_num_params, src/model.c:20-48), or -1 for an invalid shape. */
+long cngpt_hip_num_params(const cngpt_hip_config *cfg);
+
+/* Copy the flat fp32 parameter buffer (layout of assign_weights,
+ * src/model.c:54-83) into the handle's single parameter allocation.
+ * Replaces the live reads of m->params that gpt_forward_fast makes
+ * (src/fast.c:245-329); call again whenever the host buffer changes. */
+int  cngpt_hip_load_params(cngpt_hip_ctx *h, const cngpt_hip_config *cfg,
+                           const float *params, long n_params);
+
+/* Size the activation allocation for B sequences of T tokens (and a decode
+ * KV cache of kv_capacity positions per sequence; 0 = none). Replaces
+ * fast_resize (src/fast.c:140-168). forward/decode call it as needed. */
+int  cngpt_hip_reserve(cngpt_hip_ctx *h, int B, int T, int mode, int kv_capacity);
+
+/* Forward pass over host tokens [B, T] (validated: 0 <= id < vocab_size,
+ * T <= block_size). mode CNGPT_LAST copies [B, V] logits to logits_out
+ * when it is not NULL; CNGPT_ALL keeps [B, T, V] on the device and copies
+ * them only when logits_out is not NULL. Blocks until done.
+ * gpt_forward_fast (src/fast.c:227-333), plus the all-positions mode. */
+int  cngpt_hip_forward(cngpt_hip_ctx *h, const int *tokens, int B, int T, int mode,
+                       float *logits_out);
+
+/* Split form for callers that keep inputs in HBM: upload tokens [B, T]
+ * once, then enqueue forwards on the handle's stream without blocking. */
+int  cngpt_hip_upload_tokens(cngpt_hip_ctx *h, const int *tokens, int B, int T);
+int  cngpt_hip_forward_resident(cngpt_hip_ctx *h, int B, int T, int mode);
+int  cngpt_hip_synchronize(cngpt_hip_ctx *h);
+/* Copy count floats of the logits, starting at float offset, to host. */
+int  cngpt_hip_read_logits(cngpt_hip_ctx *h, size_t offset, size_t count, float *dst);
+/* Device address of the logits of the last forward / decode step. */
+const float *cngpt_hip_logits_device(cngpt_hip_ctx *h);
+
+/* Incremental decode with a device KV cache (no reference counterpart:
+ * gpt_sample, src/model.c:991-1016, recomputes the whole prefix).
+ * decode_begin runs the prompt [B, T] through the forward, keeps every
+ * layer's K and V for up to `capacity` positions per sequence
+ * (T < capacity <= block_size) and leaves the last-position logits [B, V]
+ * in logits_out (may be NULL). decode_step appends one token per sequence
+ * (tokens [B] from the host, or the device argmax of the previous logits
+ * when tokens is NULL) and produces the next [B, V] logits. */
+int  cngpt_hip_decode_begin(cngpt_hip_ctx *h, const int *prompt, int B, int T, int capacity,
+                            float *logits_out);
+int  cngpt_hip_decode_step(cngpt_hip_ctx *h, const int *tokens, float *logits_out);
+/* Greedy token per sequence from the current logits (first index on ties). */
+int  cngpt_hip_argmax(cngpt_hip_ctx *h, int *out_tokens);
+/* Positions held in the KV cache per sequence (prompt + steps). */
+int  cngpt_hip_decode_length(cngpt_hip_ctx *h);
+
+/* Per-kernel-class timing with HIP events on the handle's stream.
+ * While enabled, every launch is bracketed by an event pair; read returns
+ * the summed kernel milliseconds, the launch count and the algorithmic
+ * FLOPs and HBM bytes of those launches (synchronizes the stream). */
+int  cngpt_hip_profile_enable(cngpt_hip_ctx *h, int on);
+int  cngpt_hip_profile_reset(cngpt_hip_ctx *h);
+int  cngpt_hip_profile_read(cngpt_hip_ctx *h, int kernel_class, double *ms, long *launches,
+                            double *flops, double *bytes);
+
+/* Pinned host memory, used for staging logits (fast.h's FastCtx).
+ * NULL on failure. */
+void *cngpt_hip_host_alloc(size_t bytes);
+void  cngpt_hip_host_free(void *p);
+
+/* Host-side seeded init for synthetic weights: srand(seed) then the
+ * N(0, 0.02) / residual-scaled draw order of gpt_init_weights
+ * (src/model.c:275-331), into a host buffer of cngpt_hip_num_params floats.
+ * Needs no GPU. */
+int  cngpt_hip_init_weights(const cngpt_hip_config *cfg, float *params, unsigned seed);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* CNGPT_HIP_H */

@@ -1,0 +1,250 @@
+"""CPU oracle for cngpt's inference forward pass -- TEST INFRASTRUCTURE ONLY.
+
+The C library built from ``oracle/cngpt_oracle.c`` restates the reference's
+``gpt_forward_fast`` (src/fast.c:227-333), its all-rows variant (the
+semantics of ``gpt_forward``, src/model.c:442-625), the forward ops of
+src/ops.c, the seeded init (src/model.c:275-331) and ``sample_top_k``
+(src/model.c:927-989). This module is a ctypes front end to it.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
+``bench.py`` may import this package, and only as the checker or the timed
+CPU baseline; the product (``cngpt_amd``) never does.
+"""
+from __future__ import annotations
+
+import ctypes
+import glob
+import os
+from dataclasses import dataclass
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libcngpt_oracle.so")
+
+LAST, ALL = 0, 1
+
+
+class OrcCfg(ctypes.Structure):
+    _fields_ = [("n_layer", ctypes.c_int), ("n_head", ctypes.c_int),
+                ("n_embd", ctypes.c_int), ("vocab_size", ctypes.c_int),
+                ("block_size", ctypes.c_int)]
+
+
+@dataclass(frozen=True)
+class Cfg:
+    n_layer: int
+    n_head: int
+    n_embd: int
+    vocab_size: int
+    block_size: int
+
+    def c(self) -> OrcCfg:
+        return OrcCfg(self.n_layer, self.n_head, self.n_embd, self.vocab_size,
+                      self.block_size)
+
+
+# Model shapes: the tiny model of tests/check_fast.c:29-33 and GPT-2 sizes.
+TINY = Cfg(3, 4, 32, 70, 16)
+GPT2_SMALL = Cfg(12, 12, 768, 50257, 1024)
+GPT2_MEDIUM = Cfg(24, 16, 1024, 50257, 1024)
+GPT2_XL = Cfg(48, 25, 1600, 50257, 1024)
+
+_F = ctypes.POINTER(ctypes.c_float)
+_I = ctypes.POINTER(ctypes.c_int)
+_L = ctypes.POINTER(ctypes.c_long)
+_lib = None
+
+
+def _fp(a: np.ndarray):
+    assert a.dtype == np.float32 and a.flags.c_contiguous
+    return a.ctypes.data_as(_F)
+
+
+def _ip(a: np.ndarray):
+    assert a.dtype == np.int32 and a.flags.c_contiguous
+    return a.ctypes.data_as(_I)
+
+
+def find_openblas() -> str | None:
+    """Path of a CBLAS-compatible OpenBLAS on this host: the one bundled in
+    scipy's wheel, else a system libopenblas."""
+    try:
+        import scipy
+        d = os.path.join(os.path.dirname(os.path.dirname(scipy.__file__)), "scipy.libs")
+        hits = sorted(glob.glob(os.path.join(d, "libscipy_openblas*.so")))
+        if hits:
+            return hits[0]
+    except ImportError:
+        pass
+    for p in ("/usr/lib/x86_64-linux-gnu/libopenblas.so.0", "/usr/lib/libopenblas.so"):
+        if os.path.exists(p):
+            return p
+    return None
+
+
+def lib():
+    """Load the oracle library (built by oracle/Makefile) and bind a CBLAS."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"oracle library not built: {LIB_PATH} (run make -C oracle)")
+    L = ctypes.CDLL(LIB_PATH)
+    L.orc_num_params.argtypes = [ctypes.POINTER(OrcCfg)]
+    L.orc_num_params.restype = ctypes.c_long
+    L.orc_offsets.argtypes = [ctypes.POINTER(OrcCfg), _L]
+    L.orc_init_weights.argtypes = [ctypes.POINTER(OrcCfg), _F, ctypes.c_uint]
+    L.orc_use_blas.argtypes = [ctypes.c_char_p]
+    L.orc_use_blas.restype = ctypes.c_int
+    L.orc_blas_info.restype = ctypes.c_char_p
+    L.orc_set_threads.argtypes = [ctypes.c_int]
+    L.orc_set_threads.restype = ctypes.c_int
+    L.orc_physical_cores.restype = ctypes.c_int
+    L.orc_layernorm.argtypes = [_F, _F, _F, _F, _F, _F, ctypes.c_int, ctypes.c_int]
+    L.orc_gelu.argtypes = [_F, _F, ctypes.c_int]
+    L.orc_softmax_inplace.argtypes = [_F, ctypes.c_int, ctypes.c_int]
+    L.orc_causal_mask.argtypes = [_F, ctypes.c_int]
+    L.orc_linear.argtypes = [_F, _F, _F, _F, ctypes.c_int, ctypes.c_int, ctypes.c_int]
+    L.orc_forward.argtypes = [ctypes.POINTER(OrcCfg), _F, _I, ctypes.c_int,
+                              ctypes.c_int, ctypes.c_int, _F]
+    L.orc_forward.restype = ctypes.c_int
+    L.orc_sample_top_k.argtypes = [_F, ctypes.c_int, ctypes.c_float, ctypes.c_int,
+                                   ctypes.c_float]
+    L.orc_sample_top_k.restype = ctypes.c_int
+    L.orc_srand.argtypes = [ctypes.c_uint]
+    L.orc_rand_uniform.restype = ctypes.c_float
+    blas = os.environ.get("CNGPT_ORACLE_BLAS") or find_openblas()
+    if blas and blas != "builtin":
+        L.orc_use_blas(blas.encode())
+    _lib = L
+    return L
+
+
+def blas_info() -> str:
+    return lib().orc_blas_info().decode()
+
+
+def set_threads(n: int = 0) -> int:
+    return lib().orc_set_threads(n)
+
+
+def physical_cores() -> int:
+    return lib().orc_physical_cores()
+
+
+def num_params(cfg: Cfg) -> int:
+    return lib().orc_num_params(ctypes.byref(cfg.c()))
+
+
+def offsets(cfg: Cfg) -> np.ndarray:
+    off = np.zeros(4 + 12 * cfg.n_layer, dtype=np.int64)
+    lib().orc_offsets(ctypes.byref(cfg.c()), off.ctypes.data_as(_L))
+    return off
+
+
+def init_weights(cfg: Cfg, seed: int) -> np.ndarray:
+    p = np.zeros(num_params(cfg), dtype=np.float32)
+    lib().orc_init_weights(ctypes.byref(cfg.c()), _fp(p), seed)
+    return p
+
+
+def unpack(cfg: Cfg, params: np.ndarray) -> dict:
+    """Named views into the flat buffer (layout of src/model.c:54-83)."""
+    C, V, T = cfg.n_embd, cfg.vocab_size, cfg.block_size
+    off = offsets(cfg)
+    shapes = [(C,), (C,), (3 * C, C), (3 * C,), (C, C), (C,), (C,), (C,),
+              (4 * C, C), (4 * C,), (C, 4 * C), (C,)]
+    names = ["ln1_w", "ln1_b", "c_attn_w", "c_attn_b", "c_proj_w", "c_proj_b",
+             "ln2_w", "ln2_b", "mlp_fc_w", "mlp_fc_b", "mlp_proj_w", "mlp_proj_b"]
+
+    def view(o, shape):
+        n = int(np.prod(shape))
+        return params[o:o + n].reshape(shape)
+
+    d = {"wte": view(off[0], (V, C)), "wpe": view(off[1], (T, C)), "layers": []}
+    for l in range(cfg.n_layer):
+        o = off[2 + 12 * l: 2 + 12 * (l + 1)]
+        d["layers"].append({n: view(o[i], s) for i, (n, s) in enumerate(zip(names, shapes))})
+    of = off[2 + 12 * cfg.n_layer:]
+    d["ln_f_w"] = view(of[0], (C,))
+    d["ln_f_b"] = view(of[1], (C,))
+    return d
+
+
+def forward(cfg: Cfg, params: np.ndarray, tokens: np.ndarray, mode: int = LAST) -> np.ndarray:
+    """LAST: logits [B, V] (gpt_forward_fast); ALL: logits [B, T, V]."""
+    tokens = np.ascontiguousarray(tokens, dtype=np.int32)
+    B, T = tokens.shape
+    shape = (B, cfg.vocab_size) if mode == LAST else (B, T, cfg.vocab_size)
+    out = np.empty(shape, dtype=np.float32)
+    rc = lib().orc_forward(ctypes.byref(cfg.c()), _fp(params), _ip(tokens), B, T, mode, _fp(out))
+    if rc != 0:
+        raise ValueError(f"orc_forward failed (B={B}, T={T})")
+    return out
+
+
+def layernorm(x, w, b):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    T, C = x.shape
+    out = np.empty_like(x)
+    mean = np.empty(T, np.float32)
+    rstd = np.empty(T, np.float32)
+    lib().orc_layernorm(_fp(x), _fp(np.ascontiguousarray(w, np.float32)),
+                        _fp(np.ascontiguousarray(b, np.float32)), _fp(out), _fp(mean),
+                        _fp(rstd), T, C)
+    return out, mean, rstd
+
+
+def gelu(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(x)
+    lib().orc_gelu(_fp(x), _fp(out), x.size)
+    return out
+
+
+def softmax(x):
+    x = np.array(x, dtype=np.float32, order="C")
+    rows, cols = x.shape
+    lib().orc_softmax_inplace(_fp(x), rows, cols)
+    return x
+
+
+def causal_mask(s):
+    s = np.array(s, dtype=np.float32, order="C")
+    lib().orc_causal_mask(_fp(s), s.shape[0])
+    return s
+
+
+def linear(X, W, b=None):
+    X = np.ascontiguousarray(X, np.float32)
+    W = np.ascontiguousarray(W, np.float32)
+    M, K = X.shape
+    N = W.shape[0]
+    Y = np.empty((M, N), np.float32)
+    bp = _fp(np.ascontiguousarray(b, np.float32)) if b is not None else None
+    lib().orc_linear(_fp(X), _fp(W), bp, _fp(Y), M, K, N)
+    return Y
+
+
+def sample_top_k(logits, temp: float, top_k: int, r: float) -> int:
+    logits = np.ascontiguousarray(logits, np.float32)
+    return lib().orc_sample_top_k(_fp(logits), logits.size, temp, top_k, r)
+
+
+def srand(seed: int) -> None:
+    lib().orc_srand(seed)
+
+
+def rand_uniform() -> float:
+    return lib().orc_rand_uniform()
+
+
+def lcg_tokens(n: int, vocab: int, seed: int = 12345) -> np.ndarray:
+    """Token ids from the LCG of src/cngpt.c:338-342."""
+    out = np.empty(n, dtype=np.int32)
+    s = seed & 0xFFFFFFFF
+    for i in range(n):
+        s = (s * 1664525 + 1013904223) & 0xFFFFFFFF
+        out[i] = (s >> 8) % vocab
+    return out

@@ -1,0 +1,87 @@
+/*
+ * cngpt_oracle.h - CPU restatement of cngpt's inference forward pass.
+ *
+ * TEST INFRASTRUCTURE ONLY. This library is the checker the HIP path is
+ * compared against, and the CPU baseline that bench.py times beside it.
+ * Nothing in the product (cngpt_amd/, include/) links or loads it; only
+ * tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may.
+ *
+ * Every function cites the reference file:line it restates. All arithmetic
+ * is fp32 like the reference; the matrix products go through a CBLAS
+ * sgemm resolved at run time (OpenBLAS, as the reference links) or, when
+ * none is found, through a plain blocked C product.
+ */
+#ifndef CNGPT_ORACLE_H
+#define CNGPT_ORACLE_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Model shape; the fields of GPTHeader/GPTConfig (src/model.h:22-42). */
+typedef struct {
+    int n_layer;
+    int n_head;
+    int n_embd;
+    int vocab_size;
+    int block_size;
+} orc_cfg;
+
+enum { ORC_LAST = 0, ORC_ALL = 1 };
+
+/* Parameter count, src/model.c:20-48 (64-bit here; the reference's int
+ * overflows past 2^31 parameters, which no GPT-2 size reaches). */
+long orc_num_params(const orc_cfg *c);
+
+/* Offsets (in floats) of every tensor in the flat buffer, in the order of
+ * src/model.c:54-83. off must hold 2 + 12*n_layer + 2 entries:
+ * wte, wpe, then per layer ln1_w ln1_b c_attn_w c_attn_b c_proj_w c_proj_b
+ * ln2_w ln2_b mlp_fc_w mlp_fc_b mlp_proj_w mlp_proj_b, then ln_f_w ln_f_b. */
+void orc_offsets(const orc_cfg *c, long *off);
+
+/* srand(seed) then gpt_init_weights, src/model.c:275-331. */
+void orc_init_weights(const orc_cfg *c, float *params, unsigned seed);
+
+/* Bind a CBLAS at run time (path to a shared library exporting
+ * cblas_sgemm or scipy_cblas_sgemm). Returns 0 on success; on failure the
+ * built-in C product stays in use. */
+int  orc_use_blas(const char *path);
+/* Human-readable name of the sgemm in use (library config string). */
+const char *orc_blas_info(void);
+/* Threads for the forward (n <= 0: one per physical core, as
+ * src/fast.c:165-200 picks). Returns the count in use. */
+int  orc_set_threads(int n);
+/* Physical cores the process may run on (src/fast.c:124-156). */
+int  orc_physical_cores(void);
+
+/* Single ops, scalar paths of src/ops.c. */
+void orc_layernorm(const float *x, const float *w, const float *b, float *out,
+                   float *mean, float *rstd, int T, int C);       /* ops.c:191-248 */
+void orc_gelu(const float *x, float *out, int n);                  /* ops.c:337-380 */
+void orc_softmax_inplace(float *x, int rows, int cols);            /* ops.c:424-482 */
+void orc_causal_mask(float *scores, int T);                        /* ops.c:488-493 */
+void orc_linear(const float *X, const float *W, const float *b, float *Y,
+                int M, int K, int N);                              /* ops.c:109-123 */
+
+/* Inference forward. mode ORC_LAST: gpt_forward_fast (src/fast.c:227-333),
+ * logits [B, V] of the final position of each sequence. mode ORC_ALL: the
+ * same algorithm without the last-layer pruning, logits [B, T, V] for every
+ * position, the semantics of gpt_forward (src/model.c:442-625).
+ * Returns 0, or -1 on bad arguments / allocation failure. */
+int  orc_forward(const orc_cfg *c, const float *params, const int *tokens,
+                 int B, int T, int mode, float *logits);
+
+/* sample_top_k, src/model.c:927-989, with the uniform draw r in [0,1)
+ * passed in instead of taken from rand(). */
+int  orc_sample_top_k(const float *logits, int V, float temp, int top_k, float r);
+
+/* The draw sample_top_k makes (src/model.c:979): rand()/(RAND_MAX+1.0f). */
+void  orc_srand(unsigned seed);
+float orc_rand_uniform(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

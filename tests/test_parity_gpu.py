@@ -1,0 +1,175 @@
+"""HIP forward pass vs the CPU oracle on the same seeded weights and tokens.
+
+Bar (north star): logits max|diff| <= 1e-3 and max|diff| / max|ref| <= 1e-4,
+argmax identical. The tiny shapes of the reference's tests/check_fast.c use
+that test's own tighter bound, max|diff| < 1e-4 (check_fast.c:62).
+"""
+import sys
+
+import numpy as np
+import pytest
+
+import cngpt_amd
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+ABS_TOL = 1e-3
+REL_TOL = 1e-4
+
+
+def ocfg(cfg):
+    return oracle.Cfg(cfg.n_layer, cfg.n_head, cfg.n_embd, cfg.vocab_size, cfg.block_size)
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def compare(got, ref, abs_tol=ABS_TOL, rel_tol=REL_TOL, check_argmax=True, what=""):
+    assert got.shape == ref.shape, (got.shape, ref.shape)
+    assert np.isfinite(got).all(), f"{what}: non-finite logits"
+    err = float(np.abs(got - ref).max())
+    rel = err / float(np.abs(ref).max())
+    say(f"  {what}: max|diff|={err:.3e} rel={rel:.3e}")
+    assert err <= abs_tol and rel <= rel_tol, (what, err, rel)
+    if check_argmax:
+        ga, ra = got.argmax(-1), ref.argmax(-1)
+        if not np.array_equal(ga, ra):
+            # only a near-tie in the reference may flip the argmax
+            srt = np.sort(ref, axis=-1)
+            gap = (srt[..., -1] - srt[..., -2])[ga != ra]
+            assert np.all(gap < 2 * err), (what, "argmax differs", gap)
+
+
+def randomize(cfg, params, seed):
+    """Non-trivial LayerNorm gains and biases (the seeded init has 1 / 0)."""
+    rng = np.random.default_rng(seed)
+    p = params.copy()
+    w = oracle.unpack(ocfg(cfg), p)
+    for L in w["layers"]:
+        for k in ("ln1_w", "ln2_w"):
+            L[k][:] = 1 + 0.1 * rng.standard_normal(L[k].shape)
+        for k in ("ln1_b", "ln2_b", "c_attn_b", "c_proj_b", "mlp_fc_b", "mlp_proj_b"):
+            L[k][:] = 0.05 * rng.standard_normal(L[k].shape)
+    w["ln_f_w"][:] = 1 + 0.1 * rng.standard_normal(w["ln_f_w"].shape)
+    w["ln_f_b"][:] = 0.05 * rng.standard_normal(w["ln_f_b"].shape)
+    return p
+
+
+# ---------------------------------------------------------------- check_fast mirror
+
+def test_check_fast_shapes_tiny():
+    """tests/check_fast.c: 3L/4H/32C/V70/T16 (head size 8), srand(42), shapes
+    {1,1},{1,9},{2,6},{3,16},{1,16}, final-position logits, < 1e-4."""
+    cfg = cngpt_amd.TINY
+    params = cngpt_amd.init_weights(cfg, 42)
+    rng = np.random.default_rng(42)
+    with cngpt_amd.Model(cfg, params) as m:
+        for B, T in [(1, 1), (1, 9), (2, 6), (3, 16), (1, 16)]:
+            tk = rng.integers(0, cfg.vocab_size, size=(B, T), dtype=np.int32)
+            say(f"tiny B={B} T={T}")
+            compare(m.forward(tk, cngpt_amd.LAST), oracle.forward(ocfg(cfg), params, tk),
+                    abs_tol=1e-4, what="LAST")
+            compare(m.forward(tk, cngpt_amd.ALL),
+                    oracle.forward(ocfg(cfg), params, tk, oracle.ALL), abs_tol=1e-4, what="ALL")
+
+
+HS_CASES = {
+    "hs64": (cngpt_amd.Config(2, 4, 256, 1000, 256), [(1, 1), (1, 7), (2, 64), (3, 129), (2, 256)]),
+    "hs32": (cngpt_amd.Config(2, 4, 128, 333, 96), [(1, 5), (2, 33), (1, 96)]),
+    "hs16": (cngpt_amd.Config(1, 8, 128, 257, 70), [(2, 70)]),
+    "hs128": (cngpt_amd.Config(1, 2, 256, 500, 160), [(2, 130), (1, 160)]),
+}
+
+
+@pytest.mark.parametrize("name", list(HS_CASES))
+def test_head_sizes_and_ragged_shapes(name):
+    cfg, shapes = HS_CASES[name]
+    params = randomize(cfg, cngpt_amd.init_weights(cfg, 1234), 3)
+    rng = np.random.default_rng(9)
+    with cngpt_amd.Model(cfg, params) as m:
+        for B, T in shapes:
+            tk = rng.integers(0, cfg.vocab_size, size=(B, T), dtype=np.int32)
+            say(f"{name} B={B} T={T}")
+            compare(m.forward(tk, cngpt_amd.LAST), oracle.forward(ocfg(cfg), params, tk),
+                    what="LAST")
+            compare(m.forward(tk, cngpt_amd.ALL),
+                    oracle.forward(ocfg(cfg), params, tk, oracle.ALL), what="ALL")
+
+
+# ---------------------------------------------------------------- GPT-2 sizes
+
+@pytest.fixture(scope="module")
+def small():
+    cfg = cngpt_amd.GPT2_SMALL
+    params = cngpt_amd.init_weights(cfg, 1234)
+    m = cngpt_amd.Model(cfg, params)
+    yield cfg, params, m
+    m.close()
+
+
+def test_gpt2_small_b1_t64(small):
+    """GPT-2 small, B=1, T=64 LCG tokens (cngpt.c:338-342), both modes."""
+    cfg, params, m = small
+    tk = oracle.lcg_tokens(64, cfg.vocab_size).reshape(1, 64)
+    say("small B=1 T=64")
+    compare(m.forward(tk, cngpt_amd.LAST), oracle.forward(ocfg(cfg), params, tk), what="LAST")
+    compare(m.forward(tk, cngpt_amd.ALL), oracle.forward(ocfg(cfg), params, tk, oracle.ALL),
+            what="ALL")
+
+
+def test_gpt2_small_zero_tokens_b2_t300(small):
+    """All-zero tokens (the reference's timing input, cngpt.c:283) and a
+    sequence length that is not a multiple of any tile."""
+    cfg, params, m = small
+    tk = np.zeros((2, 300), np.int32)
+    tk[1] = oracle.lcg_tokens(300, cfg.vocab_size, seed=99)
+    say("small B=2 T=300")
+    compare(m.forward(tk, cngpt_amd.LAST), oracle.forward(ocfg(cfg), params, tk), what="LAST")
+
+
+def test_resident_path_matches(small):
+    cfg, params, m = small
+    tk = oracle.lcg_tokens(2 * 128, cfg.vocab_size, seed=5).reshape(2, 128)
+    ref = m.forward(tk, cngpt_amd.ALL)
+    m.reserve(2, 128, cngpt_amd.ALL)
+    m.upload_tokens(tk)
+    m.forward_resident(2, 128, cngpt_amd.ALL)
+    m.synchronize()
+    got = m.read_logits(0, ref.size).reshape(ref.shape)
+    assert np.array_equal(got, ref)
+
+
+def test_xl_width_one_layer():
+    """XL widths: C=1600 (K not a multiple of 128), 25 heads, N=4800/6400,
+    ragged vocabulary 50257."""
+    cfg = cngpt_amd.Config(1, 25, 1600, 50257, 128)
+    params = randomize(cfg, cngpt_amd.init_weights(cfg, 77), 8)
+    tk = np.random.default_rng(3).integers(0, cfg.vocab_size, size=(2, 100), dtype=np.int32)
+    with cngpt_amd.Model(cfg, params) as m:
+        say("xl-width B=2 T=100")
+        compare(m.forward(tk, cngpt_amd.ALL), oracle.forward(ocfg(cfg), params, tk, oracle.ALL),
+                what="ALL")
+        compare(m.forward(tk, cngpt_amd.LAST), oracle.forward(ocfg(cfg), params, tk),
+                what="LAST")
+
+
+# ---------------------------------------------------------------- errors
+
+def test_errors_are_reported(small):
+    cfg, params, m = small
+    with pytest.raises(cngpt_amd.CngptError, match="token"):
+        m.forward(np.array([[1, 2, cfg.vocab_size]], np.int32))
+    with pytest.raises(cngpt_amd.CngptError, match="token"):
+        m.forward(np.array([[-1]], np.int32))
+    with pytest.raises(cngpt_amd.CngptError, match="block_size"):
+        m.forward(np.zeros((1, cfg.block_size + 1), np.int32))
+    with pytest.raises(cngpt_amd.CngptError, match="parameter count"):
+        m.load_params(params[:-1])
+    with pytest.raises(cngpt_amd.CngptError):
+        cngpt_amd.Model(cfg, params, device=99)
+    # the handle still works after the errors
+    tk = np.zeros((1, 4), np.int32)
+    compare(m.forward(tk), oracle.forward(ocfg(cfg), params, tk), what="after errors")
