@@ -59,16 +59,32 @@ def prefill(m: cngpt_amd.Model, cfg, B: int, T: int, steps: int, warmup: int):
     return dt, prof, tokens
 
 
-def decode(m: cngpt_amd.Model, cfg, prompt_len: int, steps: int):
+def decode_bytes(cfg, params_n: int, B: int, first_pos: int, steps: int) -> float:
+    """Algorithmic HBM bytes of `steps` decode steps whose tokens sit at
+    positions first_pos.. : every weight once per step (wpe: one row), the
+    K and V rows of keys 0..p, the new q/k/v row and the logits."""
+    C, L, V = cfg.n_embd, cfg.n_layer, cfg.vocab_size
+    weights = 4.0 * (params_n - cfg.block_size * C + C)
+    total = 0.0
+    for p in range(first_pos, first_pos + steps):
+        total += weights + 4.0 * L * B * (p + 1) * 2 * C + 4.0 * L * B * 3 * C + 4.0 * B * V
+    return total
+
+
+def decode(m: cngpt_amd.Model, cfg, prompt_len: int, steps: int, draws=None):
+    """`steps` single-token decode steps after a prompt_len prompt, B=1, as
+    one cngpt_hip_generate call (one replayed HIP graph per step); greedy, or
+    temp 0.8 / top-k 40 sampling when draws are given."""
     prompt = lcg_tokens(prompt_len, cfg.vocab_size, 777).reshape(1, prompt_len)
+    kw = {} if draws is None else {"temperature": 0.8, "top_k": 40,
+                                   "draws": draws[:steps + 1]}
     m.decode_begin(prompt, capacity=prompt_len + steps)
-    m.decode_step(None, copy=False)          # warm-up step
+    warm = {} if draws is None else {"temperature": 0.8, "top_k": 40, "draws": draws[:8]}
+    m.generate(8, **warm)                     # warm-up, captures the step graph
     m.decode_begin(prompt, capacity=prompt_len + steps)
     m.synchronize()
     t0 = time.perf_counter()
-    for _ in range(steps):
-        m.decode_step(None, copy=False)
-    m.synchronize()
+    m.generate(steps + 1, **kw)
     return time.perf_counter() - t0
 
 
@@ -110,6 +126,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MiB",
                     help="also run one plain device copy of this size (counter calibration)")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="only the decode legs (for kernel traces of the decode step)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); "
@@ -121,6 +139,29 @@ def main():
     params = cngpt_amd.init_weights(cfg, SEED)
     m = cngpt_amd.Model(cfg, params)
 
+    if args.decode_only:
+        dec_dt = decode(m, cfg, 32, args.decode_steps)
+        dec_bytes = decode_bytes(cfg, params.size, 1, 32, args.decode_steps)
+        # per-kernel-class split of the same steps (direct launches, HIP events)
+        m.profile_reset()
+        m.profile(True)
+        prof_dt = decode(m, cfg, 32, args.decode_steps)
+        m.profile(False)
+        prof = m.profile_read()
+        m.close()
+        n = args.decode_steps
+        print(json.dumps({"decode_tok_s": round(n / dec_dt, 1),
+                          "ms_per_token": round(dec_dt * 1e3 / n, 4),
+                          "hbm_frac": round(dec_bytes / dec_dt / PEAK_HBM, 4),
+                          "graphs": os.environ.get("CNGPT_HIP_GRAPH", "1") != "0",
+                          "evented_ms_per_token": round(prof_dt * 1e3 / n, 4),
+                          "kernel_us_per_token": {k: round(v["ms"] * 1e3 / n, 2)
+                                                  for k, v in prof.items() if v["launches"]},
+                          "launches_per_token": {k: round(v["launches"] / n, 2)
+                                                 for k, v in prof.items() if v["launches"]}}),
+              flush=True)
+        return
+
     dt, prof, _ = prefill(m, cfg, B, T, args.steps, args.warmup)
     tokens = B * T * args.steps
     g = prof["gemm"]
@@ -129,6 +170,9 @@ def main():
     gemm_share = g["ms"] / (dt * 1e3)
 
     dec_dt = decode(m, cfg, 32, args.decode_steps)
+    dec_bytes = decode_bytes(cfg, params.size, 1, 32, args.decode_steps)
+    draws = np.random.default_rng(7).random(args.decode_steps + 1).astype(np.float32)
+    samp_dt = decode(m, cfg, 32, args.decode_steps, draws)
     m.close()
 
     # HBM-side bytes per GEMM launch from the committed rocprofv3 --pmc
@@ -166,7 +210,13 @@ def main():
         "gemm_mfma_util_pct": round(100 * achieved / PEAK_FP32_MFMA, 2),
         "decode": {"tok_s": round(args.decode_steps / dec_dt, 1),
                    "ms_per_token": round(dec_dt * 1e3 / args.decode_steps, 4),
-                   "prompt": 32, "steps": args.decode_steps, "B": 1, "sampling": "greedy"},
+                   "prompt": 32, "steps": args.decode_steps, "B": 1, "sampling": "greedy",
+                   "hbm": {"bound": "hbm", "achieved": round(dec_bytes / dec_dt / 1e9, 1),
+                           "peak": PEAK_HBM / 1e9, "unit": "GB/s",
+                           "frac": round(dec_bytes / dec_dt / PEAK_HBM, 4),
+                           "bytes_per_step": round(dec_bytes / args.decode_steps)},
+                   "sampled_tok_s": round(args.decode_steps / samp_dt, 1),
+                   "sampled": "temp 0.8, top-k 40, device sample_top_k"},
         "kernels": {k: {"ms_per_step": round(v["ms"] / args.steps, 3),
                         "launches_per_step": v["launches"] // max(args.steps, 1),
                         **({"tflops": round(v["flops"] / (v["ms"] * 1e-3) / 1e12, 2)}

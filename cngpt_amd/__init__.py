@@ -24,8 +24,10 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libcngpt_hip.so")
 
 LAST, ALL = 0, 1
-(K_GEMM, K_GEMV, K_ATTN, K_ATTN_ROW, K_LAYERNORM, K_EMBED, K_GATHER, K_ARGMAX) = range(8)
-KERNEL_CLASSES = ["gemm", "gemv", "attn", "attn_row", "layernorm", "embed", "gather", "argmax"]
+(K_GEMM, K_GEMV, K_ATTN, K_ATTN_ROW, K_LAYERNORM, K_EMBED, K_GATHER, K_ARGMAX,
+ K_SAMPLE) = range(9)
+KERNEL_CLASSES = ["gemm", "gemv", "attn", "attn_row", "layernorm", "embed", "gather", "argmax",
+                  "sample"]
 
 MAGIC = 0x434E4750
 VERSION = 1
@@ -71,7 +73,8 @@ EXPORTS = [
     "cngpt_hip_load_params", "cngpt_hip_reserve", "cngpt_hip_forward",
     "cngpt_hip_upload_tokens", "cngpt_hip_forward_resident", "cngpt_hip_synchronize",
     "cngpt_hip_read_logits", "cngpt_hip_logits_device", "cngpt_hip_decode_begin",
-    "cngpt_hip_decode_step", "cngpt_hip_argmax", "cngpt_hip_decode_length",
+    "cngpt_hip_decode_step", "cngpt_hip_generate", "cngpt_hip_argmax", "cngpt_hip_sample",
+    "cngpt_hip_decode_length",
     "cngpt_hip_profile_enable", "cngpt_hip_profile_reset", "cngpt_hip_profile_read",
     "cngpt_hip_host_alloc", "cngpt_hip_host_free", "cngpt_hip_init_weights",
     "fast_init", "fast_free", "fast_set_threads", "gpt_forward_fast", "gpt_forward_fast_all",
@@ -107,7 +110,9 @@ def lib():
     L.cngpt_hip_logits_device.restype = _VP
     L.cngpt_hip_decode_begin.argtypes = [_VP, _I, ctypes.c_int, ctypes.c_int, ctypes.c_int, _F]
     L.cngpt_hip_decode_step.argtypes = [_VP, _I, _F]
+    L.cngpt_hip_generate.argtypes = [_VP, ctypes.c_int, ctypes.c_float, ctypes.c_int, _F, _I]
     L.cngpt_hip_argmax.argtypes = [_VP, _I]
+    L.cngpt_hip_sample.argtypes = [_VP, ctypes.c_float, ctypes.c_int, _F, _I]
     L.cngpt_hip_decode_length.argtypes = [_VP]
     L.cngpt_hip_profile_enable.argtypes = [_VP, ctypes.c_int]
     L.cngpt_hip_profile_reset.argtypes = [_VP]
@@ -268,9 +273,31 @@ class Model:
                                            _fp(out) if out is not None else None), "decode_step")
         return out
 
+    def generate(self, n_new: int, temperature: float = 1.0, top_k: int = 0,
+                 draws=None) -> np.ndarray:
+        """n_new tokens per sequence after decode_begin, [B, n_new]. draws
+        None: greedy; else [n_new, B] uniform draws for sample_top_k."""
+        B = self.decode_batch
+        out = np.empty((B, n_new), dtype=np.int32)
+        dp = None
+        if draws is not None:
+            draws = np.ascontiguousarray(draws, dtype=np.float32).reshape(n_new, B)
+            dp = _fp(draws)
+        _check(lib().cngpt_hip_generate(self._h, n_new, temperature, top_k, dp, _ip(out)),
+               "generate")
+        return out
+
     def argmax(self, B: int) -> np.ndarray:
         out = np.empty(B, dtype=np.int32)
         _check(lib().cngpt_hip_argmax(self._h, _ip(out)), "argmax")
+        return out
+
+    def sample(self, B: int, temperature: float, top_k: int, draws) -> np.ndarray:
+        """One token per row of the current last-position logits."""
+        draws = np.ascontiguousarray(draws, dtype=np.float32).reshape(B)
+        out = np.empty(B, dtype=np.int32)
+        _check(lib().cngpt_hip_sample(self._h, temperature, top_k, _fp(draws), _ip(out)),
+               "sample")
         return out
 
     def decode_length(self) -> int:

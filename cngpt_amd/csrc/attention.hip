@@ -16,8 +16,8 @@
 // order of the S^T output layout is used as the k order of that product).
 // The softmax is the online (running max / running sum) form.
 //
-// k_attn_row: one query row per (sequence, head) against keys 0..t: the
-// last-position pass (fast.c:287-297) and one decode step.
+// The one-query form (the last-position pass, fast.c:287-297, and a decode
+// step) is k_attn_dec in decode.hip.
 #include "common.h"
 #include "kernels.h"
 
@@ -184,86 +184,12 @@ __global__ void __launch_bounds__(256, 2)
     }
 }
 
-// One workgroup per (sequence, head); query at position t against keys 0..t.
-template <int HS>
-__global__ void __launch_bounds__(256)
-    k_attn_row(const float* __restrict__ qkv, long seq_stride, float* __restrict__ out, int q_pos,
-               const int* __restrict__ pos_dev, int C, int H, float scale) {
-    extern __shared__ float sm[];  // [HS] query, [4] reductions, [t+1] scores
-    float* qs = sm;
-    float* red = sm + HS;
-    float* sc = sm + HS + 8;
-    __shared__ float part[256];
-
-    const int bh = blockIdx.x, b = bh / H, h = bh % H;
-    const int t = pos_dev ? *pos_dev : q_pos;
-    const int nk = t + 1;
-    const long C3 = 3L * C;
-    const float* base = qkv + (long)b * seq_stride * C3 + h * HS;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-
-    for (int d = tid; d < HS; d += 256) qs[d] = base[(long)t * C3 + d];
-    __syncthreads();
-
-    float mx = -INFINITY;
-    for (int j = tid; j < nk; j += 256) {
-        const float* kp = base + (long)j * C3 + C;
-        float acc = 0.f;
-#pragma unroll
-        for (int d = 0; d < HS; d += 4) {
-            f32x4 kv = *(const f32x4*)(kp + d);
-            acc += (kv.x * qs[d] + kv.y * qs[d + 1]) + (kv.z * qs[d + 2] + kv.w * qs[d + 3]);
-        }
-        acc *= scale;
-        sc[j] = acc;
-        mx = fmaxf(mx, acc);
-    }
-    mx = wave_max(mx);
-    if (lane == 0) red[wave] = mx;
-    __syncthreads();
-    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    float sum = 0.f;
-    for (int j = tid; j < nk; j += 256) {
-        float p = expf(sc[j] - mx);
-        sc[j] = p;
-        sum += p;
-    }
-    sum = wave_sum(sum);
-    __syncthreads();  // everyone has read red[] (max) before it is reused
-    if (lane == 0) red[4 + wave] = sum;
-    __syncthreads();
-    sum = (red[4] + red[5]) + (red[6] + red[7]);
-
-    // out[d] = sum_j p_j V[j][d]: thread = (d, slice of keys).
-    constexpr int NS = 256 / HS;
-    const int d = tid % HS, sl = tid / HS;
-    float acc = 0.f;
-    if (sl < NS)
-        for (int j = sl; j < nk; j += NS) acc += sc[j] * base[(long)j * C3 + 2 * C + d];
-    part[tid] = acc;
-    __syncthreads();
-    if (tid < HS) {
-        float s = 0.f;
-        for (int k = 0; k < NS; k++) s += part[k * HS + tid];
-        out[(long)b * C + h * HS + tid] = s * (1.0f / sum);
-    }
-}
-
 template <int HS>
 hipError_t causal_hs(const float* qkv, long seq_stride, float* out, int B, int T, int C, int H,
                      hipStream_t s) {
     const int nqb = (T + 127) / 128;
     const float scale = 1.0f / sqrtf((float)HS);
     k_attn_causal<HS><<<nqb * B * H, 256, 0, s>>>(qkv, seq_stride, out, B, T, C, H, nqb, scale);
-    return hipGetLastError();
-}
-
-template <int HS>
-hipError_t row_hs(const float* qkv, long seq_stride, float* out, int B, int q_pos,
-                  const int* pos_dev, int max_keys, int C, int H, hipStream_t s) {
-    const float scale = 1.0f / sqrtf((float)HS);
-    size_t lds = (size_t)(HS + 8 + max_keys) * sizeof(float);
-    k_attn_row<HS><<<B * H, 256, lds, s>>>(qkv, seq_stride, out, q_pos, pos_dev, C, H, scale);
     return hipGetLastError();
 }
 
@@ -278,21 +204,6 @@ hipError_t launch_attention_causal(const float* qkv, long seq_stride, float* out
         case 32: return causal_hs<32>(qkv, seq_stride, out, B, T, C, H, s);
         case 64: return causal_hs<64>(qkv, seq_stride, out, B, T, C, H, s);
         case 128: return causal_hs<128>(qkv, seq_stride, out, B, T, C, H, s);
-    }
-    return hipErrorInvalidValue;
-}
-
-hipError_t launch_attention_row(const float* qkv, long seq_stride, float* out, int B, int q_pos,
-                                const int* pos_dev, int max_keys, int C, int H, hipStream_t s) {
-    if (B <= 0) return hipSuccess;
-    if (max_keys <= 0 || (size_t)(max_keys + 136) * sizeof(float) > 64 * 1024)
-        return hipErrorInvalidValue;
-    switch (C / H) {
-        case 8: return row_hs<8>(qkv, seq_stride, out, B, q_pos, pos_dev, max_keys, C, H, s);
-        case 16: return row_hs<16>(qkv, seq_stride, out, B, q_pos, pos_dev, max_keys, C, H, s);
-        case 32: return row_hs<32>(qkv, seq_stride, out, B, q_pos, pos_dev, max_keys, C, H, s);
-        case 64: return row_hs<64>(qkv, seq_stride, out, B, q_pos, pos_dev, max_keys, C, H, s);
-        case 128: return row_hs<128>(qkv, seq_stride, out, B, q_pos, pos_dev, max_keys, C, H, s);
     }
     return hipErrorInvalidValue;
 }

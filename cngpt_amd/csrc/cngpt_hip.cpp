@@ -13,6 +13,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <vector>
 
@@ -75,9 +76,25 @@ struct cngpt_hip_ctx {
     int* dev_err = nullptr;
     int* pos = nullptr;      // decode position (device)
     int* next_tok = nullptr; // [B] decode tokens (device)
+    int* hist = nullptr;     // [B][capKV] token fed at each position (decode)
     float *x = nullptr, *ln = nullptr, *qkv = nullptr, *aout = nullptr, *hid = nullptr;
     float *logits = nullptr;
     float *xc = nullptr, *lnc = nullptr, *aoutc = nullptr, *hidc = nullptr;
+    float* am_part_v = nullptr;  // [8][V] argmax partials of the lm_head
+    int* am_part_i = nullptr;
+    float* attn_part = nullptr;  // [B*H][attn_splits][hs+4] split-key partials
+    int attn_splits = 0;
+    float* draws = nullptr;      // [capKV+1][B] uniform draws for sampling
+    float* prob = nullptr;       // [B][ldp] sampling scratch
+    long ldp = 0;
+    int pos_host = 0;            // staging for the position upload
+
+    // the decode step as a replayable graph (kernels only); CNGPT_HIP_GRAPH=0
+    // in the environment at create time selects direct launches instead
+    bool use_graph = true;
+    hipGraphExec_t step_exec = nullptr;
+    int graph_B = 0, graph_cap = 0;
+    const void *graph_act = nullptr, *graph_par = nullptr;
 
     // state of the last forward / decode
     int curB = 0, curT = 0, curMode = CNGPT_LAST;
@@ -132,9 +149,29 @@ struct Timed {
 
 // ---------------------------------------------------------------- launches
 
+// Products over M <= 8 rows go to the decode GEMV (one wavefront per output
+// column, LayerNorm of the input rows optionally folded in); larger M to the
+// MFMA tile kernel.
+constexpr int SKINNY = 8;
+
 int run_gemm(cngpt_hip_ctx* h, const float* X, const float* W, const float* bias, float* Y, int M,
              int N, int K, int epi, int seg = 0, long seg_stride = 0, long ldy = -1,
              int row_off = 0, const int* row_off_dev = nullptr) {
+    const double flops = 2.0 * M * N * K;
+    const double bytes =
+        4.0 * ((double)M * K + (double)N * K + (double)M * N * (epi == EPI_RESID ? 2 : 1));
+    if (M <= SKINNY) {
+        DecGemvArgs d{};
+        d.X = X; d.ldx = K; d.W = W; d.bias = bias; d.Y = Y;
+        d.ldy = ldy < 0 ? N : ldy;
+        d.M = M; d.N = N; d.K = K;
+        d.seg = seg; d.seg_stride = seg_stride;
+        d.row_off = row_off; d.row_off_dev = row_off_dev;
+        d.epi = epi;
+        Timed t(h, CNGPT_K_GEMV, flops, bytes);
+        HIP_TRY(launch_dgemv(d, h->stream));
+        return 0;
+    }
     GemmArgs a{};
     a.X = X; a.W = W; a.bias = bias; a.Y = Y;
     a.M = M; a.N = N; a.K = K;
@@ -142,11 +179,8 @@ int run_gemm(cngpt_hip_ctx* h, const float* X, const float* W, const float* bias
     a.seg = seg; a.seg_stride = seg_stride;
     a.row_off = row_off; a.row_off_dev = row_off_dev;
     a.epi = epi;
-    const bool skinny = M <= 8;
-    double flops = 2.0 * M * N * K;
-    double bytes = 4.0 * ((double)M * K + (double)N * K + (double)M * N * (epi == EPI_RESID ? 2 : 1));
-    Timed t(h, skinny ? CNGPT_K_GEMV : CNGPT_K_GEMM, flops, bytes);
-    HIP_TRY(skinny ? launch_gemv(a, h->stream) : launch_gemm(a, h->stream));
+    Timed t(h, CNGPT_K_GEMM, flops, bytes);
+    HIP_TRY(launch_gemm(a, h->stream));
     return 0;
 }
 
@@ -156,6 +190,118 @@ int run_ln(cngpt_hip_ctx* h, const float* x, long in_stride, const float* w, con
     Timed t(h, CNGPT_K_LAYERNORM, 0.0, 8.0 * C * rows);
     HIP_TRY(launch_layernorm(x, in_stride, w, b, out, C, rows, C, h->stream));
     return 0;
+}
+
+// Y = epi(LN(x) . W^T) over M rows of x (row stride C). For M <= 8 the
+// LayerNorm runs inside the product; otherwise into `scratch` first.
+int run_ln_gemm(cngpt_hip_ctx* h, const float* x, const float* lw, const float* lb,
+                float* scratch, const float* W, const float* bias, float* Y, int M, int N,
+                int epi, int seg = 0, long seg_stride = 0, long ldy = -1,
+                const int* row_off_dev = nullptr) {
+    const int C = h->cfg.n_embd;
+    if (M <= SKINNY) {
+        DecGemvArgs d{};
+        d.X = x; d.ldx = C; d.ln_w = lw; d.ln_b = lb; d.W = W; d.bias = bias; d.Y = Y;
+        d.ldy = ldy < 0 ? N : ldy;
+        d.M = M; d.N = N; d.K = C;
+        d.seg = seg; d.seg_stride = seg_stride;
+        d.row_off_dev = row_off_dev;
+        d.epi = epi;
+        Timed t(h, CNGPT_K_GEMV, 2.0 * M * N * C,
+                4.0 * ((double)M * C + (double)N * C + (double)M * N));
+        HIP_TRY(launch_dgemv(d, h->stream));
+        return 0;
+    }
+    if (run_ln(h, x, C, lw, lb, scratch, M)) return -1;
+    return run_gemm(h, scratch, W, bias, Y, M, N, C, epi, seg, seg_stride, ldy, 0, row_off_dev);
+}
+
+// Final LayerNorm and lm_head over M rows of x -> logits [M, V]; with
+// want_tok the greedy token of each row goes to next_tok, and pos_inc (if
+// set) is advanced once everything else of the step has run.
+int run_lm_head(cngpt_hip_ctx* h, const float* x, int M, bool want_tok, int* pos_inc) {
+    const int C = h->cfg.n_embd, V = h->cfg.vocab_size;
+    if (M <= SKINNY) {
+        DecGemvArgs d{};
+        d.X = x; d.ldx = C; d.ln_w = h->lnf_w; d.ln_b = h->lnf_b; d.W = h->wte;
+        d.Y = h->logits; d.ldy = V;
+        d.M = M; d.N = V; d.K = C;
+        d.epi = EPI_STORE;
+        const int parts = dgemv_argmax_parts(d);
+        if (want_tok) {
+            if (parts > V) return fail("argmax partials exceed their buffer");
+            d.argmax = 1;
+            d.part_v = h->am_part_v;
+            d.part_i = h->am_part_i;
+        }
+        {
+            Timed t(h, CNGPT_K_GEMV, 2.0 * M * V * C,
+                    4.0 * ((double)M * C + (double)V * C + (double)M * V));
+            HIP_TRY(launch_dgemv(d, h->stream));
+        }
+        if (want_tok) {
+            Timed t(h, CNGPT_K_ARGMAX, 0.0, 8.0 * M * parts);
+            HIP_TRY(launch_argmax_part(h->am_part_v, h->am_part_i, M, parts, h->next_tok, pos_inc,
+                                       h->stream));
+        }
+    } else {
+        if (run_ln(h, x, C, h->lnf_w, h->lnf_b, h->lnc, M)) return -1;
+        if (run_gemm(h, h->lnc, h->wte, nullptr, h->logits, M, V, C, EPI_STORE)) return -1;
+        if (want_tok) {
+            Timed t(h, CNGPT_K_ARGMAX, 0.0, 4.0 * M * V);
+            HIP_TRY(launch_argmax_rows(h->logits, M, V, h->next_tok, pos_inc, h->stream));
+        }
+    }
+    h->logits_count = (size_t)M * V;
+    return 0;
+}
+
+// Attention of one query row per sequence (position q_pos, or *pos_dev)
+// followed by the c_proj product with its residual: xres[b] += aout[b] . W^T
+// + bias. For B <= 8 the c_proj product merges the attention splits itself;
+// otherwise the merged rows go through aoutc.
+int run_attn_row_proj(cngpt_hip_ctx* h, const float* qkv, long seq_stride, int B, int q_pos,
+                      const int* pos_dev, int max_keys, const LayerW& w, float* xres) {
+    const cngpt_hip_config& c = h->cfg;
+    const int C = c.n_embd, hs = C / c.n_head;
+    AttnDecArgs a{};
+    a.qkv = qkv; a.seq_stride = seq_stride;
+    a.C = C; a.H = c.n_head;
+    a.q_pos = q_pos; a.pos_dev = pos_dev;
+    a.scale = 1.0f / sqrtf((float)hs);
+    a.part = h->attn_part; a.max_splits = h->attn_splits;
+    {
+        const double keys = pos_dev ? 0.5 * max_keys : q_pos + 1.0;
+        Timed t(h, CNGPT_K_ATTN_ROW, 4.0 * C * keys * B,
+                4.0 * ((double)B * keys * 2 * C + (double)B * C));
+        HIP_TRY(launch_attention_dec(a, B, max_keys, h->stream));
+    }
+    MergeArgs g{};
+    g.part = h->attn_part; g.stride = h->attn_splits;
+    g.H = c.n_head; g.hs = hs; g.kps = attn_dec_keys_per_split(hs);
+    g.q_pos = q_pos; g.pos_dev = pos_dev;
+    if (B <= SKINNY) {
+        DecGemvArgs d{};
+        d.merge = g;
+        d.W = w.proj_w; d.bias = w.proj_b; d.Y = xres; d.ldy = C;
+        d.M = B; d.N = C; d.K = C;
+        d.epi = EPI_RESID;
+        Timed t(h, CNGPT_K_GEMV, 2.0 * B * C * C, 4.0 * ((double)C * C + 2.0 * B * C));
+        HIP_TRY(launch_dgemv(d, h->stream));
+        return 0;
+    }
+    {
+        Timed t(h, CNGPT_K_ATTN_ROW, 0.0, 4.0 * B * C);
+        HIP_TRY(launch_attention_merge(g, B, h->aoutc, C, h->stream));
+    }
+    return run_gemm(h, h->aoutc, w.proj_w, w.proj_b, xres, B, C, C, EPI_RESID);
+}
+
+void drop_graph(cngpt_hip_ctx* h) {
+    if (h->step_exec) (void)hipGraphExecDestroy(h->step_exec);
+    h->step_exec = nullptr;
+    h->graph_B = h->graph_cap = 0;
+    h->graph_act = h->graph_par = nullptr;
 }
 
 // ---------------------------------------------------------------- arena
@@ -172,14 +318,22 @@ int ensure_arena(cngpt_hip_ctx* h, int B, int T, int all, int kv) {
     const int nT = std::max(T, h->capT);
     const int nAll = (all || h->capAll) ? 1 : 0;
     const int nKV = std::max(kv, h->capKV);
-    const size_t C = c.n_embd, V = c.vocab_size, L = c.n_layer;
+    const size_t C = c.n_embd, V = c.vocab_size, L = c.n_layer, H = c.n_head;
     const size_t rows = (size_t)nB * nT;
     const size_t qkv_rows = std::max(rows, L * nB * (size_t)nKV);
-    size_t sz[16], total = 0;
+    const int kps = attn_dec_keys_per_split(c.n_embd / c.n_head);
+    const int splits = (c.block_size + kps - 1) / kps;
+    size_t sz[24], total = 0;
     int n = 0;
     sz[n++] = rows * sizeof(int);             // tok
     sz[n++] = 4 * sizeof(int);                // dev_err, pos
     sz[n++] = (size_t)nB * sizeof(int);       // next_tok
+    sz[n++] = (size_t)nB * std::max(nKV, 1) * sizeof(int);         // hist
+    sz[n++] = 8 * V * sizeof(float);                               // am_part_v
+    sz[n++] = 8 * V * sizeof(int);                                 // am_part_i
+    sz[n++] = (size_t)nB * H * splits * (C / H + 4) * sizeof(float);  // attn_part
+    sz[n++] = (size_t)nB * (nKV + 1) * sizeof(float);              // draws
+    sz[n++] = (size_t)nB * ((V + 3) / 4 * 4) * sizeof(float);      // prob
     sz[n++] = rows * C * 4;                   // x
     sz[n++] = rows * C * 4;                   // ln
     sz[n++] = qkv_rows * 3 * C * 4;           // qkv / KV cache
@@ -194,6 +348,7 @@ int ensure_arena(cngpt_hip_ctx* h, int B, int T, int all, int kv) {
 
     if (h->d_act) {
         HIP_TRY(hipStreamSynchronize(h->stream));
+        drop_graph(h);
         HIP_TRY(hipFree(h->d_act));
         h->d_act = nullptr;
         h->act_bytes = 0;
@@ -215,6 +370,14 @@ int ensure_arena(cngpt_hip_ctx* h, int B, int T, int all, int kv) {
     h->dev_err = (int*)take(sz[n++]);
     h->pos = h->dev_err + 1;
     h->next_tok = (int*)take(sz[n++]);
+    h->hist = (int*)take(sz[n++]);
+    h->am_part_v = (float*)take(sz[n++]);
+    h->am_part_i = (int*)take(sz[n++]);
+    h->attn_part = (float*)take(sz[n++]);
+    h->attn_splits = splits;
+    h->draws = (float*)take(sz[n++]);
+    h->prob = (float*)take(sz[n++]);
+    h->ldp = (long)((V + 3) / 4 * 4);
     h->x = (float*)take(sz[n++]);
     h->ln = (float*)take(sz[n++]);
     h->qkv = (float*)take(sz[n++]);
@@ -239,23 +402,23 @@ int check_tokens(const cngpt_hip_ctx* h, const int* tokens, long n) {
 
 // Enqueue one forward over h->tok [B, T]. kv: QKV rows go to the per-layer
 // KV cache (capacity h->capKV per sequence) instead of the reused buffer.
-int enqueue_forward(cngpt_hip_ctx* h, int B, int T, int mode, bool kv) {
+// want_tok: LAST mode also leaves the greedy token of each row in next_tok.
+int enqueue_forward(cngpt_hip_ctx* h, int B, int T, int mode, bool kv, bool want_tok) {
     const cngpt_hip_config& c = h->cfg;
-    const int C = c.n_embd, V = c.vocab_size, L = c.n_layer, H = c.n_head;
+    const int C = c.n_embd, L = c.n_layer, H = c.n_head;
     const long rows = (long)B * T;
     const long seq_stride = kv ? h->capKV : T;
     {
         Timed t(h, CNGPT_K_EMBED, 0.0, 12.0 * C * rows);
-        HIP_TRY(launch_embed(h->tok, h->wte, h->wpe, h->x, rows, T, C, V, 0, nullptr, h->dev_err,
-                             h->stream));
+        HIP_TRY(launch_embed(h->tok, h->wte, h->wpe, h->x, rows, T, C, c.vocab_size, 0, nullptr,
+                             h->dev_err, nullptr, 0, h->stream));
     }
     for (int l = 0; l < L; l++) {
         const LayerW& w = h->layers[l];
         const bool last = (mode == CNGPT_LAST) && (l == L - 1);
         float* qkv = kv ? h->qkv + (size_t)l * B * h->capKV * 3 * C : h->qkv;
-        if (run_ln(h, h->x, C, w.ln1_w, w.ln1_b, h->ln, (int)rows)) return -1;
-        if (run_gemm(h, h->ln, w.attn_w, w.attn_b, qkv, (int)rows, 3 * C, C, EPI_BIAS,
-                     kv ? T : 0, seq_stride, 3L * C))
+        if (run_ln_gemm(h, h->x, w.ln1_w, w.ln1_b, h->ln, w.attn_w, w.attn_b, qkv, (int)rows,
+                        3 * C, EPI_BIAS, kv ? T : 0, seq_stride, 3L * C))
             return -1;
         if (!last) {
             {
@@ -265,77 +428,110 @@ int enqueue_forward(cngpt_hip_ctx* h, int B, int T, int mode, bool kv) {
                 HIP_TRY(launch_attention_causal(qkv, seq_stride, h->aout, B, T, C, H, h->stream));
             }
             if (run_gemm(h, h->aout, w.proj_w, w.proj_b, h->x, (int)rows, C, C, EPI_RESID)) return -1;
-            if (run_ln(h, h->x, C, w.ln2_w, w.ln2_b, h->ln, (int)rows)) return -1;
-            if (run_gemm(h, h->ln, w.fc_w, w.fc_b, h->hid, (int)rows, 4 * C, C, EPI_BIAS_GELU))
+            if (run_ln_gemm(h, h->x, w.ln2_w, w.ln2_b, h->ln, w.fc_w, w.fc_b, h->hid, (int)rows,
+                            4 * C, EPI_BIAS_GELU))
                 return -1;
             if (run_gemm(h, h->hid, w.mlp_w, w.mlp_b, h->x, (int)rows, C, 4 * C, EPI_RESID))
                 return -1;
         } else {
-            {
-                double fl = 4.0 * C * (double)T * B;
-                double by = 4.0 * ((double)B * T * 2 * C + 2.0 * B * C);
-                Timed t(h, CNGPT_K_ATTN_ROW, fl, by);
-                HIP_TRY(launch_attention_row(qkv, seq_stride, h->aoutc, B, T - 1, nullptr, T, C, H,
-                                             h->stream));
-            }
+            // Last layer, LAST mode: the final query row of each sequence only,
+            // then the rest of the layer on those B rows (fast.c:287-311).
             {
                 Timed t(h, CNGPT_K_GATHER, 0.0, 8.0 * B * C);
                 HIP_TRY(launch_gather_rows(h->x + (size_t)(T - 1) * C, (long)T * C, h->xc, B, C,
                                            h->stream));
             }
-            if (run_gemm(h, h->aoutc, w.proj_w, w.proj_b, h->xc, B, C, C, EPI_RESID)) return -1;
-            if (run_ln(h, h->xc, C, w.ln2_w, w.ln2_b, h->lnc, B)) return -1;
-            if (run_gemm(h, h->lnc, w.fc_w, w.fc_b, h->hidc, B, 4 * C, C, EPI_BIAS_GELU)) return -1;
+            if (run_attn_row_proj(h, qkv, seq_stride, B, T - 1, nullptr, T, w, h->xc)) return -1;
+            if (run_ln_gemm(h, h->xc, w.ln2_w, w.ln2_b, h->lnc, w.fc_w, w.fc_b, h->hidc, B, 4 * C,
+                            EPI_BIAS_GELU))
+                return -1;
             if (run_gemm(h, h->hidc, w.mlp_w, w.mlp_b, h->xc, B, C, 4 * C, EPI_RESID)) return -1;
         }
     }
     if (mode == CNGPT_ALL) {
         if (run_ln(h, h->x, C, h->lnf_w, h->lnf_b, h->ln, (int)rows)) return -1;
-        if (run_gemm(h, h->ln, h->wte, nullptr, h->logits, (int)rows, V, C, EPI_STORE)) return -1;
-        h->logits_count = (size_t)rows * V;
+        if (run_gemm(h, h->ln, h->wte, nullptr, h->logits, (int)rows, c.vocab_size, C, EPI_STORE))
+            return -1;
+        h->logits_count = (size_t)rows * c.vocab_size;
     } else {
-        if (run_ln(h, h->xc, C, h->lnf_w, h->lnf_b, h->lnc, B)) return -1;
-        if (run_gemm(h, h->lnc, h->wte, nullptr, h->logits, B, V, C, EPI_STORE)) return -1;
-        h->logits_count = (size_t)B * V;
+        if (run_lm_head(h, h->xc, B, want_tok, nullptr)) return -1;
     }
     h->curB = B; h->curT = T; h->curMode = mode;
     return 0;
 }
 
-// One decode step over h->next_tok [B] at position h->kvLen.
+// One decode step: the token next_tok[b] at position *pos for every cached
+// sequence; logits [B, V], the greedy tokens in next_tok, then *pos += 1.
+// Every position-dependent value is read from device memory, so the same
+// enqueued sequence (a captured graph) serves every step.
 int enqueue_decode_step(cngpt_hip_ctx* h) {
     const cngpt_hip_config& c = h->cfg;
-    const int C = c.n_embd, V = c.vocab_size, L = c.n_layer, H = c.n_head;
-    const int B = h->kvB, p = h->kvLen;
+    const int C = c.n_embd, L = c.n_layer;
+    const int B = h->kvB;
     const long cap = h->capKV;
     {
         Timed t(h, CNGPT_K_EMBED, 0.0, 12.0 * C * B);
-        HIP_TRY(launch_embed(h->next_tok, h->wte, h->wpe, h->xc, B, 1, C, V, p, nullptr,
-                             h->dev_err, h->stream));
+        HIP_TRY(launch_embed(h->next_tok, h->wte, h->wpe, h->xc, B, 1, C, c.vocab_size, 0, h->pos,
+                             h->dev_err, h->hist, cap, h->stream));
     }
     for (int l = 0; l < L; l++) {
         const LayerW& w = h->layers[l];
         float* kvl = h->qkv + (size_t)l * B * cap * 3 * C;
-        if (run_ln(h, h->xc, C, w.ln1_w, w.ln1_b, h->lnc, B)) return -1;
-        if (run_gemm(h, h->lnc, w.attn_w, w.attn_b, kvl, B, 3 * C, C, EPI_BIAS, 1, cap, 3L * C, p))
+        if (run_ln_gemm(h, h->xc, w.ln1_w, w.ln1_b, h->lnc, w.attn_w, w.attn_b, kvl, B, 3 * C,
+                        EPI_BIAS, 1, cap, 3L * C, h->pos))
             return -1;
-        {
-            double fl = 4.0 * C * (double)(p + 1) * B;
-            double by = 4.0 * ((double)B * (p + 1) * 2 * C + 2.0 * B * C);
-            Timed t(h, CNGPT_K_ATTN_ROW, fl, by);
-            HIP_TRY(launch_attention_row(kvl, cap, h->aoutc, B, p, nullptr, (int)cap, C, H,
-                                         h->stream));
-        }
-        if (run_gemm(h, h->aoutc, w.proj_w, w.proj_b, h->xc, B, C, C, EPI_RESID)) return -1;
-        if (run_ln(h, h->xc, C, w.ln2_w, w.ln2_b, h->lnc, B)) return -1;
-        if (run_gemm(h, h->lnc, w.fc_w, w.fc_b, h->hidc, B, 4 * C, C, EPI_BIAS_GELU)) return -1;
+        if (run_attn_row_proj(h, kvl, cap, B, 0, h->pos, (int)cap, w, h->xc)) return -1;
+        if (run_ln_gemm(h, h->xc, w.ln2_w, w.ln2_b, h->lnc, w.fc_w, w.fc_b, h->hidc, B, 4 * C,
+                        EPI_BIAS_GELU))
+            return -1;
         if (run_gemm(h, h->hidc, w.mlp_w, w.mlp_b, h->xc, B, C, 4 * C, EPI_RESID)) return -1;
     }
-    if (run_ln(h, h->xc, C, h->lnf_w, h->lnf_b, h->lnc, B)) return -1;
-    if (run_gemm(h, h->lnc, h->wte, nullptr, h->logits, B, V, C, EPI_STORE)) return -1;
-    h->logits_count = (size_t)B * V;
+    if (run_lm_head(h, h->xc, B, true, h->pos)) return -1;
     h->curB = B; h->curT = 1; h->curMode = CNGPT_LAST;
-    h->kvLen = p + 1;
+    return 0;
+}
+
+// Run one decode step: replay the captured graph (captured on first use,
+// again after the arena or the batch changed); direct launches while the
+// timing counters are on, so every kernel gets its event pair.
+int run_decode_step(cngpt_hip_ctx* h) {
+    if (h->prof || !h->use_graph) {
+        if (enqueue_decode_step(h)) return -1;
+    } else {
+        if (!h->step_exec || h->graph_B != h->kvB || h->graph_cap != h->capKV ||
+            h->graph_act != h->d_act || h->graph_par != h->d_params) {
+            drop_graph(h);
+            hipGraph_t g = nullptr;
+            HIP_TRY(hipStreamBeginCapture(h->stream, hipStreamCaptureModeThreadLocal));
+            const int rc = enqueue_decode_step(h);
+            const hipError_t e = hipStreamEndCapture(h->stream, &g);
+            if (rc || e != hipSuccess) {
+                if (g) (void)hipGraphDestroy(g);
+                (void)hipGetLastError();
+                return rc ? -1 : fail("decode graph capture failed: %s", hipGetErrorString(e));
+            }
+            hipGraphExec_t ex = nullptr;
+            const hipError_t ei = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+            (void)hipGraphDestroy(g);
+            if (ei != hipSuccess) return fail("decode graph instantiate: %s", hipGetErrorString(ei));
+            h->step_exec = ex;
+            h->graph_B = h->kvB;
+            h->graph_cap = h->capKV;
+            h->graph_act = h->d_act;
+            h->graph_par = h->d_params;
+        }
+        HIP_TRY(hipGraphLaunch(h->step_exec, h->stream));
+        h->curB = h->kvB; h->curT = 1; h->curMode = CNGPT_LAST;
+        h->logits_count = (size_t)h->kvB * h->cfg.vocab_size;
+    }
+    h->kvLen += 1;
+    return 0;
+}
+
+int run_sample(cngpt_hip_ctx* h, const float* draws, float temp, int top_k) {
+    Timed t(h, CNGPT_K_SAMPLE, 0.0, 4.0 * h->kvB * h->cfg.vocab_size);
+    HIP_TRY(launch_sample(h->logits, h->kvB, h->cfg.vocab_size, temp, top_k, draws, h->prob,
+                          h->ldp, h->next_tok, h->stream));
     return 0;
 }
 
@@ -381,6 +577,8 @@ int cngpt_hip_create(int device, cngpt_hip_ctx** out) {
     HIP_TRY(hipSetDevice(device));
     cngpt_hip_ctx* h = new cngpt_hip_ctx();
     h->device = device;
+    const char* g = getenv("CNGPT_HIP_GRAPH");
+    h->use_graph = !(g && g[0] == '0');
     if (hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking) != hipSuccess) {
         delete h;
         return fail("hipStreamCreate failed");
@@ -393,6 +591,7 @@ void cngpt_hip_destroy(cngpt_hip_ctx* h) {
     if (!h) return;
     (void)hipSetDevice(h->device);
     if (h->stream) (void)hipStreamSynchronize(h->stream);
+    drop_graph(h);
     for (hipEvent_t e : h->pool) (void)hipEventDestroy(e);
     if (h->d_act) (void)hipFree(h->d_act);
     if (h->d_params) (void)hipFree(h->d_params);
@@ -421,6 +620,7 @@ int cngpt_hip_load_params(cngpt_hip_ctx* h, const cngpt_hip_config* cfg, const f
             h->d_params = nullptr;
         }
         if (h->d_act) {
+            drop_graph(h);
             HIP_TRY(hipFree(h->d_act));
             h->d_act = nullptr;
             h->capB = h->capT = h->capAll = h->capKV = 0;
@@ -492,7 +692,8 @@ int cngpt_hip_forward_resident(cngpt_hip_ctx* h, int B, int T, int mode) {
     if (B > h->capB || T > h->capT || (mode == CNGPT_ALL && !h->capAll))
         return fail("forward_resident: arena not reserved for B=%d T=%d mode=%d", B, T, mode);
     HIP_TRY(hipSetDevice(h->device));
-    return enqueue_forward(h, B, T, mode, false);
+    h->kvB = h->kvLen = 0;
+    return enqueue_forward(h, B, T, mode, false, false);
 }
 
 int cngpt_hip_forward(cngpt_hip_ctx* h, const int* tokens, int B, int T, int mode,
@@ -508,7 +709,7 @@ int cngpt_hip_forward(cngpt_hip_ctx* h, const int* tokens, int B, int T, int mod
     h->kvB = h->kvLen = 0;
     HIP_TRY(hipMemcpyAsync(h->tok, tokens, (size_t)B * T * sizeof(int), hipMemcpyHostToDevice,
                            h->stream));
-    if (enqueue_forward(h, B, T, mode, false)) return -1;
+    if (enqueue_forward(h, B, T, mode, false, false)) return -1;
     if (logits_out)
         HIP_TRY(hipMemcpyAsync(logits_out, h->logits, h->logits_count * sizeof(float),
                                hipMemcpyDeviceToHost, h->stream));
@@ -548,15 +749,22 @@ int cngpt_hip_decode_begin(cngpt_hip_ctx* h, const int* prompt, int B, int T, in
     if (check_tokens(h, prompt, (long)B * T)) return -1;
     HIP_TRY(hipSetDevice(h->device));
     if (ensure_arena(h, B, T, 0, capacity)) return -1;
+    h->kvB = h->kvLen = 0;
     HIP_TRY(hipMemcpyAsync(h->tok, prompt, (size_t)B * T * sizeof(int), hipMemcpyHostToDevice,
                            h->stream));
-    if (enqueue_forward(h, B, T, CNGPT_LAST, true)) return -1;
-    h->kvB = B;
-    h->kvLen = T;
+    if (enqueue_forward(h, B, T, CNGPT_LAST, true, true)) return -1;
+    // prompt -> token history; decode position = T
+    HIP_TRY(hipMemcpy2DAsync(h->hist, (size_t)h->capKV * sizeof(int), h->tok,
+                             (size_t)T * sizeof(int), (size_t)T * sizeof(int), B,
+                             hipMemcpyDeviceToDevice, h->stream));
+    h->pos_host = T;
+    HIP_TRY(hipMemcpyAsync(h->pos, &h->pos_host, sizeof(int), hipMemcpyHostToDevice, h->stream));
     if (logits_out)
         HIP_TRY(hipMemcpyAsync(logits_out, h->logits, (size_t)B * h->cfg.vocab_size * sizeof(float),
                                hipMemcpyDeviceToHost, h->stream));
     HIP_TRY(hipStreamSynchronize(h->stream));
+    h->kvB = B;
+    h->kvLen = T;
     return 0;
 }
 
@@ -571,11 +779,10 @@ int cngpt_hip_decode_step(cngpt_hip_ctx* h, const int* tokens, float* logits_out
         if (check_tokens(h, tokens, B)) return -1;
         HIP_TRY(hipMemcpyAsync(h->next_tok, tokens, (size_t)B * sizeof(int),
                                hipMemcpyHostToDevice, h->stream));
-    } else {
-        Timed t(h, CNGPT_K_ARGMAX, 0.0, 4.0 * B * h->cfg.vocab_size);
-        HIP_TRY(launch_argmax(h->logits, B, h->cfg.vocab_size, h->next_tok, h->stream));
+        // the caller's buffer may be reused as soon as this returns
+        HIP_TRY(hipStreamSynchronize(h->stream));
     }
-    if (enqueue_decode_step(h)) return -1;
+    if (run_decode_step(h)) return -1;
     if (logits_out) {
         HIP_TRY(hipMemcpyAsync(logits_out, h->logits, (size_t)B * h->cfg.vocab_size * sizeof(float),
                                hipMemcpyDeviceToHost, h->stream));
@@ -584,13 +791,62 @@ int cngpt_hip_decode_step(cngpt_hip_ctx* h, const int* tokens, float* logits_out
     return 0;
 }
 
+int cngpt_hip_generate(cngpt_hip_ctx* h, int n_new, float temperature, int top_k,
+                       const float* draws, int* out_tokens) {
+    if (need_params(h)) return -1;
+    if (h->kvB == 0) return fail("generate before decode_begin");
+    if (!out_tokens) return fail("null output");
+    if (n_new <= 0) return fail("n_new=%d must be positive", n_new);
+    if (h->kvLen + n_new - 1 > h->capKV)
+        return fail("%d new tokens need %d cache positions, %d held", n_new,
+                    h->kvLen + n_new - 1, h->capKV);
+    HIP_TRY(hipSetDevice(h->device));
+    const int B = h->kvB;
+    const int start = h->kvLen;
+    if (draws)
+        HIP_TRY(hipMemcpyAsync(h->draws, draws, (size_t)n_new * B * sizeof(float),
+                               hipMemcpyHostToDevice, h->stream));
+    if (draws && run_sample(h, h->draws, temperature, top_k)) return -1;
+    for (int i = 1; i < n_new; i++) {
+        if (run_decode_step(h)) return -1;
+        if (draws && run_sample(h, h->draws + (size_t)i * B, temperature, top_k)) return -1;
+    }
+    // tokens fed at positions start.. are the first n_new - 1; the last is in next_tok
+    if (n_new > 1)
+        HIP_TRY(hipMemcpy2DAsync(out_tokens, (size_t)n_new * sizeof(int), h->hist + start,
+                                 (size_t)h->capKV * sizeof(int), (size_t)(n_new - 1) * sizeof(int),
+                                 B, hipMemcpyDeviceToHost, h->stream));
+    HIP_TRY(hipMemcpy2DAsync(out_tokens + (n_new - 1), (size_t)n_new * sizeof(int), h->next_tok,
+                             sizeof(int), sizeof(int), B, hipMemcpyDeviceToHost, h->stream));
+    HIP_TRY(hipStreamSynchronize(h->stream));
+    return check_dev_err(h);
+}
+
 int cngpt_hip_argmax(cngpt_hip_ctx* h, int* out_tokens) {
     if (need_params(h)) return -1;
     if (!out_tokens) return fail("null output");
     if (!h->logits || h->curB == 0) return fail("no logits yet");
     if (h->curMode != CNGPT_LAST) return fail("argmax needs last-position logits");
     HIP_TRY(hipSetDevice(h->device));
-    HIP_TRY(launch_argmax(h->logits, h->curB, h->cfg.vocab_size, h->next_tok, h->stream));
+    HIP_TRY(launch_argmax_rows(h->logits, h->curB, h->cfg.vocab_size, h->next_tok, nullptr,
+                               h->stream));
+    HIP_TRY(hipMemcpyAsync(out_tokens, h->next_tok, (size_t)h->curB * sizeof(int),
+                           hipMemcpyDeviceToHost, h->stream));
+    HIP_TRY(hipStreamSynchronize(h->stream));
+    return 0;
+}
+
+int cngpt_hip_sample(cngpt_hip_ctx* h, float temperature, int top_k, const float* draws,
+                     int* out_tokens) {
+    if (need_params(h)) return -1;
+    if (!out_tokens || !draws) return fail("null argument");
+    if (!h->logits || h->curB == 0) return fail("no logits yet");
+    if (h->curMode != CNGPT_LAST) return fail("sample needs last-position logits");
+    HIP_TRY(hipSetDevice(h->device));
+    HIP_TRY(hipMemcpyAsync(h->draws, draws, (size_t)h->curB * sizeof(float),
+                           hipMemcpyHostToDevice, h->stream));
+    HIP_TRY(launch_sample(h->logits, h->curB, h->cfg.vocab_size, temperature, top_k, h->draws,
+                          h->prob, h->ldp, h->next_tok, h->stream));
     HIP_TRY(hipMemcpyAsync(out_tokens, h->next_tok, (size_t)h->curB * sizeof(int),
                            hipMemcpyDeviceToHost, h->stream));
     HIP_TRY(hipStreamSynchronize(h->stream));

@@ -1,0 +1,746 @@
+// decode.hip - kernels of the single-token decode step and the last-position
+// pass: products over a few rows with the LayerNorm (or the merge of the
+// split attention) folded into the input staging, split-key attention for
+// one query row, the argmax of the lm_head, and top-k sampling.
+//
+// A decode step of GPT-2 small reads ~0.5 GB of weights once; every kernel
+// here is HBM- or latency-bound. The layout rules: each output column's
+// weight row streams once with 16-byte loads; a workgroup issues its weight
+// loads before anything that depends on an earlier kernel (activation rows,
+// LayerNorm, attention partials), so the HBM latency overlaps the dependent
+// reads; the few input rows sit in LDS or L2. No kernel here waits on
+// another workgroup: results that need every workgroup (argmax over the
+// vocabulary, the merge of attention splits) are finished by the next kernel.
+#include "common.h"
+#include "kernels.h"
+
+namespace {
+
+constexpr int PRE = 8;    // float4 weight loads per lane issued up front
+constexpr int LNCH = 8;   // float4 per lane of one LayerNorm row (C <= 2048)
+constexpr int MAXS = 16;  // attention splits merged by a consumer
+
+enum Src : int { SRC_X = 0, SRC_LN = 1, SRC_MERGE = 2 };
+
+__device__ __forceinline__ float dot4(f32x4 a, f32x4 b) {
+    return (a.x * b.x + a.y * b.y) + (a.z * b.z + a.w * b.w);
+}
+
+__device__ __forceinline__ long out_row(const DecGemvArgs& a, int r, int off) {
+    long o = a.seg ? (long)(r / a.seg) * a.seg_stride + r % a.seg : r;
+    return o + off;
+}
+
+__device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
+    return v > bv || (v == bv && i < bi);
+}
+
+// Merge the attention splits of rows r < M into xs[r][C] (LDS, float4
+// view), C = H * hs. Split s of (row r, head h) holds m_s, l_s and the
+// unnormalised o_s[hs] at part + ((r*H + h) * stride + s) * (hs + 4):
+//   M = max m_s,  L = sum exp(m_s - M) l_s,  out = sum exp(m_s - M) o_s / L.
+__device__ void merge_rows(const MergeArgs& g, int M, f32x4* xs, float* wts) {
+    const int t = g.pos_dev ? *g.pos_dev : g.q_pos;
+    const int ns = (t + g.kps) / g.kps;  // splits over keys 0..t
+    const int hs = g.hs, rs = hs + 4;
+    for (int idx = threadIdx.x; idx < M * g.H; idx += blockDim.x) {
+        const float* pb = g.part + (long)idx * g.stride * rs;
+        float mx = -INFINITY;
+        for (int s = 0; s < ns; s++) mx = fmaxf(mx, pb[s * rs]);
+        float L = 0.f;
+        for (int s = 0; s < ns; s++) L += expf(pb[s * rs] - mx) * pb[s * rs + 1];
+        const float inv = 1.0f / L;
+        for (int s = 0; s < ns; s++) wts[idx * MAXS + s] = expf(pb[s * rs] - mx) * inv;
+    }
+    __syncthreads();
+    const int C4 = g.H * hs / 4, h4 = hs / 4;
+    for (int e = threadIdx.x; e < M * C4; e += blockDim.x) {
+        const int r = e / C4, c4 = e - r * C4;
+        const int h = c4 / h4, d4 = c4 - h * h4;
+        const int idx = r * g.H + h;
+        const f32x4* pb = (const f32x4*)(g.part + (long)idx * g.stride * rs) + 1 + d4;
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        for (int s = 0; s < ns; s++) acc += wts[idx * MAXS + s] * pb[s * (rs / 4)];
+        xs[e] = acc;
+    }
+    __syncthreads();
+}
+
+// Y[r, n] = epi(src(X)[r, :] . W[n, :]) for r < M <= MR.
+// WPC = 1: four columns per 256-thread workgroup, one wavefront each.
+// WPC = 4: one column per workgroup, its K range split over the four
+// wavefronts (long rows, or few columns). SRC picks the input rows:
+// X from global memory, the LayerNorm of X (K = C), or the merged attention
+// splits (K = C). With ARGMAX (EPI_STORE) each workgroup also leaves its best
+// (value, column) per row in part_v / part_i for launch_argmax_part.
+template <int EPI, int MR, int SRC, int WPC, bool ARGMAX>
+__global__ void __launch_bounds__(256) k_dgemv(DecGemvArgs a) {
+    extern __shared__ f32x4 xs[];  // staged rows [MR][K/4]
+    __shared__ float wts[(SRC == SRC_MERGE) ? MR * 32 * MAXS : 1];
+    __shared__ float red[4][MR];
+    __shared__ int redi[4][MR];
+
+    constexpr int CPW = 4 / WPC;  // columns per workgroup
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int n = blockIdx.x * CPW + (WPC == 1 ? wave : 0);
+    const bool valid = n < a.N;
+    const int nn = valid ? n : a.N - 1;
+    const int K4 = a.K >> 2;
+    const int M = a.M;
+    int cb = 0, ce = K4;
+    if (WPC == 4) {
+        const int chunk = (K4 + 3) / 4;
+        cb = min(K4, wave * chunk);
+        ce = min(K4, cb + chunk);
+    }
+    const f32x4* w4 = (const f32x4*)(a.W + (long)nn * a.K);
+
+    // 1. Weights first: they do not depend on any earlier kernel.
+    f32x4 wp[PRE];
+#pragma unroll
+    for (int i = 0; i < PRE; i++) {
+        const int c = cb + lane + 64 * i;
+        wp[i] = c < ce ? w4[c] : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    // The storing thread of row r: lane r (WPC 1) or thread r (WPC 4).
+    const int off = a.row_off + (a.row_off_dev ? *a.row_off_dev : 0);
+    const bool storer = WPC == 1 ? true : wave == 0;
+    float bv = 0.f;
+    if (EPI != EPI_STORE) bv = a.bias[nn];
+    float yo[MR];
+#pragma unroll
+    for (int r = 0; r < MR; r++) {
+        yo[r] = 0.f;
+        if (EPI == EPI_RESID && storer && r < M && lane == r)
+            yo[r] = a.Y[out_row(a, r, off) * a.ldy + nn];
+    }
+
+    // 2. Input rows.
+    if (SRC == SRC_LN) {
+        // LayerNorm (reference ops.c:191-248): mean, biased variance of
+        // (x - mean), rstd = 1/sqrtf(var + 1e-5), (x - mean) * rstd * w + b.
+        const f32x4* lw = (const f32x4*)a.ln_w;
+        const f32x4* lb = (const f32x4*)a.ln_b;
+        for (int r = wave; r < M; r += 4) {
+            const f32x4* xr = (const f32x4*)(a.X + (long)r * a.ldx);
+            f32x4 v[LNCH];
+            float s = 0.f;
+#pragma unroll
+            for (int j = 0; j < LNCH; j++) {
+                const int c = lane + 64 * j;
+                v[j] = c < K4 ? xr[c] : f32x4{0.f, 0.f, 0.f, 0.f};
+                s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
+            }
+            const float mean = wave_sum(s) / (float)a.K;
+            float q = 0.f;
+#pragma unroll
+            for (int j = 0; j < LNCH; j++) {
+                const int c = lane + 64 * j;
+                if (c < K4) {
+                    f32x4 d = v[j] - mean;
+                    q += dot4(d, d);
+                }
+            }
+            const float rstd = 1.0f / sqrtf(wave_sum(q) / (float)a.K + 1e-5f);
+#pragma unroll
+            for (int j = 0; j < LNCH; j++) {
+                const int c = lane + 64 * j;
+                if (c < K4) xs[r * K4 + c] = (v[j] - mean) * rstd * lw[c] + lb[c];
+            }
+        }
+        __syncthreads();
+    } else if (SRC == SRC_MERGE) {
+        merge_rows(a.merge, M, xs, wts);
+    }
+
+    // 3. Dot products over this wavefront's K range.
+    float acc[MR];
+#pragma unroll
+    for (int r = 0; r < MR; r++) acc[r] = 0.f;
+#pragma unroll
+    for (int i = 0; i < PRE; i++) {
+        const int c = cb + lane + 64 * i;
+        if (c < ce) {
+#pragma unroll
+            for (int r = 0; r < MR; r++)
+                if (r < M) {
+                    const f32x4 x =
+                        SRC != SRC_X ? xs[r * K4 + c] : ((const f32x4*)(a.X + (long)r * a.ldx))[c];
+                    acc[r] += dot4(wp[i], x);
+                }
+        }
+    }
+    for (int c = cb + lane + 64 * PRE; c < ce; c += 64) {
+        const f32x4 w = w4[c];
+#pragma unroll
+        for (int r = 0; r < MR; r++)
+            if (r < M) {
+                const f32x4 x =
+                    SRC != SRC_X ? xs[r * K4 + c] : ((const f32x4*)(a.X + (long)r * a.ldx))[c];
+                acc[r] += dot4(w, x);
+            }
+    }
+#pragma unroll
+    for (int r = 0; r < MR; r++) acc[r] = wave_sum(acc[r]);
+    if (WPC == 4) {
+        // Sum the four wavefronts' K ranges in a fixed order.
+        if (lane == 0)
+#pragma unroll
+            for (int r = 0; r < MR; r++) red[wave][r] = acc[r];
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < MR; r++) acc[r] = (red[0][r] + red[1][r]) + (red[2][r] + red[3][r]);
+        __syncthreads();
+    }
+
+    // 4. Epilogue: the storer of row r writes it.
+#pragma unroll
+    for (int r = 0; r < MR; r++) {
+        if (r >= M) break;
+        if (valid && storer && lane == r) {
+            float* y = a.Y + out_row(a, r, off) * a.ldy + nn;
+            float v;
+            if (EPI == EPI_STORE) v = acc[r];
+            else if (EPI == EPI_BIAS) v = acc[r] + bv;
+            else if (EPI == EPI_BIAS_GELU) v = gelu_tanh(acc[r] + bv);
+            else v = (yo[r] + acc[r]) + bv;
+            *y = v;
+        }
+    }
+    if (!ARGMAX) return;
+
+    // 5. Best column of this workgroup per row.
+    if (WPC == 1) {
+        if (lane == 0)
+#pragma unroll
+            for (int r = 0; r < MR; r++) {
+                red[wave][r] = valid ? acc[r] : -INFINITY;
+                redi[wave][r] = valid ? n : 0x7fffffff;
+            }
+        __syncthreads();
+        if (tid < M) {
+            float b = red[0][tid];
+            int bi = redi[0][tid];
+#pragma unroll
+            for (int w = 1; w < 4; w++)
+                if (better(red[w][tid], redi[w][tid], b, bi)) { b = red[w][tid]; bi = redi[w][tid]; }
+            a.part_v[(long)tid * gridDim.x + blockIdx.x] = b;
+            a.part_i[(long)tid * gridDim.x + blockIdx.x] = bi;
+        }
+    } else {
+#pragma unroll
+        for (int r = 0; r < MR; r++)
+            if (r < M && tid == r) {
+                a.part_v[(long)r * gridDim.x + blockIdx.x] = valid ? acc[r] : -INFINITY;
+                a.part_i[(long)r * gridDim.x + blockIdx.x] = valid ? n : 0x7fffffff;
+            }
+    }
+}
+
+// ---------------------------------------------------------------- attention
+
+// One query row per (sequence, head) at position t (= *pos_dev, or q_pos)
+// against keys 0..t, split over workgroups of KPB keys (grid.y). Split s
+// writes its max m, sum l and unnormalised P.V to the partials; the consumer
+// merges the splits (merge_rows). Keys past t are not visited: the
+// reference's -1e9 mask gives them probability exactly 0.
+template <int HS>
+__global__ void __launch_bounds__(256) k_attn_dec(AttnDecArgs a) {
+    constexpr int LPK = HS / 4;                 // lanes per key, one float4 each
+    constexpr int KPP = 256 / LPK;              // keys per pass of the workgroup
+    constexpr int KPB = KPP > 64 ? KPP : 64;    // keys per workgroup
+    constexpr int NPASS = KPB / KPP;
+    __shared__ float red[8];
+    __shared__ f32x4 osum[4][LPK];
+
+    const int bh = blockIdx.x, s = blockIdx.y;
+    const int b = bh / a.H, h = bh % a.H;
+    const int t = a.pos_dev ? *a.pos_dev : a.q_pos;
+    const int nk = t + 1;
+    if (s * KPB >= nk) return;
+    const long C3 = 3L * a.C;
+    const float* base = a.qkv + (long)b * a.seq_stride * C3 + h * HS;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int kl = tid / LPK, d4 = tid % LPK;
+
+    // Every global load up front: q, K and V rows of this thread's keys.
+    const f32x4 q = *(const f32x4*)(base + (long)t * C3 + d4 * 4);
+    f32x4 kr[NPASS], vr[NPASS];
+#pragma unroll
+    for (int p = 0; p < NPASS; p++) {
+        const int key = s * KPB + p * KPP + kl;
+        const bool ok = key < nk;
+        const float* rp = base + (long)(ok ? key : 0) * C3 + d4 * 4;
+        kr[p] = ok ? *(const f32x4*)(rp + a.C) : f32x4{0.f, 0.f, 0.f, 0.f};
+        vr[p] = ok ? *(const f32x4*)(rp + 2 * a.C) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+
+    // Scores: reduce the LPK partial dots of each key.
+    float sc[NPASS];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int p = 0; p < NPASS; p++) {
+        float d = dot4(q, kr[p]);
+#pragma unroll
+        for (int o = 1; o < LPK; o <<= 1) d += __shfl_xor(d, o, 64);
+        const int key = s * KPB + p * KPP + kl;
+        sc[p] = key < nk ? d * a.scale : -INFINITY;
+        mx = fmaxf(mx, sc[p]);
+    }
+    mx = wave_max(mx);
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+
+    float ls = 0.f;
+    f32x4 o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int p = 0; p < NPASS; p++) {
+        const float e = expf(sc[p] - mx);  // 0 for keys past t
+        if (d4 == 0) ls += e;
+        o += e * vr[p];
+    }
+    // Sum o over the keys of the wavefront (lanes with the same d4) ...
+#pragma unroll
+    for (int off = LPK; off < 64; off <<= 1) {
+        o.x += __shfl_xor(o.x, off, 64);
+        o.y += __shfl_xor(o.y, off, 64);
+        o.z += __shfl_xor(o.z, off, 64);
+        o.w += __shfl_xor(o.w, off, 64);
+    }
+    ls = wave_sum(ls);
+    if (lane < LPK) osum[wave][lane] = o;
+    if (lane == 0) red[4 + wave] = ls;
+    __syncthreads();
+    // ... then over the four wavefronts.
+    float* part = a.part + ((long)bh * a.max_splits + s) * (HS + 4);
+    if (tid < LPK)
+        *(f32x4*)(part + 4 + tid * 4) = (osum[0][tid] + osum[1][tid]) + (osum[2][tid] + osum[3][tid]);
+    if (tid == 0) {
+        part[0] = mx;
+        part[1] = (red[4] + red[5]) + (red[6] + red[7]);
+    }
+}
+
+// Rows of merged attention for the consumers that are not k_dgemv (M > 8).
+__global__ void __launch_bounds__(256) k_attn_merge(MergeArgs g, float* __restrict__ out, long ldo) {
+    extern __shared__ f32x4 xs[];
+    __shared__ float wts[32 * MAXS];
+    // one row per workgroup: offset the partials to row blockIdx.x
+    MergeArgs gr = g;
+    gr.part = g.part + (long)blockIdx.x * g.H * g.stride * (g.hs + 4);
+    merge_rows(gr, 1, xs, wts);
+    const int C4 = g.H * g.hs / 4;
+    f32x4* o = (f32x4*)(out + (long)blockIdx.x * ldo);
+    for (int c = threadIdx.x; c < C4; c += blockDim.x) o[c] = xs[c];
+}
+
+// ---------------------------------------------------------------- argmax
+
+// out[r] = the best of the nparts (value, column) partials of row r (first
+// column on ties); then *pos_inc += 1. One 1024-thread workgroup per row.
+__global__ void __launch_bounds__(1024) k_argmax_part(const float* __restrict__ part_v,
+                                                      const int* __restrict__ part_i, int nparts,
+                                                      int* __restrict__ out, int* pos_inc) {
+    __shared__ float sv[16];
+    __shared__ int si[16];
+    const float* pv = part_v + (long)blockIdx.x * nparts;
+    const int* pi = part_i + (long)blockIdx.x * nparts;
+    float best = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int g = threadIdx.x; g < nparts; g += 1024)
+        if (better(pv[g], pi[g], best, bi)) { best = pv[g]; bi = pi[g]; }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ob = __shfl_xor(best, o, 64);
+        const int oi = __shfl_xor(bi, o, 64);
+        if (better(ob, oi, best, bi)) { best = ob; bi = oi; }
+    }
+    const int wid = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) { sv[wid] = best; si[wid] = bi; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int k = 1; k < 16; k++)
+            if (better(sv[k], si[k], best, bi)) { best = sv[k]; bi = si[k]; }
+        out[blockIdx.x] = bi;
+        if (pos_inc && blockIdx.x == 0) *pos_inc += 1;
+    }
+}
+
+// out[r] = argmax_v logits[r, v], first index on ties. One 1024-thread
+// workgroup per row. Thread 0 of workgroup 0 then advances *pos_inc.
+__global__ void __launch_bounds__(1024) k_argmax_rows(const float* __restrict__ logits, int V,
+                                                      int* __restrict__ out, int* pos_inc) {
+    __shared__ float sv[16];
+    __shared__ int si[16];
+    const float* row = logits + (long)blockIdx.x * V;
+    float best = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int v = threadIdx.x; v < V; v += 1024) {
+        const float x = row[v];
+        if (x > best) { best = x; bi = v; }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ob = __shfl_xor(best, o, 64);
+        const int oi = __shfl_xor(bi, o, 64);
+        if (better(ob, oi, best, bi)) { best = ob; bi = oi; }
+    }
+    const int wid = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) { sv[wid] = best; si[wid] = bi; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int k = 1; k < 16; k++)
+            if (better(sv[k], si[k], best, bi)) { best = sv[k]; bi = si[k]; }
+        out[blockIdx.x] = bi;
+        if (pos_inc && blockIdx.x == 0) *pos_inc += 1;
+    }
+}
+
+// ---------------------------------------------------------------- sampling
+
+constexpr int ST = 1024;      // threads of the sampling workgroup
+constexpr int SLIST = 2048;   // survivors of the top-k cut kept in index order
+
+// Block-wide reductions over ST threads (fixed order: deterministic).
+__device__ float block_max(float v, float* sh) {
+    v = wave_max(v);
+    const int w = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) sh[w] = v;
+    __syncthreads();
+    float r = sh[0];
+    for (int i = 1; i < ST / 64; i++) r = fmaxf(r, sh[i]);
+    return r;
+}
+__device__ float block_sum(float v, float* sh) {
+    v = wave_sum(v);
+    const int w = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) sh[w] = v;
+    __syncthreads();
+    float r = 0.f;
+    for (int i = 0; i < ST / 64; i++) r += sh[i];
+    return r;
+}
+// Exclusive prefix over the threads in thread order; *total = the sum.
+template <typename TV>
+__device__ TV block_excl_scan(TV v, TV* sh, TV* total) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    TV x = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const TV y = __shfl_up(x, o, 64);
+        if (lane >= o) x += y;
+    }
+    __syncthreads();
+    if (lane == 63) sh[w] = x;
+    __syncthreads();
+    TV before = 0, all = 0;
+    for (int i = 0; i < ST / 64; i++) {
+        if (i < w) before += sh[i];
+        all += sh[i];
+    }
+    *total = all;
+    return before + (x - v);
+}
+// hist[bin] += 1 for every lane with ok set; lanes of a wavefront that share
+// a bin are counted with one LDS atomic (the high bits of nearby
+// probabilities mostly coincide).
+__device__ __forceinline__ void hist_add(int* hist, unsigned bin, bool ok) {
+    unsigned long long act = __ballot(ok);
+    while (act) {
+        const int leader = __ffsll((long long)act) - 1;
+        const unsigned lb = __shfl(bin, leader, 64);
+        const unsigned long long peers = __ballot(ok && bin == lb) & act;
+        if ((int)(threadIdx.x & 63) == leader) atomicAdd(&hist[lb], __popcll(peers));
+        act &= ~peers;
+    }
+}
+
+// One token per row from logits [rows, V], with the arithmetic of the
+// reference's sample_top_k (src/model.c:927-989): scaled = logit / temp
+// (temp <= 0 -> 1), softmax, keep the values >= the top_k-th largest
+// (ties kept), renormalise, then the first index whose running sum exceeds
+// the uniform draw r[row]; V - 1 if none does. prob [rows, ldp] is scratch
+// (ldp a multiple of 4). Thread i owns the float4 groups [i*ch4, (i+1)*ch4),
+// so thread order is index order. When at most SLIST values survive the
+// cut, the renormalising sum and the running sum are taken sequentially in
+// index order, as the reference does; otherwise (top_k off, or a huge tie
+// at the threshold) each thread sums its range and the ranges are prefixed,
+// which can differ from a sequential sum in the last bits, so the token can
+// differ only when r lies within rounding of a boundary.
+__global__ void __launch_bounds__(ST) k_sample(const float* __restrict__ logits, int V, float temp,
+                                               int top_k, const float* __restrict__ r_draw,
+                                               float* __restrict__ prob, long ldp,
+                                               int* __restrict__ out) {
+    __shared__ float shf[ST / 64];
+    __shared__ int shi[ST / 64];
+    __shared__ int hist[256];
+    __shared__ int chosen, kk_left;
+    __shared__ float lv[SLIST];
+    __shared__ int li[SLIST];
+    __shared__ int tok_sh;
+
+    const int row = blockIdx.x, tid = threadIdx.x;
+    const float* lg = logits + (long)row * V;
+    float* p = prob + (long)row * ldp;
+    f32x4* p4 = (f32x4*)p;
+    const int V4 = (V + 3) / 4;
+    const int ch4 = (V4 + ST - 1) / ST;
+    const int g0 = min(tid * ch4, V4), g1 = min(g0 + ch4, V4);
+    const float tdiv = temp > 0.0f ? temp : 1.0f;
+    auto ok = [&](int i) { return i < V; };
+
+    // scaled values (coalesced read of the logits), their max
+    float mx = -INFINITY;
+    for (int i = tid; i < V4 * 4; i += ST) {
+        const float v = ok(i) ? lg[i] / tdiv : -INFINITY;
+        p[i] = v;
+        mx = fmaxf(mx, v);
+    }
+    mx = block_max(mx, shf);
+    float s = 0.f;
+    for (int i = tid; i < V4 * 4; i += ST) {
+        const float e = ok(i) ? expf(p[i] - mx) : 0.f;
+        p[i] = e;
+        s += e;
+    }
+    const float sum = block_sum(s, shf);
+    for (int i = tid; i < V4 * 4; i += ST) p[i] = ok(i) ? p[i] / sum : 0.f;
+    __syncthreads();
+
+    // k-th largest probability (with multiplicity) by MSB-first radix
+    // select on the bit patterns (non-negative floats order as integers).
+    const bool cut = top_k > 0 && top_k < V;
+    float thr = 0.f;
+    if (cut) {
+        unsigned prefix = 0, mask = 0;
+        if (tid == 0) kk_left = top_k;
+        for (int shift = 24; shift >= 0; shift -= 8) {
+            for (int i = tid; i < 256; i += ST) hist[i] = 0;
+            __syncthreads();
+            for (int i = tid; i < V4 * 4; i += ST) {
+                const unsigned u = __float_as_uint(p[i]);
+                hist_add(hist, (u >> shift) & 255u, ok(i) && (u & mask) == prefix);
+            }
+            __syncthreads();
+            if (tid == 0) {
+                int cum = 0, kk = kk_left, d = 255;
+                for (; d > 0; d--) {
+                    if (cum + hist[d] >= kk) break;
+                    cum += hist[d];
+                }
+                chosen = d;
+                kk_left = kk - cum;
+            }
+            __syncthreads();
+            prefix |= (unsigned)chosen << shift;
+            mask |= 255u << shift;
+        }
+        thr = __uint_as_float(prefix);
+    }
+
+    // Survivors (all values when there is no cut) in index order.
+    int cnt = 0;
+    for (int g = g0; g < g1; g++) {
+        const f32x4 v = p4[g];
+        const int i = g * 4;
+        cnt += (ok(i) && (!cut || v.x >= thr)) + (ok(i + 1) && (!cut || v.y >= thr)) +
+               (ok(i + 2) && (!cut || v.z >= thr)) + (ok(i + 3) && (!cut || v.w >= thr));
+    }
+    int total;
+    const int base = block_excl_scan<int>(cnt, shi, &total);
+    const float r = r_draw[row];
+    if (cut && total <= SLIST) {
+        int k = base;
+        for (int g = g0; g < g1; g++) {
+            const f32x4 v = p4[g];
+            const float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                if (ok(g * 4 + j) && vv[j] >= thr) {
+                    lv[k] = vv[j];
+                    li[k] = g * 4 + j;
+                    k++;
+                }
+        }
+        __syncthreads();
+        if (tid == 0) {
+            float ns = 0.f;
+            for (int q = 0; q < total; q++) ns += lv[q];
+            int tok = V - 1;
+            float cdf = 0.f;
+            for (int q = 0; q < total; q++) {
+                cdf += ns > 0.0f ? lv[q] / ns : lv[q];
+                if (r < cdf) { tok = li[q]; break; }
+            }
+            out[row] = tok;
+        }
+        return;
+    }
+    // Blocked form: zero the cut values, renormalise, prefix by ranges.
+    float ps = 0.f;
+    for (int g = g0; g < g1; g++) {
+        f32x4 v = p4[g];
+        if (cut) {
+            v.x = v.x < thr ? 0.f : v.x;
+            v.y = v.y < thr ? 0.f : v.y;
+            v.z = v.z < thr ? 0.f : v.z;
+            v.w = v.w < thr ? 0.f : v.w;
+            p4[g] = v;
+        }
+        ps += ((v.x + v.y) + v.z) + v.w;
+    }
+    if (cut) {
+        const float ns = block_sum(ps, shf);
+        if (ns > 0.0f) {
+            ps = 0.f;
+            for (int g = g0; g < g1; g++) {
+                f32x4 v = p4[g];
+                v.x /= ns; v.y /= ns; v.z /= ns; v.w /= ns;
+                p4[g] = v;
+                ps += ((v.x + v.y) + v.z) + v.w;
+            }
+        }
+    }
+    float all;
+    float cdf = block_excl_scan<float>(ps, shf, &all);
+    if (tid == 0) tok_sh = V - 1;
+    __syncthreads();
+    // Every thread scans its own range from its prefix; the smallest index
+    // whose running sum exceeds r wins (robust to rounding gaps between
+    // neighbouring ranges). Zero-probability values are never chosen.
+    for (int i = g0 * 4; i < g1 * 4 && i < V; i++) {
+        const float v = p[i];
+        cdf += v;
+        if (v > 0.0f && r < cdf) { atomicMin(&tok_sh, i); break; }
+    }
+    __syncthreads();
+    if (tid == 0) out[row] = tok_sh;
+}
+
+// ---------------------------------------------------------------- launchers
+
+template <int EPI, int MR, int SRC, int WPC, bool ARGMAX>
+hipError_t dgemv_go(const DecGemvArgs& a, hipStream_t s) {
+    const size_t lds = SRC != SRC_X ? (size_t)MR * a.K * sizeof(float) : 0;
+    constexpr int CPW = 4 / WPC;
+    k_dgemv<EPI, MR, SRC, WPC, ARGMAX><<<(a.N + CPW - 1) / CPW, 256, lds, s>>>(a);
+    return hipGetLastError();
+}
+
+template <int EPI, int SRC, int WPC, bool ARGMAX>
+hipError_t dgemv_rows(const DecGemvArgs& a, hipStream_t s) {
+    if (a.M <= 1) return dgemv_go<EPI, 1, SRC, WPC, ARGMAX>(a, s);
+    if (a.M <= 2) return dgemv_go<EPI, 2, SRC, WPC, ARGMAX>(a, s);
+    if (a.M <= 4) return dgemv_go<EPI, 4, SRC, WPC, ARGMAX>(a, s);
+    return dgemv_go<EPI, 8, SRC, WPC, ARGMAX>(a, s);
+}
+
+// One wavefront per column while that gives enough workgroups and the row
+// fits the up-front loads; otherwise the four wavefronts split the row.
+template <int EPI, int SRC, bool ARGMAX>
+hipError_t dgemv_wpc(const DecGemvArgs& a, hipStream_t s) {
+    const bool split = a.N < 2048 || a.K > 4 * 64 * PRE;
+    if (split) return dgemv_rows<EPI, SRC, 4, ARGMAX>(a, s);
+    return dgemv_rows<EPI, SRC, 1, ARGMAX>(a, s);
+}
+
+template <int EPI>
+hipError_t dgemv_src(const DecGemvArgs& a, hipStream_t s) {
+    if (a.ln_w) return dgemv_wpc<EPI, SRC_LN, false>(a, s);
+    if (a.merge.part) return dgemv_wpc<EPI, SRC_MERGE, false>(a, s);
+    return dgemv_wpc<EPI, SRC_X, false>(a, s);
+}
+
+template <int HS>
+hipError_t attn_dec_hs(const AttnDecArgs& a, int B, int max_keys, hipStream_t s) {
+    constexpr int LPK = HS / 4;
+    constexpr int KPP = 256 / LPK;
+    constexpr int KPB = KPP > 64 ? KPP : 64;
+    const int splits = (max_keys + KPB - 1) / KPB;
+    if (splits > a.max_splits) return hipErrorInvalidValue;
+    dim3 grid(B * a.H, splits);
+    k_attn_dec<HS><<<grid, 256, 0, s>>>(a);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+int attn_dec_keys_per_split(int hs) {
+    const int kpp = 256 / (hs / 4);
+    return kpp > 64 ? kpp : 64;
+}
+
+hipError_t launch_dgemv(const DecGemvArgs& a, hipStream_t s) {
+    if (a.M <= 0 || a.N <= 0) return hipSuccess;
+    if (a.M > 8 || a.K <= 0 || (a.K & 3)) return hipErrorInvalidValue;
+    if (a.ln_w && (a.K > 256 * LNCH || a.merge.part)) return hipErrorInvalidValue;
+    if (a.merge.part) {
+        const MergeArgs& g = a.merge;
+        if (g.H > 32 || g.hs * g.H != a.K || (g.hs & 3) || g.stride > MAXS || g.kps <= 0)
+            return hipErrorInvalidValue;
+    }
+    if (a.argmax) {
+        if (a.epi != EPI_STORE || !a.part_v || !a.part_i || a.merge.part)
+            return hipErrorInvalidValue;
+        if (a.ln_w) return dgemv_wpc<EPI_STORE, SRC_LN, true>(a, s);
+        return dgemv_wpc<EPI_STORE, SRC_X, true>(a, s);
+    }
+    switch (a.epi) {
+        case EPI_STORE: return dgemv_src<EPI_STORE>(a, s);
+        case EPI_BIAS: return dgemv_src<EPI_BIAS>(a, s);
+        case EPI_BIAS_GELU: return dgemv_src<EPI_BIAS_GELU>(a, s);
+        case EPI_RESID: return dgemv_src<EPI_RESID>(a, s);
+    }
+    return hipErrorInvalidValue;
+}
+
+int dgemv_argmax_parts(const DecGemvArgs& a) {
+    const bool split = a.N < 2048 || a.K > 4 * 64 * PRE;
+    const int cpw = split ? 1 : 4;
+    return (a.N + cpw - 1) / cpw;
+}
+
+hipError_t launch_attention_dec(const AttnDecArgs& a, int B, int max_keys, hipStream_t s) {
+    if (B <= 0) return hipSuccess;
+    if (max_keys <= 0) return hipErrorInvalidValue;
+    switch (a.C / a.H) {
+        case 8: return attn_dec_hs<8>(a, B, max_keys, s);
+        case 16: return attn_dec_hs<16>(a, B, max_keys, s);
+        case 32: return attn_dec_hs<32>(a, B, max_keys, s);
+        case 64: return attn_dec_hs<64>(a, B, max_keys, s);
+        case 128: return attn_dec_hs<128>(a, B, max_keys, s);
+    }
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_attention_merge(const MergeArgs& g, int B, float* out, long ldo, hipStream_t s) {
+    if (B <= 0) return hipSuccess;
+    if (g.H > 32 || (g.hs & 3) || g.stride > MAXS || g.kps <= 0) return hipErrorInvalidValue;
+    k_attn_merge<<<B, 256, (size_t)g.H * g.hs * sizeof(float), s>>>(g, out, ldo);
+    return hipGetLastError();
+}
+
+hipError_t launch_argmax_part(const float* part_v, const int* part_i, int rows, int nparts,
+                              int* out, int* pos_inc, hipStream_t s) {
+    if (rows <= 0) return hipSuccess;
+    k_argmax_part<<<rows, 1024, 0, s>>>(part_v, part_i, nparts, out, pos_inc);
+    return hipGetLastError();
+}
+
+hipError_t launch_argmax_rows(const float* logits, int rows, int V, int* out, int* pos_inc,
+                              hipStream_t s) {
+    if (rows <= 0) return hipSuccess;
+    k_argmax_rows<<<rows, 1024, 0, s>>>(logits, V, out, pos_inc);
+    return hipGetLastError();
+}
+
+hipError_t launch_sample(const float* logits, int rows, int V, float temp, int top_k,
+                         const float* r_draw, float* prob, long ldp, int* out, hipStream_t s) {
+    if (rows <= 0) return hipSuccess;
+    if ((ldp & 3) || ldp < V) return hipErrorInvalidValue;
+    k_sample<<<rows, ST, 0, s>>>(logits, V, temp, top_k, r_draw, prob, ldp, out);
+    return hipGetLastError();
+}

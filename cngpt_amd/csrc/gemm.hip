@@ -15,9 +15,8 @@
 // wavefront). Ragged M and N edges (e.g. the 50257-wide vocabulary) clamp
 // loads to the last valid row and mask stores.
 //
-// k_gemv: rows M <= 8 (decode and the last-position pass). One wavefront
-// per output column: the weight row streams once with 16-byte loads and is
-// dotted with every input row, then a butterfly reduction.
+// Products over M <= 8 rows (decode, the last-position pass) are k_dgemv in
+// decode.hip.
 #include "common.h"
 #include "kernels.h"
 
@@ -155,59 +154,10 @@ __global__ void __launch_bounds__(NTHREADS, 2) k_gemm(GemmArgs a, int tiles_m, i
     }
 }
 
-// ---------------------------------------------------------------- GEMV
-
-template <int EPI, int MR>
-__global__ void __launch_bounds__(256) k_gemv(GemmArgs a) {
-    const int lane = threadIdx.x & 63;
-    const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (n >= a.N) return;
-    const int K = a.K;
-    const float* w = a.W + (long)n * K;
-    float acc[MR];
-#pragma unroll
-    for (int r = 0; r < MR; r++) acc[r] = 0.f;
-    for (int k = lane * 4; k < K; k += 256) {
-        f32x4 wv = *(const f32x4*)(w + k);
-#pragma unroll
-        for (int r = 0; r < MR; r++) {
-            if (r < a.M) {
-                f32x4 xv = *(const f32x4*)(a.X + (long)r * K + k);
-                acc[r] += (wv.x * xv.x + wv.y * xv.y) + (wv.z * xv.z + wv.w * xv.w);
-            }
-        }
-    }
-#pragma unroll
-    for (int r = 0; r < MR; r++) {
-        if (r >= a.M) break;
-        float s = wave_sum(acc[r]);
-        if (lane == 0) {
-            long orow = a.seg ? (long)(r / a.seg) * a.seg_stride + r % a.seg : r;
-            orow += a.row_off + (a.row_off_dev ? *a.row_off_dev : 0);
-            float* y = a.Y + orow * a.ldy + n;
-            *y = apply_epi<EPI>(s, a.bias, n, y);
-        }
-    }
-}
-
 template <int EPI>
 hipError_t gemm_epi(const GemmArgs& a, hipStream_t s) {
     const int tiles_m = (a.M + BM - 1) / BM, tiles_n = (a.N + BN - 1) / BN;
     k_gemm<EPI><<<tiles_m * tiles_n, NTHREADS, 0, s>>>(a, tiles_m, tiles_n);
-    return hipGetLastError();
-}
-
-template <int EPI>
-hipError_t gemv_epi(const GemmArgs& a, hipStream_t s) {
-    dim3 grid((a.N + 3) / 4), block(256);
-    if (a.M <= 1)
-        k_gemv<EPI, 1><<<grid, block, 0, s>>>(a);
-    else if (a.M <= 2)
-        k_gemv<EPI, 2><<<grid, block, 0, s>>>(a);
-    else if (a.M <= 4)
-        k_gemv<EPI, 4><<<grid, block, 0, s>>>(a);
-    else
-        k_gemv<EPI, 8><<<grid, block, 0, s>>>(a);
     return hipGetLastError();
 }
 
@@ -221,18 +171,6 @@ hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
         case EPI_BIAS: return gemm_epi<EPI_BIAS>(a, s);
         case EPI_BIAS_GELU: return gemm_epi<EPI_BIAS_GELU>(a, s);
         case EPI_RESID: return gemm_epi<EPI_RESID>(a, s);
-    }
-    return hipErrorInvalidValue;
-}
-
-hipError_t launch_gemv(const GemmArgs& a, hipStream_t s) {
-    if (a.M <= 0 || a.N <= 0) return hipSuccess;
-    if (a.M > 8 || a.K <= 0 || (a.K & 3)) return hipErrorInvalidValue;
-    switch (a.epi) {
-        case EPI_STORE: return gemv_epi<EPI_STORE>(a, s);
-        case EPI_BIAS: return gemv_epi<EPI_BIAS>(a, s);
-        case EPI_BIAS_GELU: return gemv_epi<EPI_BIAS_GELU>(a, s);
-        case EPI_RESID: return gemv_epi<EPI_RESID>(a, s);
     }
     return hipErrorInvalidValue;
 }

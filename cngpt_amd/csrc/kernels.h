@@ -6,12 +6,11 @@
 // rowops.hip
 hipError_t launch_embed(const int* tok, const float* wte, const float* wpe, float* x, long rows,
                         int T, int C, int V, int pos0, const int* pos_dev, int* err,
-                        hipStream_t s);
+                        int* hist, long hist_stride, hipStream_t s);
 hipError_t launch_layernorm(const float* x, long in_stride, const float* w, const float* b,
                             float* out, long out_stride, int rows, int C, hipStream_t s);
 hipError_t launch_gather_rows(const float* src, long src_stride, float* dst, int rows, int C,
                               hipStream_t s);
-hipError_t launch_argmax(const float* logits, int rows, int V, int* out, hipStream_t s);
 
 // gemm.hip: Y[M,N] = epi(X[M,K] . W[N,K]^T). X rows are K floats apart.
 // Output row m goes to Y + ((m / seg) * seg_stride + m % seg) * ldy, which
@@ -31,17 +30,83 @@ struct GemmArgs {
     int epi;                   // EpiMode
 };
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t s);
-// Skinny products (M <= 8 rows, decode and the last-position pass): one
-// wavefront per weight row, weights streamed once.
-hipError_t launch_gemv(const GemmArgs& a, hipStream_t s);
+
+// decode.hip
+// Partials of the split one-query attention, merged by their consumer:
+// split s of (row r, head h) at part + ((r*H + h) * stride + s) * (hs + 4)
+// holds m, l, -, -, o[hs]; the splits cover keys 0..t in runs of kps,
+// t = *pos_dev (or q_pos).
+struct MergeArgs {
+    const float* part;
+    int stride;
+    int H, hs, kps;
+    int q_pos;
+    const int* pos_dev;
+};
+
+// Products over M <= 8 rows with the same row mapping and epilogues as
+// GemmArgs. The input rows are X (row stride ldx), or the LayerNorm of X
+// (ln_w != null, K = C <= 2048), or the merged attention partials
+// (merge.part != null, K = C). argmax (EPI_STORE, not with merge): each
+// workgroup also leaves its best (value, column) per row in
+// part_v / part_i [M][dgemv_argmax_parts(a)].
+struct DecGemvArgs {
+    const float* X;
+    long ldx;
+    const float* ln_w;
+    const float* ln_b;
+    MergeArgs merge;
+    const float* W;
+    const float* bias;
+    float* Y;
+    long ldy;
+    int M, N, K;
+    int seg;
+    long seg_stride;
+    int row_off;
+    const int* row_off_dev;
+    int epi;
+    int argmax;
+    float* part_v;
+    int* part_i;
+};
+hipError_t launch_dgemv(const DecGemvArgs& a, hipStream_t s);
+int dgemv_argmax_parts(const DecGemvArgs& a);
+// out[r] = best of row r's nparts partials (first column on ties), then
+// *pos_inc += 1 when pos_inc is set.
+hipError_t launch_argmax_part(const float* part_v, const int* part_i, int rows, int nparts,
+                              int* out, int* pos_inc, hipStream_t s);
+
+// One query row per (sequence, head) against keys 0..t, t = *pos_dev (or
+// q_pos when pos_dev is null); key/value rows as for the causal kernel.
+// Keys are split over workgroups of attn_dec_keys_per_split(hs) keys; each
+// writes its partial to part (layout of MergeArgs, stride = max_splits).
+struct AttnDecArgs {
+    const float* qkv;
+    long seq_stride;
+    int C, H;
+    int q_pos;
+    const int* pos_dev;
+    float scale;
+    float* part;
+    int max_splits;
+};
+int attn_dec_keys_per_split(int hs);
+// max_keys bounds t + 1 over every launch of a captured graph (sizes the grid).
+hipError_t launch_attention_dec(const AttnDecArgs& a, int B, int max_keys, hipStream_t s);
+// Merged attention rows [B, C] (row stride ldo) from the partials.
+hipError_t launch_attention_merge(const MergeArgs& g, int B, float* out, long ldo, hipStream_t s);
+// out[r] = argmax of logits row r (first index on ties); then *pos_inc += 1.
+hipError_t launch_argmax_rows(const float* logits, int rows, int V, int* out, int* pos_inc,
+                              hipStream_t s);
+// One token per row with the reference's sample_top_k arithmetic, the
+// uniform draw of row r in r_draw[r]; prob [rows, ldp] is scratch
+// (ldp >= V, a multiple of 4).
+hipError_t launch_sample(const float* logits, int rows, int V, float temp, int top_k,
+                         const float* r_draw, float* prob, long ldp, int* out, hipStream_t s);
 
 // attention.hip
 // qkv rows hold [q | k | v] (3C floats); sequence b's row t sits at
 // qkv + (b * seq_stride + t) * 3C. out row (b*T + t) gets the merged heads.
 hipError_t launch_attention_causal(const float* qkv, long seq_stride, float* out, int B, int T,
                                    int C, int H, hipStream_t s);
-// One query row per (sequence, head): query at position q_pos (or *pos_dev)
-// against keys 0..q_pos. out row b gets the merged heads. max_keys bounds
-// q_pos + 1 (it sizes the score buffer in LDS).
-hipError_t launch_attention_row(const float* qkv, long seq_stride, float* out, int B, int q_pos,
-                                const int* pos_dev, int max_keys, int C, int H, hipStream_t s);

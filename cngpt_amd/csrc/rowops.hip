@@ -1,5 +1,5 @@
 // rowops.hip - bandwidth-bound row kernels: token+position embedding,
-// LayerNorm, row gather and greedy argmax.
+// LayerNorm and row gather.
 //
 // All are HBM-bound. Each row of C floats is owned by one wavefront and
 // moved with 16-byte loads; reductions stay inside the wavefront (butterfly
@@ -10,12 +10,14 @@
 // x[i, :] = wte[tok[i], :] + wpe[pos0 + i % T, :]   (reference fast.c:245-254)
 // One thread per float4. pos0 comes from *pos_dev when pos_dev is set, so a
 // captured decode step can advance the position on the device. Token ids
-// outside [0, V) are clamped and reported through *err.
+// outside [0, V) are clamped and reported through *err. With hist set, the
+// token of row i is also recorded at hist[i * hist_stride + position].
 __global__ void __launch_bounds__(256) k_embed(const int* __restrict__ tok,
                                                const float* __restrict__ wte,
                                                const float* __restrict__ wpe, float* __restrict__ x,
                                                long rows, int T, int C, int V, int pos0,
-                                               const int* __restrict__ pos_dev, int* __restrict__ err) {
+                                               const int* __restrict__ pos_dev, int* __restrict__ err,
+                                               int* __restrict__ hist, long hist_stride) {
     const int c4 = C >> 2;
     long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= rows * c4) return;
@@ -27,6 +29,7 @@ __global__ void __launch_bounds__(256) k_embed(const int* __restrict__ tok,
         if (err) atomicOr(err, 1);
         id = id < 0 ? 0 : V - 1;
     }
+    if (hist && c == 0) hist[r * hist_stride + t] = tok[r];
     f32x4 a = *(const f32x4*)(wte + (long)id * C + c);
     f32x4 b = *(const f32x4*)(wpe + (long)t * C + c);
     *(f32x4*)(x + r * C + c) = a + b;
@@ -93,43 +96,15 @@ __global__ void __launch_bounds__(256) k_gather_rows(const float* __restrict__ s
     *(f32x4*)(dst + (long)r * C + c) = *(const f32x4*)(src + (long)r * src_stride + c);
 }
 
-// out[b] = argmax_v logits[b, v] (first index on ties). One block per row.
-__global__ void __launch_bounds__(256) k_argmax(const float* __restrict__ logits, int V,
-                                                int* __restrict__ out) {
-    __shared__ float sv[4];
-    __shared__ int si[4];
-    const float* row = logits + (long)blockIdx.x * V;
-    float best = -INFINITY;
-    int bi = 0x7fffffff;
-    for (int v = threadIdx.x; v < V; v += blockDim.x) {
-        float x = row[v];
-        if (x > best) { best = x; bi = v; }
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        float ob = __shfl_xor(best, o, 64);
-        int oi = __shfl_xor(bi, o, 64);
-        if (ob > best || (ob == best && oi < bi)) { best = ob; bi = oi; }
-    }
-    const int wid = threadIdx.x >> 6;
-    if ((threadIdx.x & 63) == 0) { sv[wid] = best; si[wid] = bi; }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        for (int k = 1; k < 4; k++)
-            if (sv[k] > best || (sv[k] == best && si[k] < bi)) { best = sv[k]; bi = si[k]; }
-        out[blockIdx.x] = bi;
-    }
-}
-
 // ---------------------------------------------------------------- launchers
 
 hipError_t launch_embed(const int* tok, const float* wte, const float* wpe, float* x, long rows,
                         int T, int C, int V, int pos0, const int* pos_dev, int* err,
-                        hipStream_t s) {
+                        int* hist, long hist_stride, hipStream_t s) {
     long n = rows * (C / 4);
     if (n == 0) return hipSuccess;
     k_embed<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(tok, wte, wpe, x, rows, T, C, V, pos0,
-                                                         pos_dev, err);
+                                                         pos_dev, err, hist, hist_stride);
     return hipGetLastError();
 }
 
@@ -158,11 +133,5 @@ hipError_t launch_gather_rows(const float* src, long src_stride, float* dst, int
     long n = (long)rows * (C / 4);
     if (n == 0) return hipSuccess;
     k_gather_rows<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(src, src_stride, dst, rows, C);
-    return hipGetLastError();
-}
-
-hipError_t launch_argmax(const float* logits, int rows, int V, int* out, hipStream_t s) {
-    if (rows == 0) return hipSuccess;
-    k_argmax<<<rows, 256, 0, s>>>(logits, V, out);
     return hipGetLastError();
 }

@@ -47,7 +47,8 @@ enum {
     CNGPT_K_EMBED = 5,
     CNGPT_K_GATHER = 6,
     CNGPT_K_ARGMAX = 7,
-    CNGPT_K_COUNT = 8
+    CNGPT_K_SAMPLE = 8,      /* top-k sampling */
+    CNGPT_K_COUNT = 9
 };
 
 /* Last error message of the calling thread ("" if none). */
@@ -98,15 +99,33 @@ const float *cngpt_hip_logits_device(cngpt_hip_ctx *h);
  * gpt_sample, src/model.c:991-1016, recomputes the whole prefix).
  * decode_begin runs the prompt [B, T] through the forward, keeps every
  * layer's K and V for up to `capacity` positions per sequence
- * (T < capacity <= block_size) and leaves the last-position logits [B, V]
- * in logits_out (may be NULL). decode_step appends one token per sequence
- * (tokens [B] from the host, or the device argmax of the previous logits
- * when tokens is NULL) and produces the next [B, V] logits. */
+ * (T < capacity <= block_size), leaves the last-position logits [B, V]
+ * in logits_out (may be NULL) and their greedy tokens on the device.
+ * decode_step appends one token per sequence (tokens [B] from the host, or,
+ * when tokens is NULL, the token the device selected from the previous
+ * logits: their argmax, or the sampled token after cngpt_hip_generate with
+ * draws) and produces the next [B, V] logits. The step runs as one
+ * replayed HIP graph. */
 int  cngpt_hip_decode_begin(cngpt_hip_ctx *h, const int *prompt, int B, int T, int capacity,
                             float *logits_out);
 int  cngpt_hip_decode_step(cngpt_hip_ctx *h, const int *tokens, float *logits_out);
+/* n_new tokens per sequence after decode_begin (the loop of gpt_sample,
+ * src/model.c:991-1016, with the KV cache): token 0 is selected from the
+ * current logits, each further token from the logits of one more decode
+ * step fed the previous token. draws == NULL: greedy (argmax, first index on
+ * ties). Otherwise draws[i * B + b] is the uniform draw in [0, 1) for token
+ * i of sequence b, and tokens are selected with the arithmetic of
+ * sample_top_k (src/model.c:927-989; temperature <= 0 means 1, top_k <= 0 or
+ * >= vocab_size means no cut). out_tokens is [B, n_new]. Needs
+ * decode_length() + n_new - 1 <= capacity. */
+int  cngpt_hip_generate(cngpt_hip_ctx *h, int n_new, float temperature, int top_k,
+                        const float *draws, int *out_tokens);
 /* Greedy token per sequence from the current logits (first index on ties). */
 int  cngpt_hip_argmax(cngpt_hip_ctx *h, int *out_tokens);
+/* One token per sequence from the current logits by sample_top_k's
+ * arithmetic (src/model.c:927-989), draws [B] uniform in [0, 1). */
+int  cngpt_hip_sample(cngpt_hip_ctx *h, float temperature, int top_k, const float *draws,
+                      int *out_tokens);
 /* Positions held in the KV cache per sequence (prompt + steps). */
 int  cngpt_hip_decode_length(cngpt_hip_ctx *h);
 

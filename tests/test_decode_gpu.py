@@ -76,3 +76,135 @@ def test_teacher_forced_decode_tiny_and_capacity():
             m.decode_step(seq[:, 0])
         with pytest.raises(cngpt_amd.CngptError, match="capacity"):
             m.decode_begin(seq[:, :4], capacity=cfg.block_size + 1)
+
+
+# ---------------------------------------------------------------- generate / sampling
+
+def cdf_gap(logits, temp, top_k, r):
+    """Distance from r to the nearest boundary of the sampling CDF that
+    sample_top_k (src/model.c:927-989) builds from these logits (float64)."""
+    x = logits.astype(np.float64) / (temp if temp > 0 else 1.0)
+    p = np.exp(x - x.max())
+    p /= p.sum()
+    if 0 < top_k < p.size:
+        thr = np.sort(p)[-top_k]
+        p = np.where(p < thr, 0.0, p)
+        p /= p.sum()
+    c = np.cumsum(p)
+    return float(np.abs(c - r).min())
+
+
+def test_generate_greedy_matches_stepwise_and_oracle():
+    cfg = cngpt_amd.Config(2, 4, 256, 1000, 128)
+    params = randomize(cfg, cngpt_amd.init_weights(cfg, 5), 6)
+    prompt = np.random.default_rng(11).integers(0, cfg.vocab_size, size=(3, 17), dtype=np.int32)
+    n = 40
+    with cngpt_amd.Model(cfg, params) as m:
+        first = m.decode_begin(prompt, capacity=17 + n - 1)
+        gen = m.generate(n)
+        assert gen.shape == (3, n)
+        assert m.decode_length() == 17 + n - 1
+        m.decode_begin(prompt, capacity=17 + n - 1)
+        toks = [first.argmax(-1).astype(np.int32)]
+        for _ in range(n - 1):
+            toks.append(m.decode_step(toks[-1]).argmax(-1).astype(np.int32))
+    assert np.array_equal(gen, np.stack(toks, 1))
+    seq = np.concatenate([prompt, gen[:, :-1]], axis=1)
+    ref = oracle.forward(ocfg(cfg), params, seq, oracle.ALL)[:, 16:]
+    srt = np.sort(ref, axis=-1)
+    tie = (srt[..., -1] - srt[..., -2]) < 1e-4
+    assert np.array_equal(np.where(tie, 0, ref.argmax(-1)), np.where(tie, 0, gen))
+    say("generate greedy B=3 n=40")
+
+
+def test_decode_more_than_eight_sequences():
+    """B > 8 takes the MFMA tile products and the row argmax kernel."""
+    cfg = cngpt_amd.Config(2, 4, 256, 1000, 128)
+    params = randomize(cfg, cngpt_amd.init_weights(cfg, 8), 9)
+    prompt = np.random.default_rng(12).integers(0, cfg.vocab_size, size=(12, 9), dtype=np.int32)
+    with cngpt_amd.Model(cfg, params) as m:
+        logits = [m.decode_begin(prompt, capacity=40)]
+        toks = [logits[0].argmax(-1).astype(np.int32)]
+        for _ in range(20):
+            logits.append(m.decode_step(toks[-1]))
+            toks.append(logits[-1].argmax(-1).astype(np.int32))
+        m.decode_begin(prompt, capacity=40)
+        gen = m.generate(21)
+    assert np.array_equal(gen, np.stack(toks, 1))
+    seq = np.concatenate([prompt, np.stack(toks[:-1], 1)], axis=1)
+    ref = oracle.forward(ocfg(cfg), params, seq, oracle.ALL)[:, 8:]
+    say("decode B=12")
+    compare(np.stack(logits, 1), ref, what="B=12 decode")
+
+
+SAMPLE_CASES = [(0.8, 40), (1.0, 40), (0.0, 40), (1.0, 1), (1.3, 0), (0.7, 50257),
+                (1.0, 5000)]
+
+
+def test_device_sampling_matches_oracle():
+    """cngpt_hip_sample vs the oracle's sample_top_k on the same logits and
+    draws; a token may differ only when the draw sits within rounding of a
+    CDF boundary. (1.0, 5000) keeps more than 2048 values and takes the
+    blocked running-sum path; top_k 0 / >= V means no cut."""
+    cfg = cngpt_amd.Config(1, 4, 256, 50257, 64)
+    params = cngpt_amd.init_weights(cfg, 21)
+    w = oracle.unpack(ocfg(cfg), params)
+    w["wte"][:] *= 40.0          # logits with a realistic spread (sd ~ 3)
+    prompt = np.tile(oracle.lcg_tokens(20, cfg.vocab_size, seed=3), (8, 1))
+    rng = np.random.default_rng(4)
+    with cngpt_amd.Model(cfg, params) as m:
+        logits = m.decode_begin(prompt, capacity=32)
+        row = logits[0]
+        assert np.array_equal(logits, np.tile(row, (8, 1)))
+        checked = skipped = 0
+        for temp, k in SAMPLE_CASES:
+            draws = rng.random(48).astype(np.float32)
+            draws[:3] = [0.0, 0.5, np.float32(0.99999994)]
+            for i in range(0, draws.size, 8):
+                got = m.sample(8, temp, k, draws[i:i + 8])
+                for r, g in zip(draws[i:i + 8], got):
+                    ref = oracle.sample_top_k(row, temp, k, float(r))
+                    if g != ref:
+                        assert cdf_gap(row, temp, k, float(r)) < 1e-5, (temp, k, r, g, ref)
+                        skipped += 1
+                    checked += 1
+        say(f"sampling: {checked} draws, {skipped} at a boundary")
+        assert skipped <= 2
+        # all-equal logits: every value ties at the threshold
+        flat = np.zeros((8, 20), np.int32)
+        params2 = params.copy()
+        oracle.unpack(ocfg(cfg), params2)["wte"][:] = 0.0
+        m.load_params(params2)
+        row2 = m.decode_begin(flat, capacity=32)[0]
+        assert np.all(row2 == row2[0])
+        draws = np.array([0.0, 0.1, 0.25, 0.5, 0.75, 0.9, 0.999, 0.3333], np.float32)
+        got = m.sample(8, 1.0, 40, draws)
+        for r, g in zip(draws, got):
+            ref = oracle.sample_top_k(row2, 1.0, 40, float(r))
+            assert g == ref or cdf_gap(row2, 1.0, 40, float(r)) < 1e-5, (r, g, ref)
+
+
+def test_generate_sampling_gpt2_small_rand_stream():
+    """The sampling loop of gpt_sample (src/model.c:991-1016) with the KV
+    cache: draws from the reference's rand() stream after srand(7), temp 0.8,
+    top-k 40. Each token is checked against sample_top_k over the oracle's
+    logits of the sequence generated so far."""
+    cfg = cngpt_amd.GPT2_SMALL
+    params = cngpt_amd.init_weights(cfg, 1234)
+    prompt = oracle.lcg_tokens(32, cfg.vocab_size).reshape(1, 32)
+    n = 48
+    oracle.srand(7)
+    draws = np.array([oracle.rand_uniform() for _ in range(n)], np.float32)
+    with cngpt_amd.Model(cfg, params) as m:
+        m.decode_begin(prompt, capacity=32 + n - 1)
+        gen = m.generate(n, 0.8, 40, draws)[0]
+    seq = np.concatenate([prompt[0], gen[:-1]]).reshape(1, -1)
+    ref = oracle.forward(ocfg(cfg), params, seq, oracle.ALL)[0, 31:]
+    for i in range(n):
+        want = oracle.sample_top_k(ref[i], 0.8, 40, float(draws[i]))
+        if want != gen[i]:
+            # the device logits differ from the oracle's by <= 1e-3
+            assert cdf_gap(ref[i], 0.8, 40, float(draws[i])) < 1e-3, (i, gen[i], want)
+            say(f"  diverged at a CDF boundary at token {i}")
+            break
+    say(f"generate sampled small: {n} tokens")
