@@ -222,8 +222,11 @@ int run_ln_gemm(cngpt_hip_ctx* h, const float* x, const float* lw, const float* 
 int run_lm_head(cngpt_hip_ctx* h, const float* x, int M, bool want_tok, int* pos_inc) {
     const int C = h->cfg.n_embd, V = h->cfg.vocab_size;
     if (M <= SKINNY) {
+        // The final LayerNorm runs once on its own: recomputing it in each of
+        // the ~V/4 workgroups of the product costs more than the launch.
+        if (run_ln(h, x, C, h->lnf_w, h->lnf_b, h->lnc, M)) return -1;
         DecGemvArgs d{};
-        d.X = x; d.ldx = C; d.ln_w = h->lnf_w; d.ln_b = h->lnf_b; d.W = h->wte;
+        d.X = h->lnc; d.ldx = C; d.W = h->wte;
         d.Y = h->logits; d.ldy = V;
         d.M = M; d.N = V; d.K = C;
         d.epi = EPI_STORE;
@@ -469,7 +472,8 @@ int enqueue_decode_step(cngpt_hip_ctx* h) {
     const int C = c.n_embd, L = c.n_layer;
     const int B = h->kvB;
     const long cap = h->capKV;
-    {
+    const bool fused_embed = B <= SKINNY;
+    if (!fused_embed) {
         Timed t(h, CNGPT_K_EMBED, 0.0, 12.0 * C * B);
         HIP_TRY(launch_embed(h->next_tok, h->wte, h->wpe, h->xc, B, 1, C, c.vocab_size, 0, h->pos,
                              h->dev_err, h->hist, cap, h->stream));
@@ -477,9 +481,24 @@ int enqueue_decode_step(cngpt_hip_ctx* h) {
     for (int l = 0; l < L; l++) {
         const LayerW& w = h->layers[l];
         float* kvl = h->qkv + (size_t)l * B * cap * 3 * C;
-        if (run_ln_gemm(h, h->xc, w.ln1_w, w.ln1_b, h->lnc, w.attn_w, w.attn_b, kvl, B, 3 * C,
-                        EPI_BIAS, 1, cap, 3L * C, h->pos))
+        if (l == 0 && fused_embed) {
+            // x = wte[token] + wpe[pos] is built inside layer 0's QKV product
+            DecGemvArgs d{};
+            d.ln_w = w.ln1_w; d.ln_b = w.ln1_b;
+            d.emb.tok = h->next_tok; d.emb.wte = h->wte; d.emb.wpe = h->wpe;
+            d.emb.pos_dev = h->pos; d.emb.x_out = h->xc; d.emb.hist = h->hist;
+            d.emb.hist_stride = cap; d.emb.V = c.vocab_size; d.emb.err = h->dev_err;
+            d.W = w.attn_w; d.bias = w.attn_b; d.Y = kvl; d.ldy = 3L * C;
+            d.M = B; d.N = 3 * C; d.K = C;
+            d.seg = 1; d.seg_stride = cap; d.row_off_dev = h->pos;
+            d.epi = EPI_BIAS;
+            Timed t(h, CNGPT_K_GEMV, 2.0 * B * 3 * C * C,
+                    4.0 * (3.0 * C * C + 3.0 * B * C + 2.0 * B * C));
+            HIP_TRY(launch_dgemv(d, h->stream));
+        } else if (run_ln_gemm(h, h->xc, w.ln1_w, w.ln1_b, h->lnc, w.attn_w, w.attn_b, kvl, B,
+                               3 * C, EPI_BIAS, 1, cap, 3L * C, h->pos)) {
             return -1;
+        }
         if (run_attn_row_proj(h, kvl, cap, B, 0, h->pos, (int)cap, w, h->xc)) return -1;
         if (run_ln_gemm(h, h->xc, w.ln2_w, w.ln2_b, h->lnc, w.fc_w, w.fc_b, h->hidc, B, 4 * C,
                         EPI_BIAS_GELU))

@@ -20,7 +20,7 @@ constexpr int PRE = 8;    // float4 weight loads per lane issued up front
 constexpr int LNCH = 8;   // float4 per lane of one LayerNorm row (C <= 2048)
 constexpr int MAXS = 16;  // attention splits merged by a consumer
 
-enum Src : int { SRC_X = 0, SRC_LN = 1, SRC_MERGE = 2 };
+enum Src : int { SRC_X = 0, SRC_LN = 1, SRC_MERGE = 2, SRC_EMBED = 3 };
 
 __device__ __forceinline__ float dot4(f32x4 a, f32x4 b) {
     return (a.x * b.x + a.y * b.y) + (a.z * b.z + a.w * b.w);
@@ -38,32 +38,63 @@ __device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
 // Merge the attention splits of rows r < M into xs[r][C] (LDS, float4
 // view), C = H * hs. Split s of (row r, head h) holds m_s, l_s and the
 // unnormalised o_s[hs] at part + ((r*H + h) * stride + s) * (hs + 4):
-//   M = max m_s,  L = sum exp(m_s - M) l_s,  out = sum exp(m_s - M) o_s / L.
-__device__ void merge_rows(const MergeArgs& g, int M, f32x4* xs, float* wts) {
+//   M = max m_s,  L = sum exp(m_s - M) l_s,  out = sum exp(m_s - M) o_s / L,
+// accumulated online so every split's loads are issued together.
+__device__ void merge_rows(const MergeArgs& g, int M, f32x4* xs) {
     const int t = g.pos_dev ? *g.pos_dev : g.q_pos;
     const int ns = (t + g.kps) / g.kps;  // splits over keys 0..t
-    const int hs = g.hs, rs = hs + 4;
-    for (int idx = threadIdx.x; idx < M * g.H; idx += blockDim.x) {
-        const float* pb = g.part + (long)idx * g.stride * rs;
-        float mx = -INFINITY;
-        for (int s = 0; s < ns; s++) mx = fmaxf(mx, pb[s * rs]);
-        float L = 0.f;
-        for (int s = 0; s < ns; s++) L += expf(pb[s * rs] - mx) * pb[s * rs + 1];
-        const float inv = 1.0f / L;
-        for (int s = 0; s < ns; s++) wts[idx * MAXS + s] = expf(pb[s * rs] - mx) * inv;
-    }
-    __syncthreads();
-    const int C4 = g.H * hs / 4, h4 = hs / 4;
+    const int rs = g.hs + 4, h4 = g.hs / 4;
+    const int C4 = g.H * h4;
     for (int e = threadIdx.x; e < M * C4; e += blockDim.x) {
         const int r = e / C4, c4 = e - r * C4;
         const int h = c4 / h4, d4 = c4 - h * h4;
-        const int idx = r * g.H + h;
-        const f32x4* pb = (const f32x4*)(g.part + (long)idx * g.stride * rs) + 1 + d4;
+        const float* pb = g.part + (long)(r * g.H + h) * g.stride * rs;
+        float mx = -INFINITY, L = 0.f;
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        for (int s = 0; s < ns; s++) acc += wts[idx * MAXS + s] * pb[s * (rs / 4)];
-        xs[e] = acc;
+#pragma unroll
+        for (int s = 0; s < MAXS; s++) {
+            if (s < ns) {
+                const float ms = pb[s * rs], ls = pb[s * rs + 1];
+                const f32x4 os = *(const f32x4*)(pb + s * rs + 4 + 4 * d4);
+                const float mn = fmaxf(mx, ms);
+                const float a = expf(mx - mn), b = expf(ms - mn);
+                acc = acc * a + os * b;
+                L = L * a + ls * b;
+                mx = mn;
+            }
+        }
+        xs[e] = acc * (1.0f / L);
     }
     __syncthreads();
+}
+
+// x rows of a decode step, built in the first product of layer 0:
+// x[r] = wte[tok[r]] + wpe[*pos_dev] (reference fast.c:245-254). Workgroup 0
+// also stores them (the residual stream) and records the token in hist.
+template <int NCH>
+__device__ __forceinline__ void embed_row(const EmbedArgs& e, int r, int K4, int lane, f32x4* v) {
+    int id = e.tok[r];
+    if (id < 0 || id >= e.V) {
+        if (lane == 0 && e.err) atomicOr(e.err, 1);
+        id = id < 0 ? 0 : e.V - 1;
+    }
+    const int pos = *e.pos_dev;
+    const f32x4* wr = (const f32x4*)(e.wte + (long)id * K4 * 4);
+    const f32x4* pr = (const f32x4*)(e.wpe + (long)pos * K4 * 4);
+#pragma unroll
+    for (int j = 0; j < NCH; j++) {
+        const int c = lane + 64 * j;
+        v[j] = c < K4 ? wr[c] + pr[c] : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    if (blockIdx.x == 0) {
+        f32x4* xo = (f32x4*)(e.x_out + (long)r * K4 * 4);
+#pragma unroll
+        for (int j = 0; j < NCH; j++) {
+            const int c = lane + 64 * j;
+            if (c < K4) xo[c] = v[j];
+        }
+        if (lane == 0 && e.hist) e.hist[(long)r * e.hist_stride + pos] = e.tok[r];
+    }
 }
 
 // Y[r, n] = epi(src(X)[r, :] . W[n, :]) for r < M <= MR.
@@ -76,7 +107,6 @@ __device__ void merge_rows(const MergeArgs& g, int M, f32x4* xs, float* wts) {
 template <int EPI, int MR, int SRC, int WPC, bool ARGMAX>
 __global__ void __launch_bounds__(256) k_dgemv(DecGemvArgs a) {
     extern __shared__ f32x4 xs[];  // staged rows [MR][K/4]
-    __shared__ float wts[(SRC == SRC_MERGE) ? MR * 32 * MAXS : 1];
     __shared__ float red[4][MR];
     __shared__ int redi[4][MR];
 
@@ -116,21 +146,26 @@ __global__ void __launch_bounds__(256) k_dgemv(DecGemvArgs a) {
     }
 
     // 2. Input rows.
-    if (SRC == SRC_LN) {
+    if (SRC == SRC_LN || SRC == SRC_EMBED) {
         // LayerNorm (reference ops.c:191-248): mean, biased variance of
         // (x - mean), rstd = 1/sqrtf(var + 1e-5), (x - mean) * rstd * w + b.
         const f32x4* lw = (const f32x4*)a.ln_w;
         const f32x4* lb = (const f32x4*)a.ln_b;
         for (int r = wave; r < M; r += 4) {
-            const f32x4* xr = (const f32x4*)(a.X + (long)r * a.ldx);
             f32x4 v[LNCH];
+            if (SRC == SRC_EMBED) {
+                embed_row<LNCH>(a.emb, r, K4, lane, v);
+            } else {
+                const f32x4* xr = (const f32x4*)(a.X + (long)r * a.ldx);
+#pragma unroll
+                for (int j = 0; j < LNCH; j++) {
+                    const int c = lane + 64 * j;
+                    v[j] = c < K4 ? xr[c] : f32x4{0.f, 0.f, 0.f, 0.f};
+                }
+            }
             float s = 0.f;
 #pragma unroll
-            for (int j = 0; j < LNCH; j++) {
-                const int c = lane + 64 * j;
-                v[j] = c < K4 ? xr[c] : f32x4{0.f, 0.f, 0.f, 0.f};
-                s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
-            }
+            for (int j = 0; j < LNCH; j++) s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
             const float mean = wave_sum(s) / (float)a.K;
             float q = 0.f;
 #pragma unroll
@@ -150,7 +185,7 @@ __global__ void __launch_bounds__(256) k_dgemv(DecGemvArgs a) {
         }
         __syncthreads();
     } else if (SRC == SRC_MERGE) {
-        merge_rows(a.merge, M, xs, wts);
+        merge_rows(a.merge, M, xs);
     }
 
     // 3. Dot products over this wavefront's K range.
@@ -325,11 +360,10 @@ __global__ void __launch_bounds__(256) k_attn_dec(AttnDecArgs a) {
 // Rows of merged attention for the consumers that are not k_dgemv (M > 8).
 __global__ void __launch_bounds__(256) k_attn_merge(MergeArgs g, float* __restrict__ out, long ldo) {
     extern __shared__ f32x4 xs[];
-    __shared__ float wts[32 * MAXS];
     // one row per workgroup: offset the partials to row blockIdx.x
     MergeArgs gr = g;
     gr.part = g.part + (long)blockIdx.x * g.H * g.stride * (g.hs + 4);
-    merge_rows(gr, 1, xs, wts);
+    merge_rows(gr, 1, xs);
     const int C4 = g.H * g.hs / 4;
     f32x4* o = (f32x4*)(out + (long)blockIdx.x * ldo);
     for (int c = threadIdx.x; c < C4; c += blockDim.x) o[c] = xs[c];
@@ -649,6 +683,7 @@ hipError_t dgemv_wpc(const DecGemvArgs& a, hipStream_t s) {
 
 template <int EPI>
 hipError_t dgemv_src(const DecGemvArgs& a, hipStream_t s) {
+    if (a.ln_w && a.emb.tok) return dgemv_wpc<EPI, SRC_EMBED, false>(a, s);
     if (a.ln_w) return dgemv_wpc<EPI, SRC_LN, false>(a, s);
     if (a.merge.part) return dgemv_wpc<EPI, SRC_MERGE, false>(a, s);
     return dgemv_wpc<EPI, SRC_X, false>(a, s);
@@ -677,13 +712,15 @@ hipError_t launch_dgemv(const DecGemvArgs& a, hipStream_t s) {
     if (a.M <= 0 || a.N <= 0) return hipSuccess;
     if (a.M > 8 || a.K <= 0 || (a.K & 3)) return hipErrorInvalidValue;
     if (a.ln_w && (a.K > 256 * LNCH || a.merge.part)) return hipErrorInvalidValue;
+    if (a.emb.tok && (!a.ln_w || !a.emb.wte || !a.emb.wpe || !a.emb.pos_dev || !a.emb.x_out))
+        return hipErrorInvalidValue;
     if (a.merge.part) {
         const MergeArgs& g = a.merge;
         if (g.H > 32 || g.hs * g.H != a.K || (g.hs & 3) || g.stride > MAXS || g.kps <= 0)
             return hipErrorInvalidValue;
     }
     if (a.argmax) {
-        if (a.epi != EPI_STORE || !a.part_v || !a.part_i || a.merge.part)
+        if (a.epi != EPI_STORE || !a.part_v || !a.part_i || a.merge.part || a.emb.tok)
             return hipErrorInvalidValue;
         if (a.ln_w) return dgemv_wpc<EPI_STORE, SRC_LN, true>(a, s);
         return dgemv_wpc<EPI_STORE, SRC_X, true>(a, s);

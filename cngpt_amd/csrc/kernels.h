@@ -44,10 +44,27 @@ struct MergeArgs {
     const int* pos_dev;
 };
 
+// Token + position embedding of a decode step built inside the first
+// product: x[r] = wte[tok[r]] + wpe[*pos_dev] (ids outside [0, V) clamped
+// and flagged in *err); workgroup 0 stores x to x_out and the token to
+// hist[r * hist_stride + *pos_dev] (hist may be null).
+struct EmbedArgs {
+    const int* tok;
+    const float* wte;
+    const float* wpe;
+    const int* pos_dev;
+    float* x_out;
+    int* hist;
+    long hist_stride;
+    int V;
+    int* err;
+};
+
 // Products over M <= 8 rows with the same row mapping and epilogues as
 // GemmArgs. The input rows are X (row stride ldx), or the LayerNorm of X
-// (ln_w != null, K = C <= 2048), or the merged attention partials
-// (merge.part != null, K = C). argmax (EPI_STORE, not with merge): each
+// (ln_w != null, K = C <= 2048; with emb.tok set, X is the embedding of
+// emb), or the merged attention partials (merge.part != null, K = C).
+// argmax (EPI_STORE, X or LayerNorm input only): each
 // workgroup also leaves its best (value, column) per row in
 // part_v / part_i [M][dgemv_argmax_parts(a)].
 struct DecGemvArgs {
@@ -55,6 +72,7 @@ struct DecGemvArgs {
     long ldx;
     const float* ln_w;
     const float* ln_b;
+    EmbedArgs emb;
     MergeArgs merge;
     const float* W;
     const float* bias;
