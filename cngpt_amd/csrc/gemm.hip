@@ -15,6 +15,7 @@
 // wavefront). Ragged M and N edges (e.g. the 50257-wide vocabulary) clamp
 // loads to the last valid row and mask stores.
 //
+// k_skinny: 8 < M <= 64 rows, 16-column tiles, K split over 8 wavefronts.
 // Products over M <= 8 rows (decode, the last-position pass) are k_dgemv in
 // decode.hip.
 #include "common.h"
@@ -154,6 +155,89 @@ __global__ void __launch_bounds__(NTHREADS, 2) k_gemm(GemmArgs a, int tiles_m, i
     }
 }
 
+// ---------------------------------------------------------------- skinny
+
+// k_skinny: 8 < M <= 64 rows (batched decode, last-position passes of
+// larger batches, short prefills). Weight-bandwidth bound: each workgroup
+// owns 16 output columns and streams those 16 weight rows once; its NW
+// wavefronts split K, each keeping D k-steps of 16 in flight (one 16-byte
+// weight load and MB 16-byte input loads per lane per step), and multiply
+// with v_mfma_f32_16x16x4f32 (16 rows x 16 columns x 4 k). Inside a step
+// lane l feeds column / row l%16 and k = 4*(l/16)..+3, one k per
+// instruction. The wavefronts' partial tiles are summed in LDS in a fixed
+// order, then the epilogue of k_gemm applies.
+constexpr int SK_NW = 8;
+
+template <int EPI, int MB>
+__global__ void __launch_bounds__(SK_NW * 64) k_skinny(GemmArgs a) {
+    constexpr int D = MB <= 2 ? 8 : 4;
+    __shared__ float part[SK_NW][MB][4][64];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int lc = lane & 15, lk = (lane >> 4) * 4;
+    const int n0 = blockIdx.x * 16;
+    const int K = a.K;
+    const int nsteps = (K + 15) / 16;
+    const int per = (nsteps + SK_NW - 1) / SK_NW;
+    const int s0 = min(nsteps, wave * per), s1 = min(nsteps, s0 + per);
+    const float* wrow = a.W + (long)min(n0 + lc, a.N - 1) * K + lk;
+    const float* xrow[MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; mb++) xrow[mb] = a.X + (long)min(mb * 16 + lc, a.M - 1) * K + lk;
+
+    f32x4 acc[MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; mb++) acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int s = s0; s < s1; s += D) {
+        f32x4 wv[D], xv[D][MB];
+#pragma unroll
+        for (int d = 0; d < D; d++) {
+            const int k = (s + d) * 16;
+            const bool ok = s + d < s1 && k + lk < K;
+            wv[d] = ok ? *(const f32x4*)(wrow + k) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int mb = 0; mb < MB; mb++)
+                xv[d][mb] = ok ? *(const f32x4*)(xrow[mb] + k) : f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int d = 0; d < D; d++)
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+#pragma unroll
+                for (int mb = 0; mb < MB; mb++)
+                    acc[mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[d][mb][e], wv[d][e], acc[mb],
+                                                                    0, 0, 0);
+    }
+    // acc[mb][r]: row mb*16 + 4*(lane/16) + r, column n0 + lane%16.
+#pragma unroll
+    for (int mb = 0; mb < MB; mb++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) part[wave][mb][r][lane] = acc[mb][r];
+    __syncthreads();
+    const long roff = a.row_off + (a.row_off_dev ? *a.row_off_dev : 0);
+    for (int idx = tid; idx < MB * 4 * 64; idx += SK_NW * 64) {
+        const int mb = idx / 256, r = (idx / 64) & 3, l = idx & 63;
+        float v = 0.f;
+#pragma unroll
+        for (int w = 0; w < SK_NW; w++) v += part[w][mb][r][l];
+        const int row = mb * 16 + 4 * (l >> 4) + r, col = n0 + (l & 15);
+        if (row >= a.M || col >= a.N) continue;
+        long orow = a.seg ? (long)(row / a.seg) * a.seg_stride + row % a.seg : row;
+        orow += roff;
+        float* y = a.Y + orow * a.ldy + col;
+        *y = apply_epi<EPI>(v, a.bias, col, y);
+    }
+}
+
+template <int EPI>
+hipError_t skinny_epi(const GemmArgs& a, hipStream_t s) {
+    const int grid = (a.N + 15) / 16;
+    if (a.M <= 16) k_skinny<EPI, 1><<<grid, SK_NW * 64, 0, s>>>(a);
+    else if (a.M <= 32) k_skinny<EPI, 2><<<grid, SK_NW * 64, 0, s>>>(a);
+    else if (a.M <= 48) k_skinny<EPI, 3><<<grid, SK_NW * 64, 0, s>>>(a);
+    else k_skinny<EPI, 4><<<grid, SK_NW * 64, 0, s>>>(a);
+    return hipGetLastError();
+}
+
 template <int EPI>
 hipError_t gemm_epi(const GemmArgs& a, hipStream_t s) {
     const int tiles_m = (a.M + BM - 1) / BM, tiles_n = (a.N + BN - 1) / BN;
@@ -166,6 +250,15 @@ hipError_t gemm_epi(const GemmArgs& a, hipStream_t s) {
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
     if (a.M <= 0 || a.N <= 0) return hipSuccess;
     if (a.K <= 0 || (a.K & 3)) return hipErrorInvalidValue;
+    if (a.M <= SKINNY_MAX_M) {
+        switch (a.epi) {
+            case EPI_STORE: return skinny_epi<EPI_STORE>(a, s);
+            case EPI_BIAS: return skinny_epi<EPI_BIAS>(a, s);
+            case EPI_BIAS_GELU: return skinny_epi<EPI_BIAS_GELU>(a, s);
+            case EPI_RESID: return skinny_epi<EPI_RESID>(a, s);
+        }
+        return hipErrorInvalidValue;
+    }
     switch (a.epi) {
         case EPI_STORE: return gemm_epi<EPI_STORE>(a, s);
         case EPI_BIAS: return gemm_epi<EPI_BIAS>(a, s);

@@ -29,6 +29,9 @@ struct GemmArgs {
     const int* row_off_dev;    // if set, *row_off_dev is added too (decode position)
     int epi;                   // EpiMode
 };
+// M <= SKINNY_MAX_M rows take the weight-streaming k_skinny, larger M the
+// 128 x 128 MFMA tiles.
+constexpr int SKINNY_MAX_M = 64;
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t s);
 
 // decode.hip
