@@ -1,11 +1,17 @@
-"""Benchmark: GPT-2 small fp32 batched forward, B=16, T=1024, full logits.
+"""Benchmark: GPT-2 fp32 batched forward with full logits, and batched decode.
 
-Prints one JSON line. value = forward tokens/s over the timed steps (tokens
-already in HBM, logits [16, 1024, 50257] left in HBM); roofline = the MFMA
-GEMM kernels (all linear layers and the lm_head) timed with HIP events on
-the library's stream during the same steps, against MI355X's dense fp32
-matrix peak. Also reported: single-stream decode tok/s (32-token prompt,
-512 greedy steps with the KV cache) and the CPU oracle timed on this host.
+Default workload (the headline): GPT-2 small, B=16, T=1024, all-position
+logits [16, 1024, 50257] left in HBM. Prints one JSON line:
+  value     forward tokens/s over the timed steps (tokens already in HBM);
+  roofline  the MFMA GEMM kernels (all linear layers and the lm_head), each
+            launch timed with a HIP event pair on the library's stream during
+            the same steps, against MI355X's dense fp32 matrix peak;
+  decode    greedy single-token steps with the KV cache (one replayed HIP
+            graph per step), tok/s and algorithmic HBM bytes / time;
+  cpu_baseline  the oracle (C restatement of the reference's fast path with
+            OpenBLAS) timed on this host on a bounded sample.
+--workload medium / xl measures GPT-2 medium (prefill B=8, decode B=8 after a
+768-token prompt) and XL (prefill B=4, decode B=32 after a 32-token prompt).
 """
 from __future__ import annotations
 
@@ -24,8 +30,15 @@ import cngpt_amd  # noqa: E402
 
 PEAK_FP32_MFMA = 157.3e12   # 256 CUs x 2.4 GHz x 256 FLOP/clk/CU
 PEAK_HBM = 8.0e12
-METRIC = "forward tokens/sec + GEMM MFMA util %, GPT-2 small fp32 B=16 T=1024; decode tok/s"
 SEED = 1234
+
+# name -> (config, prefill B, T, decode B, prompt, decode steps)
+WORKLOADS = {
+    "small": (cngpt_amd.GPT2_SMALL, 16, 1024, 1, 32, 512),
+    "medium": (cngpt_amd.GPT2_MEDIUM, 8, 1024, 8, 768, 256),
+    "xl": (cngpt_amd.GPT2_XL, 4, 1024, 32, 32, 128),
+}
+NAMES = {"small": "GPT-2 small", "medium": "GPT-2 medium", "xl": "GPT-2 XL"}
 
 
 def lcg_tokens(n: int, vocab: int, seed: int) -> np.ndarray:
@@ -36,6 +49,18 @@ def lcg_tokens(n: int, vocab: int, seed: int) -> np.ndarray:
         s = (s * 1664525 + 1013904223) & 0xFFFFFFFF
         out[i] = (s >> 8) % vocab
     return out.astype(np.int32)
+
+
+def weights(name: str, cfg):
+    """GPT-2 small: the reference's seeded init (srand(1234), the draw order of
+    gpt_init_weights). Medium / XL: N(0, 0.02) from numpy's generator (the
+    rand() stream would take minutes for 0.35-1.5 G values)."""
+    if name == "small":
+        return cngpt_amd.init_weights(cfg, SEED), \
+            "seeded N(0,0.02) weights (srand 1234, gpt_init_weights order)"
+    p = np.random.default_rng(SEED).standard_normal(cngpt_amd.num_params(cfg), dtype=np.float32)
+    p *= np.float32(0.02)
+    return p, "N(0,0.02) weights from numpy PCG64 seed 1234"
 
 
 def prefill(m: cngpt_amd.Model, cfg, B: int, T: int, steps: int, warmup: int):
@@ -56,30 +81,31 @@ def prefill(m: cngpt_amd.Model, cfg, B: int, T: int, steps: int, warmup: int):
     m.profile(False)
     prof = m.profile_read()
     m.profile_reset()
-    return dt, prof, tokens
+    return dt, prof
 
 
 def decode_bytes(cfg, params_n: int, B: int, first_pos: int, steps: int) -> float:
     """Algorithmic HBM bytes of `steps` decode steps whose tokens sit at
-    positions first_pos.. : every weight once per step (wpe: one row), the
-    K and V rows of keys 0..p, the new q/k/v row and the logits."""
+    positions first_pos.. : every weight once per step (wpe: one row per
+    sequence), the K and V rows of keys 0..p, the new q/k/v row and the
+    logits of each sequence."""
     C, L, V = cfg.n_embd, cfg.n_layer, cfg.vocab_size
-    weights = 4.0 * (params_n - cfg.block_size * C + C)
+    weights_b = 4.0 * (params_n - cfg.block_size * C + B * C)
     total = 0.0
     for p in range(first_pos, first_pos + steps):
-        total += weights + 4.0 * L * B * (p + 1) * 2 * C + 4.0 * L * B * 3 * C + 4.0 * B * V
+        total += weights_b + 4.0 * L * B * (p + 1) * 2 * C + 4.0 * L * B * 3 * C + 4.0 * B * V
     return total
 
 
-def decode(m: cngpt_amd.Model, cfg, prompt_len: int, steps: int, draws=None):
-    """`steps` single-token decode steps after a prompt_len prompt, B=1, as
-    one cngpt_hip_generate call (one replayed HIP graph per step); greedy, or
-    temp 0.8 / top-k 40 sampling when draws are given."""
-    prompt = lcg_tokens(prompt_len, cfg.vocab_size, 777).reshape(1, prompt_len)
+def decode(m: cngpt_amd.Model, cfg, B: int, prompt_len: int, steps: int, draws=None):
+    """`steps` single-token decode steps for B sequences after a prompt_len
+    prompt, as one cngpt_hip_generate call; greedy, or temp 0.8 / top-k 40
+    sampling when draws are given."""
+    prompt = lcg_tokens(B * prompt_len, cfg.vocab_size, 777).reshape(B, prompt_len)
     kw = {} if draws is None else {"temperature": 0.8, "top_k": 40,
-                                   "draws": draws[:steps + 1]}
+                                   "draws": draws[:(steps + 1) * B]}
+    warm = {} if draws is None else {"temperature": 0.8, "top_k": 40, "draws": draws[:8 * B]}
     m.decode_begin(prompt, capacity=prompt_len + steps)
-    warm = {} if draws is None else {"temperature": 0.8, "top_k": 40, "draws": draws[:8]}
     m.generate(8, **warm)                     # warm-up, captures the step graph
     m.decode_begin(prompt, capacity=prompt_len + steps)
     m.synchronize()
@@ -88,10 +114,26 @@ def decode(m: cngpt_amd.Model, cfg, prompt_len: int, steps: int, draws=None):
     return time.perf_counter() - t0
 
 
-def cpu_baseline(cfg, params, budget_s: float):
+def reference_shape(m: cngpt_amd.Model, iters: int = 20):
+    """The shape the reference publishes its fast-path numbers at (B=1,
+    T=128, final-position logits, README.md:410-416), through the whole
+    host API (tokens H2D, logits D2H, synchronise) as `cngpt bench --fast`
+    does."""
+    tk = np.zeros((1, 128), np.int32)
+    m.forward(tk, cngpt_amd.LAST)
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        m.forward(tk, cngpt_amd.LAST)
+    dt = (time.perf_counter() - t0) / iters
+    return {"B": 1, "T": 128, "tok_s": round(128 / dt, 1), "ms_per_forward": round(dt * 1e3, 3),
+            "published_cpu_tok_s": 2261.6,
+            "published_cpu": "Ryzen 5 7600, 6 threads, OpenBLAS 0.3.29 (reference README.md:415)"}
+
+
+def cpu_baseline(name: str, cfg, params, budget_s: float):
     """The oracle (C restatement of the reference's gpt_forward_fast with
-    OpenBLAS, one pinned thread per physical core) on a bounded sample of
-    the same workload: B=1 sequences of T=1024 tokens, all-position logits."""
+    OpenBLAS, one pinned thread per physical core) on a bounded sample of the
+    same workload: B=1 sequences of T=1024 tokens, all-position logits."""
     import oracle
 
     ocfg = oracle.Cfg(cfg.n_layer, cfg.n_head, cfg.n_embd, cfg.vocab_size, cfg.block_size)
@@ -111,125 +153,9 @@ def cpu_baseline(cfg, params, budget_s: float):
     oracle.forward(ocfg, params, tk, oracle.LAST)
     last_s = time.perf_counter() - t1
     return {"value": round(tok_s, 2), "unit": "tokens/s", "cores": cores, "kind": "port",
-            "sample": f"{n} forward(s) of B=1 x T=1024 GPT-2 small fp32, all-position logits "
+            "sample": f"{n} forward(s) of B=1 x T=1024 {NAMES[name]} fp32, all-position logits "
                       f"({dt:.1f} s); oracle C restatement of fast.c + {oracle.blas_info()}",
             "last_position_tok_s": round(1024 / last_s, 2)}
-
-
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
-    ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--decode-steps", type=int, default=512)
-    ap.add_argument("--cpu-budget", type=float, default=10.0)
-    ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MiB",
-                    help="also run one plain device copy of this size (counter calibration)")
-    ap.add_argument("--decode-only", action="store_true",
-                    help="only the decode legs (for kernel traces of the decode step)")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print(f"bench.py measures one GPU only (this build has no multi-GPU path); "
-              f"--gpus {args.gpus} is not supported", file=sys.stderr)
-        sys.exit(2)
-
-    cfg = cngpt_amd.GPT2_SMALL
-    B, T = 16, 1024
-    params = cngpt_amd.init_weights(cfg, SEED)
-    m = cngpt_amd.Model(cfg, params)
-
-    if args.decode_only:
-        dec_dt = decode(m, cfg, 32, args.decode_steps)
-        dec_bytes = decode_bytes(cfg, params.size, 1, 32, args.decode_steps)
-        # per-kernel-class split of the same steps (direct launches, HIP events)
-        m.profile_reset()
-        m.profile(True)
-        prof_dt = decode(m, cfg, 32, args.decode_steps)
-        m.profile(False)
-        prof = m.profile_read()
-        m.close()
-        n = args.decode_steps
-        print(json.dumps({"decode_tok_s": round(n / dec_dt, 1),
-                          "ms_per_token": round(dec_dt * 1e3 / n, 4),
-                          "hbm_frac": round(dec_bytes / dec_dt / PEAK_HBM, 4),
-                          "graphs": os.environ.get("CNGPT_HIP_GRAPH", "1") != "0",
-                          "evented_ms_per_token": round(prof_dt * 1e3 / n, 4),
-                          "kernel_us_per_token": {k: round(v["ms"] * 1e3 / n, 2)
-                                                  for k, v in prof.items() if v["launches"]},
-                          "launches_per_token": {k: round(v["launches"] / n, 2)
-                                                 for k, v in prof.items() if v["launches"]}}),
-              flush=True)
-        return
-
-    dt, prof, _ = prefill(m, cfg, B, T, args.steps, args.warmup)
-    tokens = B * T * args.steps
-    g = prof["gemm"]
-    gemm_ms_avg = g["ms"] / g["launches"]
-    achieved = g["flops"] / (g["ms"] * 1e-3)
-    gemm_share = g["ms"] / (dt * 1e3)
-
-    dec_dt = decode(m, cfg, 32, args.decode_steps)
-    dec_bytes = decode_bytes(cfg, params.size, 1, 32, args.decode_steps)
-    draws = np.random.default_rng(7).random(args.decode_steps + 1).astype(np.float32)
-    samp_dt = decode(m, cfg, 32, args.decode_steps, draws)
-    m.close()
-
-    # HBM-side bytes per GEMM launch from the committed rocprofv3 --pmc
-    # summary of this workload (FETCH_SIZE + WRITE_SIZE, calibrated).
-    traffic = None
-    tpath = os.path.join(ROOT, "profiles", "gemm_traffic.json")
-    if os.path.exists(tpath):
-        with open(tpath) as f:
-            traffic = json.load(f).get("measured_bytes_per_launch")
-
-    line = {
-        "metric": METRIC,
-        "value": round(tokens / dt, 1),
-        "unit": "tokens/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(dt * 1e3 / args.steps, 3),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "f32",
-        "data": "synthetic: seeded N(0,0.02) weights (srand 1234, gpt_init_weights order), "
-                "LCG token ids uniform in [0,50257)",
-        "config": {"workload": "GPT-2 small fp32 batched prefill, full logits [16,1024,50257]",
-                   "B": B, "T": T, "n_layer": 12, "n_embd": 768, "vocab": 50257,
-                   "logits": "all positions, left in HBM"},
-        "roofline": {"bound": "mfma", "achieved": round(achieved / 1e12, 2),
-                     "peak": PEAK_FP32_MFMA / 1e12, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_FP32_MFMA, 4), "traffic": traffic,
-                     "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE+WRITE_SIZE)",
-                     "kernel": "k_gemm (all MFMA linear layers + lm_head)",
-                     "avg_launch_ms": round(gemm_ms_avg, 4),
-                     "launches": g["launches"], "share_of_step": round(gemm_share, 4)},
-        "gemm_mfma_util_pct": round(100 * achieved / PEAK_FP32_MFMA, 2),
-        "decode": {"tok_s": round(args.decode_steps / dec_dt, 1),
-                   "ms_per_token": round(dec_dt * 1e3 / args.decode_steps, 4),
-                   "prompt": 32, "steps": args.decode_steps, "B": 1, "sampling": "greedy",
-                   "hbm": {"bound": "hbm", "achieved": round(dec_bytes / dec_dt / 1e9, 1),
-                           "peak": PEAK_HBM / 1e9, "unit": "GB/s",
-                           "frac": round(dec_bytes / dec_dt / PEAK_HBM, 4),
-                           "bytes_per_step": round(dec_bytes / args.decode_steps)},
-                   "sampled_tok_s": round(args.decode_steps / samp_dt, 1),
-                   "sampled": "temp 0.8, top-k 40, device sample_top_k"},
-        "kernels": {k: {"ms_per_step": round(v["ms"] / args.steps, 3),
-                        "launches_per_step": v["launches"] // max(args.steps, 1),
-                        **({"tflops": round(v["flops"] / (v["ms"] * 1e-3) / 1e12, 2)}
-                           if v["flops"] and v["ms"] else {}),
-                        **({"gbps": round(v["bytes"] / (v["ms"] * 1e-3) / 1e9, 1)}
-                           if v["bytes"] and v["ms"] else {})}
-                    for k, v in prof.items() if v["launches"]},
-    }
-    if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(cfg, params, args.cpu_budget)
-    if args.copy_calibration:
-        line["copy_calibration_bytes"] = copy_calibration(args.copy_calibration << 20)
-    print(json.dumps(line), flush=True)
 
 
 def copy_calibration(nbytes: int) -> int:
@@ -249,6 +175,133 @@ def copy_calibration(nbytes: int) -> int:
     hip.hipFree(src)
     hip.hipFree(dst)
     return nbytes
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="small")
+    ap.add_argument("--decode-steps", type=int, default=None,
+                    help="decode steps (default: the workload's)")
+    ap.add_argument("--cpu-budget", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MiB",
+                    help="also run one plain device copy of this size (counter calibration)")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="only the decode legs (for kernel traces of the decode step)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build has no multi-GPU path); "
+              f"--gpus {args.gpus} is not supported", file=sys.stderr)
+        sys.exit(2)
+
+    name = args.workload
+    cfg, B, T, dB, prompt, dsteps = WORKLOADS[name]
+    if args.decode_steps is not None:
+        dsteps = args.decode_steps
+    params, data = weights(name, cfg)
+    m = cngpt_amd.Model(cfg, params)
+
+    if args.decode_only:
+        dec_dt = decode(m, cfg, dB, prompt, dsteps)
+        dec_bytes = decode_bytes(cfg, params.size, dB, prompt, dsteps)
+        draws = np.random.default_rng(7).random((dsteps + 1) * dB).astype(np.float32)
+        samp_dt = decode(m, cfg, dB, prompt, dsteps, draws)
+        # per-kernel-class split of the sampled steps (direct launches, HIP events)
+        m.profile_reset()
+        m.profile(True)
+        prof_dt = decode(m, cfg, dB, prompt, dsteps, draws)
+        m.profile(False)
+        prof = m.profile_read()
+        m.close()
+        n = dsteps
+        print(json.dumps({"workload": name, "B": dB, "decode_tok_s": round(n * dB / dec_dt, 1),
+                          "ms_per_step": round(dec_dt * 1e3 / n, 4),
+                          "hbm_frac": round(dec_bytes / dec_dt / PEAK_HBM, 4),
+                          "sampled_tok_s": round(n * dB / samp_dt, 1),
+                          "graphs": os.environ.get("CNGPT_HIP_GRAPH", "1") != "0",
+                          "evented_ms_per_step": round(prof_dt * 1e3 / n, 4),
+                          "kernel_us_per_step": {k: round(v["ms"] * 1e3 / n, 2)
+                                                 for k, v in prof.items() if v["launches"]},
+                          "launches_per_step": {k: round(v["launches"] / n, 2)
+                                                for k, v in prof.items() if v["launches"]}}),
+              flush=True)
+        return
+
+    dt, prof = prefill(m, cfg, B, T, args.steps, args.warmup)
+    tokens = B * T * args.steps
+    g = prof["gemm"]
+    gemm_ms_avg = g["ms"] / g["launches"]
+    achieved = g["flops"] / (g["ms"] * 1e-3)
+    gemm_share = g["ms"] / (dt * 1e3)
+
+    dec_dt = decode(m, cfg, dB, prompt, dsteps)
+    dec_bytes = decode_bytes(cfg, params.size, dB, prompt, dsteps)
+    draws = np.random.default_rng(7).random((dsteps + 1) * dB).astype(np.float32)
+    samp_dt = decode(m, cfg, dB, prompt, dsteps, draws)
+    ref_shape = reference_shape(m) if name == "small" else None
+    m.close()
+
+    # HBM-side bytes per GEMM launch from the committed rocprofv3 --pmc
+    # summary of this workload (FETCH_SIZE + WRITE_SIZE, calibrated).
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "gemm_traffic.json")
+    if name == "small" and os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("measured_bytes_per_launch")
+
+    line = {
+        "metric": f"forward tokens/sec + GEMM MFMA util %, {NAMES[name]} fp32 B={B} T={T}; "
+                  f"decode tok/s",
+        "value": round(tokens / dt, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dt * 1e3 / args.steps, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": f"synthetic: {data}, LCG token ids uniform in [0,{cfg.vocab_size})",
+        "config": {"workload": f"{NAMES[name]} fp32 batched prefill, full logits "
+                               f"[{B},{T},{cfg.vocab_size}]",
+                   "B": B, "T": T, "n_layer": cfg.n_layer, "n_embd": cfg.n_embd,
+                   "vocab": cfg.vocab_size, "logits": "all positions, left in HBM"},
+        "roofline": {"bound": "mfma", "achieved": round(achieved / 1e12, 2),
+                     "peak": PEAK_FP32_MFMA / 1e12, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_FP32_MFMA, 4), "traffic": traffic,
+                     "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE+WRITE_SIZE)",
+                     "kernel": "k_gemm (all MFMA linear layers + lm_head)",
+                     "avg_launch_ms": round(gemm_ms_avg, 4),
+                     "launches": g["launches"], "share_of_step": round(gemm_share, 4)},
+        "gemm_mfma_util_pct": round(100 * achieved / PEAK_FP32_MFMA, 2),
+        "decode": {"tok_s": round(dsteps * dB / dec_dt, 1),
+                   "ms_per_step": round(dec_dt * 1e3 / dsteps, 4),
+                   "prompt": prompt, "steps": dsteps, "B": dB, "sampling": "greedy",
+                   "hbm": {"bound": "hbm", "achieved": round(dec_bytes / dec_dt / 1e9, 1),
+                           "peak": PEAK_HBM / 1e9, "unit": "GB/s",
+                           "frac": round(dec_bytes / dec_dt / PEAK_HBM, 4),
+                           "bytes_per_step": round(dec_bytes / dsteps)},
+                   "sampled_tok_s": round(dsteps * dB / samp_dt, 1),
+                   "sampled": "temp 0.8, top-k 40, device sample_top_k"},
+        "kernels": {k: {"ms_per_step": round(v["ms"] / args.steps, 3),
+                        "launches_per_step": v["launches"] // max(args.steps, 1),
+                        **({"tflops": round(v["flops"] / (v["ms"] * 1e-3) / 1e12, 2)}
+                           if v["flops"] and v["ms"] else {}),
+                        **({"gbps": round(v["bytes"] / (v["ms"] * 1e-3) / 1e9, 1)}
+                           if v["bytes"] and v["ms"] else {})}
+                    for k, v in prof.items() if v["launches"]},
+    }
+    if ref_shape:
+        line["reference_shape"] = ref_shape
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(name, cfg, params, args.cpu_budget)
+    if args.copy_calibration:
+        line["copy_calibration_bytes"] = copy_calibration(args.copy_calibration << 20)
+    print(json.dumps(line), flush=True)
 
 
 if __name__ == "__main__":

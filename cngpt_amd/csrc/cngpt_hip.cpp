@@ -149,10 +149,14 @@ struct Timed {
 
 // ---------------------------------------------------------------- launches
 
-// Products over M <= 8 rows go to the decode GEMV (one wavefront per output
-// column, LayerNorm of the input rows optionally folded in); larger M to the
-// MFMA tile kernel.
-constexpr int SKINNY = 8;
+// Products over M <= SKINNY rows go to the decode GEMV (one wavefront per
+// output column, LayerNorm of the input rows optionally folded in); larger M
+// to the MFMA kernels (16-column tiles up to 64 rows, then 128 x 128).
+// Up to SKINNY rows the per-column products (LayerNorm, attention merge or
+// embedding folded into their input staging) beat a separate LayerNorm plus
+// the 16-column MFMA tiles; from 3 rows on the tiles' reuse of the input
+// rows wins (measured on GPT-2 medium, 8 sequences: 1.72 vs 1.88 ms a step).
+constexpr int SKINNY = 2;
 
 int run_gemm(cngpt_hip_ctx* h, const float* X, const float* W, const float* bias, float* Y, int M,
              int N, int K, int epi, int seg = 0, long seg_stride = 0, long ldy = -1,
@@ -283,7 +287,11 @@ int run_attn_row_proj(cngpt_hip_ctx* h, const float* qkv, long seq_stride, int B
     g.part = h->attn_part; g.stride = h->attn_splits;
     g.H = c.n_head; g.hs = hs; g.kps = attn_dec_keys_per_split(hs);
     g.q_pos = q_pos; g.pos_dev = pos_dev;
-    if (B <= SKINNY) {
+    // Every workgroup of the c_proj product merges all splits it needs; that
+    // pays while the partials are small (one sequence, short context).
+    const int splits = (max_keys + g.kps - 1) / g.kps;
+    const double merge_bytes = 4.0 * B * c.n_head * splits * (hs + 4);
+    if (B <= SKINNY && merge_bytes <= 64.0 * 1024) {
         DecGemvArgs d{};
         d.merge = g;
         d.W = w.proj_w; d.bias = w.proj_b; d.Y = xres; d.ldy = C;

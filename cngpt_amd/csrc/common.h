@@ -8,6 +8,16 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 #define CNGPT_WAVE 64
 
+// Guarded 16-byte load that always reads *p (the caller clamps the index to
+// a valid address) and returns zero when !ok. Unlike `ok ? *p : 0`, which
+// masks the load off for lanes without ok, it costs a real access per lane;
+// it serves where the masked-off lanes are few and a fixed instruction
+// sequence keeps register pressure down (LayerNorm rows).
+__device__ __forceinline__ f32x4 ld4_or0(const f32x4* p, bool ok) {
+    const f32x4 v = *p;
+    return ok ? v : f32x4{0.f, 0.f, 0.f, 0.f};
+}
+
 // Butterfly sum / max over the 64 lanes of a wavefront.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

@@ -524,24 +524,54 @@ __global__ void __launch_bounds__(ST) k_sample(const float* __restrict__ logits,
     const int ch4 = (V4 + ST - 1) / ST;
     const int g0 = min(tid * ch4, V4), g1 = min(g0 + ch4, V4);
     const float tdiv = temp > 0.0f ? temp : 1.0f;
-    auto ok = [&](int i) { return i < V; };
+    const int NP = V4 * 4;  // padded length of the scratch row
+    constexpr int U = 8;    // loads in flight per thread in the strided passes
 
-    // scaled values (coalesced read of the logits), their max
+    // scaled values (coalesced reads of the logits) and their max
     float mx = -INFINITY;
-    for (int i = tid; i < V4 * 4; i += ST) {
-        const float v = ok(i) ? lg[i] / tdiv : -INFINITY;
-        p[i] = v;
-        mx = fmaxf(mx, v);
+    for (int i0 = 0; i0 < NP; i0 += ST * U) {
+        float v[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int i = i0 + u * ST + tid;
+            const float x = lg[min(i, V - 1)] / tdiv;
+            v[u] = i < V ? x : -INFINITY;
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int i = i0 + u * ST + tid;
+            if (i < NP) p[i] = v[u];
+            mx = fmaxf(mx, v[u]);
+        }
     }
     mx = block_max(mx, shf);
     float s = 0.f;
-    for (int i = tid; i < V4 * 4; i += ST) {
-        const float e = ok(i) ? expf(p[i] - mx) : 0.f;
-        p[i] = e;
-        s += e;
+    for (int i0 = 0; i0 < NP; i0 += ST * U) {
+        float v[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int i = i0 + u * ST + tid;
+            const float x = p[min(i, NP - 1)];
+            v[u] = i < V ? expf(x - mx) : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int i = i0 + u * ST + tid;
+            if (i < NP) p[i] = v[u];
+            s += v[u];
+        }
     }
     const float sum = block_sum(s, shf);
-    for (int i = tid; i < V4 * 4; i += ST) p[i] = ok(i) ? p[i] / sum : 0.f;
+    for (int i0 = 0; i0 < NP; i0 += ST * U) {
+        float v[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) v[u] = p[min(i0 + u * ST + tid, NP - 1)];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int i = i0 + u * ST + tid;
+            if (i < NP) p[i] = i < V ? v[u] / sum : 0.f;
+        }
+    }
     __syncthreads();
 
     // k-th largest probability (with multiplicity) by MSB-first radix
@@ -554,9 +584,15 @@ __global__ void __launch_bounds__(ST) k_sample(const float* __restrict__ logits,
         for (int shift = 24; shift >= 0; shift -= 8) {
             for (int i = tid; i < 256; i += ST) hist[i] = 0;
             __syncthreads();
-            for (int i = tid; i < V4 * 4; i += ST) {
-                const unsigned u = __float_as_uint(p[i]);
-                hist_add(hist, (u >> shift) & 255u, ok(i) && (u & mask) == prefix);
+            for (int i0 = 0; i0 < NP; i0 += ST * U) {
+                unsigned uv[U];
+#pragma unroll
+                for (int u = 0; u < U; u++) uv[u] = __float_as_uint(p[min(i0 + u * ST + tid, NP - 1)]);
+#pragma unroll
+                for (int u = 0; u < U; u++) {
+                    const int i = i0 + u * ST + tid;
+                    hist_add(hist, (uv[u] >> shift) & 255u, i < V && (uv[u] & mask) == prefix);
+                }
             }
             __syncthreads();
             if (tid == 0) {
@@ -575,27 +611,32 @@ __global__ void __launch_bounds__(ST) k_sample(const float* __restrict__ logits,
         thr = __uint_as_float(prefix);
     }
 
-    // Survivors (all values when there is no cut) in index order.
+    // Survivors (all values when there is no cut) in index order. Thread
+    // ranges: float4 groups g0 + j, j < ch4 (a uniform trip count).
+    auto keep = [&](int i, float v) { return i < V && (!cut || v >= thr); };
     int cnt = 0;
-    for (int g = g0; g < g1; g++) {
-        const f32x4 v = p4[g];
-        const int i = g * 4;
-        cnt += (ok(i) && (!cut || v.x >= thr)) + (ok(i + 1) && (!cut || v.y >= thr)) +
-               (ok(i + 2) && (!cut || v.z >= thr)) + (ok(i + 3) && (!cut || v.w >= thr));
+#pragma unroll 4
+    for (int j = 0; j < ch4; j++) {
+        const int g = g0 + j;
+        const f32x4 v = ld4_or0(p4 + min(g, V4 - 1), g < g1);
+        if (g < g1)
+            cnt += keep(4 * g, v.x) + keep(4 * g + 1, v.y) + keep(4 * g + 2, v.z) +
+                   keep(4 * g + 3, v.w);
     }
     int total;
     const int base = block_excl_scan<int>(cnt, shi, &total);
     const float r = r_draw[row];
     if (cut && total <= SLIST) {
         int k = base;
-        for (int g = g0; g < g1; g++) {
-            const f32x4 v = p4[g];
+        for (int j = 0; j < ch4; j++) {
+            const int g = g0 + j;
+            const f32x4 v = ld4_or0(p4 + min(g, V4 - 1), g < g1);
             const float vv[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-            for (int j = 0; j < 4; j++)
-                if (ok(g * 4 + j) && vv[j] >= thr) {
-                    lv[k] = vv[j];
-                    li[k] = g * 4 + j;
+            for (int e = 0; e < 4; e++)
+                if (g < g1 && keep(4 * g + e, vv[e])) {
+                    lv[k] = vv[e];
+                    li[k] = 4 * g + e;
                     k++;
                 }
         }
@@ -613,16 +654,18 @@ __global__ void __launch_bounds__(ST) k_sample(const float* __restrict__ logits,
         }
         return;
     }
-    // Blocked form: zero the cut values, renormalise, prefix by ranges.
+    // Blocked form: zero the cut values, renormalise, prefix by ranges
+    // (scratch padding past V holds 0).
     float ps = 0.f;
-    for (int g = g0; g < g1; g++) {
-        f32x4 v = p4[g];
+    for (int j = 0; j < ch4; j++) {
+        const int g = g0 + j;
+        f32x4 v = ld4_or0(p4 + min(g, V4 - 1), g < g1);
         if (cut) {
             v.x = v.x < thr ? 0.f : v.x;
             v.y = v.y < thr ? 0.f : v.y;
             v.z = v.z < thr ? 0.f : v.z;
             v.w = v.w < thr ? 0.f : v.w;
-            p4[g] = v;
+            if (g < g1) p4[g] = v;
         }
         ps += ((v.x + v.y) + v.z) + v.w;
     }
@@ -630,10 +673,11 @@ __global__ void __launch_bounds__(ST) k_sample(const float* __restrict__ logits,
         const float ns = block_sum(ps, shf);
         if (ns > 0.0f) {
             ps = 0.f;
-            for (int g = g0; g < g1; g++) {
-                f32x4 v = p4[g];
+            for (int j = 0; j < ch4; j++) {
+                const int g = g0 + j;
+                f32x4 v = ld4_or0(p4 + min(g, V4 - 1), g < g1);
                 v.x /= ns; v.y /= ns; v.z /= ns; v.w /= ns;
-                p4[g] = v;
+                if (g < g1) p4[g] = v;
                 ps += ((v.x + v.y) + v.z) + v.w;
             }
         }

@@ -15,7 +15,7 @@
 // wavefront). Ragged M and N edges (e.g. the 50257-wide vocabulary) clamp
 // loads to the last valid row and mask stores.
 //
-// k_skinny: 8 < M <= 64 rows, 16-column tiles, K split over 8 wavefronts.
+// k_skinny: 8 < M <= 64 rows, 16-column tiles, K split over 16 wavefronts.
 // Products over M <= 8 rows (decode, the last-position pass) are k_dgemv in
 // decode.hip.
 #include "common.h"
@@ -158,19 +158,21 @@ __global__ void __launch_bounds__(NTHREADS, 2) k_gemm(GemmArgs a, int tiles_m, i
 // ---------------------------------------------------------------- skinny
 
 // k_skinny: 8 < M <= 64 rows (batched decode, last-position passes of
-// larger batches, short prefills). Weight-bandwidth bound: each workgroup
-// owns 16 output columns and streams those 16 weight rows once; its NW
-// wavefronts split K, each keeping D k-steps of 16 in flight (one 16-byte
-// weight load and MB 16-byte input loads per lane per step), and multiply
-// with v_mfma_f32_16x16x4f32 (16 rows x 16 columns x 4 k). Inside a step
-// lane l feeds column / row l%16 and k = 4*(l/16)..+3, one k per
-// instruction. The wavefronts' partial tiles are summed in LDS in a fixed
-// order, then the epilogue of k_gemm applies.
-constexpr int SK_NW = 8;
+// larger batches, short prefills). Weight-bandwidth bound, and near the
+// fp32 ridge at M = 32 (2 * 32 FLOP per 4-byte weight = 16 FLOP/B against
+// 157.3 / 8 = 19.7). Each workgroup owns 16 output columns and streams those
+// 16 weight rows once; its SK_NW wavefronts split K, and each double-buffers
+// D k-steps of 16 (one 16-byte weight load and MB 16-byte input loads per
+// lane per step): the loads of the next D steps are in flight while the
+// current ones are multiplied with v_mfma_f32_16x16x4f32 (16 rows x 16
+// columns x 4 k). Inside a step lane l feeds column / row l%16 and
+// k = 4*(l/16)..+3, one k per instruction. The wavefronts' partial tiles are
+// summed in LDS in a fixed order, then the epilogue of k_gemm applies.
+constexpr int SK_NW = 16;
 
 template <int EPI, int MB>
 __global__ void __launch_bounds__(SK_NW * 64) k_skinny(GemmArgs a) {
-    constexpr int D = MB <= 2 ? 8 : 4;
+    constexpr int D = MB <= 2 ? 4 : 2;
     __shared__ float part[SK_NW][MB][4][64];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int lc = lane & 15, lk = (lane >> 4) * 4;
@@ -179,33 +181,60 @@ __global__ void __launch_bounds__(SK_NW * 64) k_skinny(GemmArgs a) {
     const int nsteps = (K + 15) / 16;
     const int per = (nsteps + SK_NW - 1) / SK_NW;
     const int s0 = min(nsteps, wave * per), s1 = min(nsteps, s0 + per);
-    const float* wrow = a.W + (long)min(n0 + lc, a.N - 1) * K + lk;
+    const float* wrow = a.W + (long)min(n0 + lc, a.N - 1) * K;
     const float* xrow[MB];
 #pragma unroll
-    for (int mb = 0; mb < MB; mb++) xrow[mb] = a.X + (long)min(mb * 16 + lc, a.M - 1) * K + lk;
+    for (int mb = 0; mb < MB; mb++) xrow[mb] = a.X + (long)min(mb * 16 + lc, a.M - 1) * K;
 
     f32x4 acc[MB];
 #pragma unroll
     for (int mb = 0; mb < MB; mb++) acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int s = s0; s < s1; s += D) {
-        f32x4 wv[D], xv[D][MB];
+    f32x4 wa[D], xa[D][MB], wb[D], xb[D][MB];
+    bool oa[D], ob[D];
+    // No branches around the loads (a branch per guarded load makes the
+    // compiler wait for every outstanding load at its join, which defeats
+    // the double buffer): a step past this wavefront's range re-reads its
+    // last step (cached) and a k past K re-reads the row's last 4 floats,
+    // and the weight value is zeroed at its use so the product vanishes (a
+    // select in the load phase would wait for the load there).
+    const int slast = max(s0, s1 - 1);
+    auto load = [&](f32x4* w, f32x4 (*x)[MB], bool* ok, int s) {
 #pragma unroll
         for (int d = 0; d < D; d++) {
-            const int k = (s + d) * 16;
-            const bool ok = s + d < s1 && k + lk < K;
-            wv[d] = ok ? *(const f32x4*)(wrow + k) : f32x4{0.f, 0.f, 0.f, 0.f};
+            const int k = min(s + d, slast) * 16 + lk;
+            ok[d] = s + d < s1 && k < K;
+            const int kk = min(k, K - 4);
+            w[d] = *(const f32x4*)(wrow + kk);
 #pragma unroll
-            for (int mb = 0; mb < MB; mb++)
-                xv[d][mb] = ok ? *(const f32x4*)(xrow[mb] + k) : f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int mb = 0; mb < MB; mb++) x[d][mb] = *(const f32x4*)(xrow[mb] + kk);
         }
+    };
+    auto mul = [&](const f32x4* w, f32x4 (*x)[MB], const bool* ok) {
 #pragma unroll
         for (int d = 0; d < D; d++)
 #pragma unroll
-            for (int e = 0; e < 4; e++)
+            for (int e = 0; e < 4; e++) {
+                const float we = ok[d] ? w[d][e] : 0.f;
 #pragma unroll
                 for (int mb = 0; mb < MB; mb++)
-                    acc[mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[d][mb][e], wv[d][e], acc[mb],
-                                                                    0, 0, 0);
+                    acc[mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[d][mb][e], we, acc[mb], 0, 0,
+                                                                    0);
+            }
+    };
+    // sched_barrier keeps the scheduler from sinking each load next to its
+    // first use, which would undo the double buffer.
+    if (s0 < s1) {
+        load(wa, xa, oa, s0);
+        for (int s = s0; s < s1; s += 2 * D) {
+            load(wb, xb, ob, s + D);
+            __builtin_amdgcn_sched_barrier(0);
+            mul(wa, xa, oa);
+            __builtin_amdgcn_sched_barrier(0);
+            load(wa, xa, oa, s + 2 * D);
+            __builtin_amdgcn_sched_barrier(0);
+            mul(wb, xb, ob);
+            __builtin_amdgcn_sched_barrier(0);
+        }
     }
     // acc[mb][r]: row mb*16 + 4*(lane/16) + r, column n0 + lane%16.
 #pragma unroll

@@ -49,17 +49,17 @@ __global__ void __launch_bounds__(256) k_layernorm(const float* __restrict__ x, 
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= rows) return;
     const float* xr = x + (long)row * in_stride;
-    f32x4 v[NCH];
+    // gain and bias are loaded with the row, not after the reductions
+    f32x4 v[NCH], wv[NCH], bv[NCH];
     float s = 0.f;
 #pragma unroll
     for (int j = 0; j < NCH; j++) {
-        int c = (lane + j * 64) * 4;
-        if (c < C) {
-            v[j] = *(const f32x4*)(xr + c);
-            s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
-        } else {
-            v[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-        }
+        const int c = (lane + j * 64) * 4;
+        const int cc = min(c, C - 4);
+        v[j] = ld4_or0((const f32x4*)(xr + cc), c < C);
+        wv[j] = ld4_or0((const f32x4*)(w + cc), c < C);
+        bv[j] = ld4_or0((const f32x4*)(b + cc), c < C);
+        s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
     }
     const float m = wave_sum(s) / (float)C;
     float q = 0.f;
@@ -76,12 +76,7 @@ __global__ void __launch_bounds__(256) k_layernorm(const float* __restrict__ x, 
 #pragma unroll
     for (int j = 0; j < NCH; j++) {
         int c = (lane + j * 64) * 4;
-        if (c < C) {
-            f32x4 wv = *(const f32x4*)(w + c);
-            f32x4 bv = *(const f32x4*)(b + c);
-            f32x4 o = (v[j] - m) * rs * wv + bv;
-            *(f32x4*)(orow + c) = o;
-        }
+        if (c < C) *(f32x4*)(orow + c) = (v[j] - m) * rs * wv[j] + bv[j];
     }
 }
 
