@@ -104,9 +104,10 @@ def decode(m: cngpt_amd.Model, cfg, B: int, prompt_len: int, steps: int, draws=N
     prompt = lcg_tokens(B * prompt_len, cfg.vocab_size, 777).reshape(B, prompt_len)
     kw = {} if draws is None else {"temperature": 0.8, "top_k": 40,
                                    "draws": draws[:(steps + 1) * B]}
-    warm = {} if draws is None else {"temperature": 0.8, "top_k": 40, "draws": draws[:8 * B]}
+    nwarm = min(8, steps + 1)
+    warm = {} if draws is None else {"temperature": 0.8, "top_k": 40, "draws": draws[:nwarm * B]}
     m.decode_begin(prompt, capacity=prompt_len + steps)
-    m.generate(8, **warm)                     # warm-up, captures the step graph
+    m.generate(nwarm, **warm)                 # warm-up, captures the step graph
     m.decode_begin(prompt, capacity=prompt_len + steps)
     m.synchronize()
     t0 = time.perf_counter()

@@ -5,12 +5,17 @@
 // (fast.c:175-205). Both operands are K-contiguous, so both tiles are staged
 // in LDS the same way and read back with 16-byte LDS reads.
 //
-// k_gemm: 128x128 output tile per 256-thread workgroup, K in steps of 32,
+// k_gemm: 128x128 output tile per 256-thread workgroup, K in steps of BK,
 // double-buffered LDS (global loads for step k+1 are in flight while step k
 // is multiplied). Each wavefront owns a 64x64 sub-tile = 2x2 blocks of
-// v_mfma_f32_32x32x2f32. Inside a K step, lanes 0-31 feed k = 0..15 and
-// lanes 32-63 feed k = 16..31 of the step, so each lane reads 4 contiguous
-// floats per row per LDS read. The epilogue adds bias / GELU / residual and
+// v_mfma_f32_32x32x2f32. Inside a K step, lanes 0-31 feed the first half of
+// the step's k and lanes 32-63 the second half, so each lane reads 4
+// contiguous floats per row per LDS read. Short K steps keep the LDS small
+// enough for 3-4 workgroups per CU, whose wavefronts hide each other's
+// barrier and load stalls: BK = 8 with 4 workgroups per CU is the fastest
+// variant on most GPT-2 shapes (122-135 TFLOP/s measured, against 93-121
+// for BK = 32 with 2); gemm_epi picks among BK = 8, 16 and 32 by how full
+// the last round of tiles is. The epilogue adds bias / GELU / residual and
 // stores straight from the accumulators (one 128-byte row segment per half
 // wavefront). Ragged M and N edges (e.g. the 50257-wide vocabulary) clamp
 // loads to the last valid row and mask stores.
@@ -23,11 +28,8 @@
 
 namespace {
 
-constexpr int BM = 128, BN = 128, BK = 32;
-constexpr int LDS_ROW = BK + 4;  // padded row, keeps 16-byte alignment
+constexpr int BM = 128, BN = 128;
 constexpr int NTHREADS = 256;
-constexpr int A_ITERS = BM * BK / 4 / NTHREADS;  // float4 loads per thread per tile
-constexpr int B_ITERS = BN * BK / 4 / NTHREADS;
 
 // Workgroups are dispatched round-robin over the 8 XCDs (pid % 8). Renumber
 // them so that each XCD receives a contiguous run of tile ids, then order
@@ -47,8 +49,13 @@ __device__ __forceinline__ void tile_coords(int pid, int tiles_m, int tiles_n, i
     tn = in_group / gsize;
 }
 
-template <int EPI>
-__global__ void __launch_bounds__(NTHREADS, 2) k_gemm(GemmArgs a, int tiles_m, int tiles_n) {
+template <int EPI, int BK, int PAD, int OCC>
+__global__ void __launch_bounds__(NTHREADS, OCC) k_gemm(GemmArgs a, int tiles_m, int tiles_n) {
+    constexpr int LDS_ROW = BK + PAD;            // padded row, keeps 16-byte alignment
+    constexpr int KQ = BK / 4;                   // float4 per row per K step
+    constexpr int RPI = NTHREADS / KQ;           // rows covered per load iteration
+    constexpr int A_ITERS = BM / RPI;            // float4 loads per thread per tile
+    constexpr int B_ITERS = BN / RPI;
     __shared__ float As[2][BM * LDS_ROW];
     __shared__ float Bs[2][BN * LDS_ROW];
 
@@ -58,18 +65,18 @@ __global__ void __launch_bounds__(NTHREADS, 2) k_gemm(GemmArgs a, int tiles_m, i
     const int tid = threadIdx.x;
     const int K = a.K;
 
-    // Global -> register staging: thread covers rows tid/8 + 32*i, float4 kq.
-    const int kq = (tid & 7) * 4;
+    // Global -> register staging: thread covers rows tid/KQ + RPI*i, float4 kq.
+    const int kq = (tid % KQ) * 4, r0 = tid / KQ;
     const float* xp[A_ITERS];
     const float* wp[B_ITERS];
 #pragma unroll
     for (int i = 0; i < A_ITERS; i++) {
-        int r = m0 + (tid >> 3) + 32 * i;
+        int r = m0 + r0 + RPI * i;
         xp[i] = a.X + (long)min(r, a.M - 1) * K + kq;
     }
 #pragma unroll
     for (int i = 0; i < B_ITERS; i++) {
-        int r = n0 + (tid >> 3) + 32 * i;
+        int r = n0 + r0 + RPI * i;
         wp[i] = a.W + (long)min(r, a.N - 1) * K + kq;
     }
     f32x4 ra[A_ITERS], rb[B_ITERS];
@@ -84,11 +91,9 @@ __global__ void __launch_bounds__(NTHREADS, 2) k_gemm(GemmArgs a, int tiles_m, i
     };
     auto lstore = [&](int buf) {
 #pragma unroll
-        for (int i = 0; i < A_ITERS; i++)
-            *(f32x4*)&As[buf][((tid >> 3) + 32 * i) * LDS_ROW + kq] = ra[i];
+        for (int i = 0; i < A_ITERS; i++) *(f32x4*)&As[buf][(r0 + RPI * i) * LDS_ROW + kq] = ra[i];
 #pragma unroll
-        for (int i = 0; i < B_ITERS; i++)
-            *(f32x4*)&Bs[buf][((tid >> 3) + 32 * i) * LDS_ROW + kq] = rb[i];
+        for (int i = 0; i < B_ITERS; i++) *(f32x4*)&Bs[buf][(r0 + RPI * i) * LDS_ROW + kq] = rb[i];
     };
 
     const int wave = tid >> 6, lane = tid & 63;
@@ -113,8 +118,8 @@ __global__ void __launch_bounds__(NTHREADS, 2) k_gemm(GemmArgs a, int tiles_m, i
         const float* as = &As[cur][0];
         const float* bs = &Bs[cur][0];
 #pragma unroll
-        for (int g = 0; g < 4; g++) {
-            const int kk = lh * 16 + g * 4;
+        for (int g = 0; g < BK / 8; g++) {
+            const int kk = lh * (BK / 2) + g * 4;
             f32x4 av[2], bv[2];
 #pragma unroll
             for (int i = 0; i < 2; i++) av[i] = *(const f32x4*)&as[(wm + i * 32 + lr) * LDS_ROW + kk];
@@ -267,10 +272,29 @@ hipError_t skinny_epi(const GemmArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
+// Share of the tile slots the last round of a launch fills when `res`
+// tiles are resident at a time.
+double round_fill(int tiles, int res) {
+    const int rounds = (tiles + res - 1) / res;
+    return rounds <= 1 ? 1.0 : (double)tiles / ((double)rounds * res);
+}
+
+// Variant choice, from a sweep of the three over the GPT-2 small / medium /
+// XL prefill products (M = 16384 / 8192 / 4096 rows): BK = 8 with 4
+// workgroups per CU is fastest whenever its tiles fit one round or fill its
+// last round; else BK = 16 with 3 per CU when that fills its last round
+// (e.g. 1536 or 2304 tiles); else BK = 32 with 2 per CU, whose longer K
+// steps hold up best when a round is left part-empty (e.g. 1216 tiles).
 template <int EPI>
 hipError_t gemm_epi(const GemmArgs& a, hipStream_t s) {
     const int tiles_m = (a.M + BM - 1) / BM, tiles_n = (a.N + BN - 1) / BN;
-    k_gemm<EPI><<<tiles_m * tiles_n, NTHREADS, 0, s>>>(a, tiles_m, tiles_n);
+    const int tiles = tiles_m * tiles_n, cus = 256;
+    if (tiles <= 4 * cus || round_fill(tiles, 4 * cus) >= 0.9)
+        k_gemm<EPI, 8, 4, 4><<<tiles, NTHREADS, 0, s>>>(a, tiles_m, tiles_n);
+    else if (round_fill(tiles, 3 * cus) >= 0.9)
+        k_gemm<EPI, 16, 8, 3><<<tiles, NTHREADS, 0, s>>>(a, tiles_m, tiles_n);
+    else
+        k_gemm<EPI, 32, 4, 2><<<tiles, NTHREADS, 0, s>>>(a, tiles_m, tiles_n);
     return hipGetLastError();
 }
 
