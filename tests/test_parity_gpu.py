@@ -130,6 +130,40 @@ def test_gpt2_small_zero_tokens_b2_t300(small):
     compare(m.forward(tk, cngpt_amd.LAST), oracle.forward(ocfg(cfg), params, tk), what="LAST")
 
 
+def test_gpt2_small_b16_t1024(small):
+    """The B=16 T=1024 workload the bench times (16384 rows: 128-row tiles
+    with the K=16 three-per-CU QKV variant): final-position logits of all 16
+    sequences, then the all-position logits of sequences 0 and 15 read back
+    from HBM at every position."""
+    cfg, params, m = small
+    V, T = cfg.vocab_size, 1024
+    tk = oracle.lcg_tokens(16 * T, V, seed=12345).reshape(16, T)
+    say("small B=16 T=1024 LAST")
+    compare(m.forward(tk, cngpt_amd.LAST), oracle.forward(ocfg(cfg), params, tk), what="LAST")
+    m.reserve(16, T, cngpt_amd.ALL)
+    m.upload_tokens(tk)
+    m.forward_resident(16, T, cngpt_amd.ALL)
+    m.synchronize()
+    for b in (0, 15):
+        say(f"small B=16 T=1024 ALL, sequence {b}")
+        got = m.read_logits(b * T * V, T * V).reshape(1, T, V)
+        compare(got, oracle.forward(ocfg(cfg), params, tk[b:b + 1], oracle.ALL),
+                what=f"ALL seq {b}")
+
+
+def test_gpt2_small_b17_t512(small):
+    """8704 rows: 68 row tiles leave the last round of the QKV (1224 tiles)
+    and fc (1632 tiles) products under 90 % full at 4 and at 3 workgroups
+    per CU, so both take the K=32 two-per-CU GEMM variant."""
+    cfg, params, m = small
+    tk = oracle.lcg_tokens(17 * 512, cfg.vocab_size, seed=777).reshape(17, 512)
+    say("small B=17 T=512")
+    compare(m.forward(tk, cngpt_amd.LAST), oracle.forward(ocfg(cfg), params, tk), what="LAST")
+    say("small B=17 T=512 ALL, sequence 16")
+    got = m.forward(tk, cngpt_amd.ALL)[16:]
+    compare(got, oracle.forward(ocfg(cfg), params, tk[16:], oracle.ALL), what="ALL seq 16")
+
+
 def test_resident_path_matches(small):
     cfg, params, m = small
     tk = oracle.lcg_tokens(2 * 128, cfg.vocab_size, seed=5).reshape(2, 128)
