@@ -97,6 +97,9 @@ def decode_bytes(cfg, params_n: int, B: int, first_pos: int, steps: int) -> floa
     return total
 
 
+PATHS = {cngpt_amd.DECODE_KERNELS: "kernels", cngpt_amd.DECODE_PERSISTENT: "persistent"}
+
+
 def decode(m: cngpt_amd.Model, cfg, B: int, prompt_len: int, steps: int, draws=None):
     """`steps` single-token decode steps for B sequences after a prompt_len
     prompt, as one cngpt_hip_generate call; greedy, or temp 0.8 / top-k 40
@@ -112,7 +115,7 @@ def decode(m: cngpt_amd.Model, cfg, B: int, prompt_len: int, steps: int, draws=N
     m.synchronize()
     t0 = time.perf_counter()
     m.generate(steps + 1, **kw)
-    return time.perf_counter() - t0
+    return time.perf_counter() - t0, PATHS.get(m.decode_path(), "none")
 
 
 def reference_shape(m: cngpt_amd.Model, iters: int = 20):
@@ -206,14 +209,20 @@ def main():
     m = cngpt_amd.Model(cfg, params)
 
     if args.decode_only:
-        dec_dt = decode(m, cfg, dB, prompt, dsteps)
+        dec_dt, dec_path = decode(m, cfg, dB, prompt, dsteps)
         dec_bytes = decode_bytes(cfg, params.size, dB, prompt, dsteps)
+        pers_ms = None
+        if dB == 1:
+            m.set_decode_path(cngpt_amd.DECODE_PERSISTENT)
+            pers_dt, _ = decode(m, cfg, dB, prompt, dsteps)
+            pers_ms = round(pers_dt * 1e3 / dsteps, 4)
+            m.set_decode_path(cngpt_amd.DECODE_AUTO)
         draws = np.random.default_rng(7).random((dsteps + 1) * dB).astype(np.float32)
-        samp_dt = decode(m, cfg, dB, prompt, dsteps, draws)
+        samp_dt, _ = decode(m, cfg, dB, prompt, dsteps, draws)
         # per-kernel-class split of the sampled steps (direct launches, HIP events)
         m.profile_reset()
         m.profile(True)
-        prof_dt = decode(m, cfg, dB, prompt, dsteps, draws)
+        prof_dt, _ = decode(m, cfg, dB, prompt, dsteps, draws)
         m.profile(False)
         prof = m.profile_read()
         m.close()
@@ -221,6 +230,8 @@ def main():
         print(json.dumps({"workload": name, "B": dB, "decode_tok_s": round(n * dB / dec_dt, 1),
                           "ms_per_step": round(dec_dt * 1e3 / n, 4),
                           "hbm_frac": round(dec_bytes / dec_dt / PEAK_HBM, 4),
+                          "path": dec_path,
+                          "persistent_ms_per_step": pers_ms,
                           "sampled_tok_s": round(n * dB / samp_dt, 1),
                           "graphs": os.environ.get("CNGPT_HIP_GRAPH", "1") != "0",
                           "evented_ms_per_step": round(prof_dt * 1e3 / n, 4),
@@ -238,10 +249,10 @@ def main():
     achieved = g["flops"] / (g["ms"] * 1e-3)
     gemm_share = g["ms"] / (dt * 1e3)
 
-    dec_dt = decode(m, cfg, dB, prompt, dsteps)
+    dec_dt, dec_path = decode(m, cfg, dB, prompt, dsteps)
     dec_bytes = decode_bytes(cfg, params.size, dB, prompt, dsteps)
     draws = np.random.default_rng(7).random((dsteps + 1) * dB).astype(np.float32)
-    samp_dt = decode(m, cfg, dB, prompt, dsteps, draws)
+    samp_dt, _ = decode(m, cfg, dB, prompt, dsteps, draws)
     ref_shape = reference_shape(m) if name == "small" else None
     m.close()
 
@@ -281,7 +292,7 @@ def main():
         "gemm_mfma_util_pct": round(100 * achieved / PEAK_FP32_MFMA, 2),
         "decode": {"tok_s": round(dsteps * dB / dec_dt, 1),
                    "ms_per_step": round(dec_dt * 1e3 / dsteps, 4),
-                   "prompt": prompt, "steps": dsteps, "B": dB, "sampling": "greedy",
+                   "prompt": prompt, "steps": dsteps, "B": dB, "sampling": "greedy", "path": dec_path,
                    "hbm": {"bound": "hbm", "achieved": round(dec_bytes / dec_dt / 1e9, 1),
                            "peak": PEAK_HBM / 1e9, "unit": "GB/s",
                            "frac": round(dec_bytes / dec_dt / PEAK_HBM, 4),

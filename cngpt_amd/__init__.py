@@ -25,9 +25,11 @@ LIB_PATH = os.path.join(_HERE, "libcngpt_hip.so")
 
 LAST, ALL = 0, 1
 (K_GEMM, K_GEMV, K_ATTN, K_ATTN_ROW, K_LAYERNORM, K_EMBED, K_GATHER, K_ARGMAX,
- K_SAMPLE) = range(9)
+ K_SAMPLE, K_STEP) = range(10)
 KERNEL_CLASSES = ["gemm", "gemv", "attn", "attn_row", "layernorm", "embed", "gather", "argmax",
-                  "sample"]
+                  "sample", "step"]
+# decode paths (include/cngpt_hip.h)
+DECODE_AUTO, DECODE_KERNELS, DECODE_PERSISTENT = 0, 1, 2
 
 MAGIC = 0x434E4750
 VERSION = 1
@@ -74,7 +76,7 @@ EXPORTS = [
     "cngpt_hip_upload_tokens", "cngpt_hip_forward_resident", "cngpt_hip_synchronize",
     "cngpt_hip_read_logits", "cngpt_hip_logits_device", "cngpt_hip_decode_begin",
     "cngpt_hip_decode_step", "cngpt_hip_generate", "cngpt_hip_argmax", "cngpt_hip_sample",
-    "cngpt_hip_decode_length",
+    "cngpt_hip_decode_length", "cngpt_hip_set_decode_path", "cngpt_hip_decode_path",
     "cngpt_hip_profile_enable", "cngpt_hip_profile_reset", "cngpt_hip_profile_read",
     "cngpt_hip_host_alloc", "cngpt_hip_host_free", "cngpt_hip_init_weights",
     "fast_init", "fast_free", "fast_set_threads", "gpt_forward_fast", "gpt_forward_fast_all",
@@ -114,6 +116,8 @@ def lib():
     L.cngpt_hip_argmax.argtypes = [_VP, _I]
     L.cngpt_hip_sample.argtypes = [_VP, ctypes.c_float, ctypes.c_int, _F, _I]
     L.cngpt_hip_decode_length.argtypes = [_VP]
+    L.cngpt_hip_set_decode_path.argtypes = [_VP, ctypes.c_int]
+    L.cngpt_hip_decode_path.argtypes = [_VP]
     L.cngpt_hip_profile_enable.argtypes = [_VP, ctypes.c_int]
     L.cngpt_hip_profile_reset.argtypes = [_VP]
     L.cngpt_hip_profile_read.argtypes = [_VP, ctypes.c_int, _D, _Lp, _D, _D]
@@ -302,6 +306,14 @@ class Model:
 
     def decode_length(self) -> int:
         return lib().cngpt_hip_decode_length(self._h)
+
+    def set_decode_path(self, path: int) -> None:
+        """DECODE_AUTO, DECODE_KERNELS or DECODE_PERSISTENT for later steps."""
+        _check(lib().cngpt_hip_set_decode_path(self._h, path), "set_decode_path")
+
+    def decode_path(self) -> int:
+        """Path of the last decode step (DECODE_KERNELS / DECODE_PERSISTENT)."""
+        return lib().cngpt_hip_decode_path(self._h)
 
     # -- timing ---------------------------------------------------------
     def profile(self, on: bool) -> None:

@@ -41,11 +41,6 @@ int fail(const char* fmt, ...) {
                         __LINE__);                                                      \
     } while (0)
 
-struct LayerW {
-    const float *ln1_w, *ln1_b, *attn_w, *attn_b, *proj_w, *proj_b;
-    const float *ln2_w, *ln2_b, *fc_w, *fc_b, *mlp_w, *mlp_b;
-};
-
 struct ProfRec {
     int cls;
     hipEvent_t a, b;
@@ -67,6 +62,7 @@ struct cngpt_hip_ctx {
     long n_params = 0;
     const float *wte = nullptr, *wpe = nullptr, *lnf_w = nullptr, *lnf_b = nullptr;
     std::vector<LayerW> layers;
+    LayerW* d_layers = nullptr;  // device copy of layers (persistent decode)
 
     // activation arena: one allocation, carved below
     char* d_act = nullptr;
@@ -88,6 +84,13 @@ struct cngpt_hip_ctx {
     float* prob = nullptr;       // [B][ldp] sampling scratch
     long ldp = 0;
     int pos_host = 0;            // staging for the position upload
+    unsigned* pbar = nullptr;    // grid-barrier counters of the persistent decode
+
+    // decode path: CNGPT_DECODE_AUTO / _KERNELS / _PERSISTENT (set_decode_path;
+    // CNGPT_HIP_PERSIST=0 in the environment at create time selects _KERNELS)
+    int decode_path = CNGPT_DECODE_AUTO;
+    int last_path = 0;           // path of the last decode step
+    int persist_G = -1;          // workgroups of the persistent launch (-1: not queried)
 
     // the decode step as a replayable graph (kernels only); CNGPT_HIP_GRAPH=0
     // in the environment at create time selects direct launches instead
@@ -333,7 +336,7 @@ int ensure_arena(cngpt_hip_ctx* h, int B, int T, int all, int kv) {
     const size_t rows = (size_t)nB * nT;
     const size_t qkv_rows = std::max(rows, L * nB * (size_t)nKV);
     const int kps = attn_dec_keys_per_split(c.n_embd / c.n_head);
-    const int splits = (c.block_size + kps - 1) / kps;
+    const int splits = std::max((c.block_size + kps - 1) / kps, persist_max_splits());
     size_t sz[24], total = 0;
     int n = 0;
     sz[n++] = rows * sizeof(int);             // tok
@@ -355,6 +358,7 @@ int ensure_arena(cngpt_hip_ctx* h, int B, int T, int all, int kv) {
     sz[n++] = nB * C * 4;                     // lnc
     sz[n++] = nB * C * 4;                     // aoutc
     sz[n++] = nB * 4 * C * 4;                 // hidc
+    sz[n++] = (size_t)persist_barrier_words() * sizeof(unsigned);  // pbar
     for (int i = 0; i < n; i++) total += align_up(sz[i]);
 
     if (h->d_act) {
@@ -399,6 +403,7 @@ int ensure_arena(cngpt_hip_ctx* h, int B, int T, int all, int kv) {
     h->lnc = (float*)take(sz[n++]);
     h->aoutc = (float*)take(sz[n++]);
     h->hidc = (float*)take(sz[n++]);
+    h->pbar = (unsigned*)take(sz[n++]);
     h->capB = nB; h->capT = nT; h->capAll = nAll; h->capKV = nKV;
     HIP_TRY(hipMemsetAsync(h->dev_err, 0, 4 * sizeof(int), h->stream));
     return 0;
@@ -552,6 +557,53 @@ int run_decode_step(cngpt_hip_ctx* h) {
         h->logits_count = (size_t)h->kvB * h->cfg.vocab_size;
     }
     h->kvLen += 1;
+    h->last_path = CNGPT_DECODE_KERNELS;
+    return 0;
+}
+
+// Whether the next decode steps run as one persistent launch: one cached
+// sequence, head size 64, widths the kernel supports, cooperative launch.
+bool persist_usable(cngpt_hip_ctx* h) {
+    if (h->decode_path != CNGPT_DECODE_PERSISTENT || h->kvB != 1) return false;
+    if (h->persist_G < 0) h->persist_G = persist_workgroups(h->device);
+    const cngpt_hip_config& c = h->cfg;
+    return h->persist_G > 0 &&
+           persist_supported(c.n_embd, c.n_head, c.vocab_size, h->capKV, h->persist_G);
+}
+
+int persist_refused(cngpt_hip_ctx* h) {
+    return fail("persistent decode needs one cached sequence (B=%d), head size 64, n_embd <= "
+                "1024 and a device with cooperative launch", h->kvB);
+}
+
+// n greedy decode steps of the single cached sequence as one launch.
+int run_persist(cngpt_hip_ctx* h, int n) {
+    const cngpt_hip_config& c = h->cfg;
+    const double C = c.n_embd, L = c.n_layer, V = c.vocab_size;
+    PersistArgs a{};
+    a.layers = h->d_layers;
+    a.wte = h->wte; a.wpe = h->wpe; a.lnf_w = h->lnf_w; a.lnf_b = h->lnf_b;
+    a.L = c.n_layer; a.C = c.n_embd; a.H = c.n_head; a.V = c.vocab_size; a.cap = h->capKV;
+    a.cache = h->qkv; a.x = h->xc; a.hid = h->hidc; a.apart = h->attn_part;
+    a.am_v = h->am_part_v; a.am_i = h->am_part_i; a.logits = h->logits; a.hist = h->hist;
+    a.pos = h->pos; a.tok = h->next_tok; a.bar = h->pbar; a.err = h->dev_err;
+    a.n_steps = n;
+    a.scale = 1.0f / sqrtf((float)(c.n_embd / c.n_head));
+    // weights + K/V rows read per step (keys 0..t), summed over the steps
+    double bytes = 0.0, flops = 0.0;
+    for (int i = 0; i < n; i++) {
+        const double t = h->kvLen + i;
+        bytes += 4.0 * (L * (12.0 * C * C + 13.0 * C) + V * C + 2.0 * C) + 8.0 * L * C * (t + 1.0);
+        flops += 2.0 * (L * 12.0 * C * C + V * C) + 4.0 * L * C * (t + 1.0);
+    }
+    {
+        Timed tm(h, CNGPT_K_STEP, flops, bytes);
+        HIP_TRY(launch_decode_persist(a, h->persist_G, h->stream));
+    }
+    h->kvLen += n;
+    h->curB = 1; h->curT = 1; h->curMode = CNGPT_LAST;
+    h->logits_count = (size_t)c.vocab_size;
+    h->last_path = CNGPT_DECODE_PERSISTENT;
     return 0;
 }
 
@@ -574,6 +626,7 @@ int check_dev_err(cngpt_hip_ctx* h) {
     HIP_TRY(hipStreamSynchronize(h->stream));
     if (e) {
         HIP_TRY(hipMemsetAsync(h->dev_err, 0, sizeof(int), h->stream));
+        if (e & 2) return fail("persistent decode: a grid barrier timed out");
         return fail("device-resident token ids outside [0, %d) were clamped", h->cfg.vocab_size);
     }
     return 0;
@@ -606,6 +659,8 @@ int cngpt_hip_create(int device, cngpt_hip_ctx** out) {
     h->device = device;
     const char* g = getenv("CNGPT_HIP_GRAPH");
     h->use_graph = !(g && g[0] == '0');
+    const char* pp = getenv("CNGPT_HIP_PERSIST");
+    if (pp && pp[0] == '0') h->decode_path = CNGPT_DECODE_KERNELS;
     if (hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking) != hipSuccess) {
         delete h;
         return fail("hipStreamCreate failed");
@@ -622,6 +677,7 @@ void cngpt_hip_destroy(cngpt_hip_ctx* h) {
     for (hipEvent_t e : h->pool) (void)hipEventDestroy(e);
     if (h->d_act) (void)hipFree(h->d_act);
     if (h->d_params) (void)hipFree(h->d_params);
+    if (h->d_layers) (void)hipFree(h->d_layers);
     if (h->stream) (void)hipStreamDestroy(h->stream);
     delete h;
 }
@@ -688,6 +744,17 @@ int cngpt_hip_load_params(cngpt_hip_ctx* h, const cngpt_hip_config* cfg, const f
     }
     h->lnf_w = p; p += C;
     h->lnf_b = p;
+    const size_t lbytes = (size_t)cfg->n_layer * sizeof(LayerW);
+    if (!same_shape || !h->d_layers) {
+        if (h->d_layers) HIP_TRY(hipFree(h->d_layers));
+        h->d_layers = nullptr;
+        if (hipMalloc(&h->d_layers, lbytes) != hipSuccess) {
+            (void)hipGetLastError();
+            h->d_layers = nullptr;
+            return fail("layer table allocation failed");
+        }
+    }
+    HIP_TRY(hipMemcpy(h->d_layers, h->layers.data(), lbytes, hipMemcpyHostToDevice));
     h->have_params = true;
     return 0;
 }
@@ -809,13 +876,15 @@ int cngpt_hip_decode_step(cngpt_hip_ctx* h, const int* tokens, float* logits_out
         // the caller's buffer may be reused as soon as this returns
         HIP_TRY(hipStreamSynchronize(h->stream));
     }
-    if (run_decode_step(h)) return -1;
+    const bool persist = persist_usable(h);
+    if (!persist && h->decode_path == CNGPT_DECODE_PERSISTENT) return persist_refused(h);
+    if (persist ? run_persist(h, 1) : run_decode_step(h)) return -1;
     if (logits_out) {
         HIP_TRY(hipMemcpyAsync(logits_out, h->logits, (size_t)B * h->cfg.vocab_size * sizeof(float),
                                hipMemcpyDeviceToHost, h->stream));
         HIP_TRY(hipStreamSynchronize(h->stream));
     }
-    return 0;
+    return persist ? check_dev_err(h) : 0;
 }
 
 int cngpt_hip_generate(cngpt_hip_ctx* h, int n_new, float temperature, int top_k,
@@ -834,9 +903,15 @@ int cngpt_hip_generate(cngpt_hip_ctx* h, int n_new, float temperature, int top_k
         HIP_TRY(hipMemcpyAsync(h->draws, draws, (size_t)n_new * B * sizeof(float),
                                hipMemcpyHostToDevice, h->stream));
     if (draws && run_sample(h, h->draws, temperature, top_k)) return -1;
-    for (int i = 1; i < n_new; i++) {
-        if (run_decode_step(h)) return -1;
-        if (draws && run_sample(h, h->draws + (size_t)i * B, temperature, top_k)) return -1;
+    const bool persist = !draws && persist_usable(h);
+    if (!draws && !persist && h->decode_path == CNGPT_DECODE_PERSISTENT) return persist_refused(h);
+    if (persist) {
+        if (n_new > 1 && run_persist(h, n_new - 1)) return -1;
+    } else {
+        for (int i = 1; i < n_new; i++) {
+            if (run_decode_step(h)) return -1;
+            if (draws && run_sample(h, h->draws + (size_t)i * B, temperature, top_k)) return -1;
+        }
     }
     // tokens fed at positions start.. are the first n_new - 1; the last is in next_tok
     if (n_new > 1)
@@ -891,6 +966,17 @@ void* cngpt_hip_host_alloc(size_t bytes) {
     }
     return p;
 }
+
+int cngpt_hip_set_decode_path(cngpt_hip_ctx* h, int path) {
+    if (!h) return fail("null handle");
+    if (path != CNGPT_DECODE_AUTO && path != CNGPT_DECODE_KERNELS &&
+        path != CNGPT_DECODE_PERSISTENT)
+        return fail("bad decode path %d", path);
+    h->decode_path = path;
+    return 0;
+}
+
+int cngpt_hip_decode_path(cngpt_hip_ctx* h) { return h ? h->last_path : -1; }
 
 void cngpt_hip_host_free(void* p) {
     if (p) (void)hipHostFree(p);

@@ -126,6 +126,44 @@ hipError_t launch_argmax_rows(const float* logits, int rows, int V, int* out, in
 hipError_t launch_sample(const float* logits, int rows, int V, float temp, int top_k,
                          const float* r_draw, float* prob, long ldp, int* out, hipStream_t s);
 
+// persist.hip
+// Parameter pointers of one layer (the carve order of assign_weights).
+struct LayerW {
+    const float *ln1_w, *ln1_b, *attn_w, *attn_b, *proj_w, *proj_b;
+    const float *ln2_w, *ln2_b, *fc_w, *fc_b, *mlp_w, *mlp_b;
+};
+// Greedy decode of one sequence (B = 1, head size 64) for n_steps steps as
+// one cooperative launch: feeds *tok at position *pos, leaves the logits of
+// the last step in logits, the tokens fed in hist[pos..], the next token in
+// *tok and the next position in *pos. *err |= 1 for a token outside
+// [0, V) (clamped), |= 2 when a grid barrier timed out.
+struct PersistArgs {
+    const LayerW* layers;   // device array [L]
+    const float *wte, *wpe, *lnf_w, *lnf_b;
+    int L, C, H, V, cap;
+    float* cache;           // KV cache rows [L][cap][3C]
+    float* x;               // [C] residual stream
+    float* hid;             // [4C]
+    float* apart;           // [H][persist_max_splits()][68] attention partials
+    float* am_v;            // [workgroups] argmax partials
+    int* am_i;
+    float* logits;          // [V]
+    int* hist;              // [cap]
+    int* pos;
+    int* tok;
+    unsigned* bar;          // persist_barrier_words() words, zeroed by the launcher
+    int* err;
+    int n_steps;
+    float scale;            // 1 / sqrt(head size)
+};
+// Workgroups of the launch (one per CU, a multiple of 8), 0 if the device
+// has no cooperative launch.
+int persist_workgroups(int device);
+bool persist_supported(int C, int H, int V, int cap, int G);
+int persist_max_splits();
+int persist_barrier_words();
+hipError_t launch_decode_persist(const PersistArgs& a, int G, hipStream_t s);
+
 // attention.hip
 // qkv rows hold [q | k | v] (3C floats); sequence b's row t sits at
 // qkv + (b * seq_stride + t) * 3C. out row (b*T + t) gets the merged heads.

@@ -48,8 +48,16 @@ enum {
     CNGPT_K_GATHER = 6,
     CNGPT_K_ARGMAX = 7,
     CNGPT_K_SAMPLE = 8,      /* top-k sampling */
-    CNGPT_K_COUNT = 9
+    CNGPT_K_STEP = 9,        /* whole decode steps in one persistent launch */
+    CNGPT_K_COUNT = 10
 };
+
+/* How decode steps run. KERNELS: one replayed graph of per-stage kernels
+ * per step (any batch). PERSISTENT: the greedy steps of one sequence as one
+ * cooperative launch whose workgroups meet at grid barriers between stages
+ * (B = 1, head size 64, n_embd <= 1024). AUTO: KERNELS (the persistent
+ * launch is opt-in while it is slower on GPT-2 small). */
+enum { CNGPT_DECODE_AUTO = 0, CNGPT_DECODE_KERNELS = 1, CNGPT_DECODE_PERSISTENT = 2 };
 
 /* Last error message of the calling thread ("" if none). */
 const char *cngpt_hip_last_error(void);
@@ -128,6 +136,14 @@ int  cngpt_hip_sample(cngpt_hip_ctx *h, float temperature, int top_k, const floa
                       int *out_tokens);
 /* Positions held in the KV cache per sequence (prompt + steps). */
 int  cngpt_hip_decode_length(cngpt_hip_ctx *h);
+/* Decode path for the following steps (CNGPT_DECODE_*; the default is AUTO,
+ * or KERNELS when CNGPT_HIP_PERSIST=0 was set at create time). Asking for
+ * PERSISTENT makes a step that cannot run that way fail. No reference
+ * counterpart: the reference has one CPU path. */
+int  cngpt_hip_set_decode_path(cngpt_hip_ctx *h, int path);
+/* The path the last decode step ran on (CNGPT_DECODE_KERNELS or
+ * CNGPT_DECODE_PERSISTENT; 0 before any step). */
+int  cngpt_hip_decode_path(cngpt_hip_ctx *h);
 
 /* Per-kernel-class timing with HIP events on the handle's stream.
  * While enabled, every launch is bracketed by an event pair; read returns

@@ -1,0 +1,118 @@
+"""Single-sequence greedy decode as one persistent launch (the stages of a
+step as phases separated by grid barriers) vs the oracle and vs the
+kernel-per-stage decode.
+
+Reference values as in test_decode_gpu.py: without window truncation the
+logits of decode step i are row prompt+i-1 of one all-positions forward
+over the final sequence (src/model.c:991-1016 reruns the prefix instead).
+"""
+import numpy as np
+import pytest
+
+import cngpt_amd
+import oracle
+from test_parity_gpu import compare, ocfg, randomize, say
+
+pytestmark = pytest.mark.gpu
+
+# widths 256 / 512 / 768 / 1024 take 1 / 2 / 3 / 4 float4 per lane per column
+CASES = {
+    "c256_v1000": cngpt_amd.Config(2, 4, 256, 1000, 128),
+    "c512_v3000": cngpt_amd.Config(2, 8, 512, 3000, 256),
+    "c768_v50257": cngpt_amd.Config(3, 12, 768, 50257, 1024),
+    "c1024_v50257": cngpt_amd.Config(2, 16, 1024, 50257, 1024),
+}
+
+
+def model(cfg, seed):
+    params = randomize(cfg, cngpt_amd.init_weights(cfg, seed), seed + 1)
+    return params, cngpt_amd.Model(cfg, params)
+
+
+@pytest.mark.parametrize("name", list(CASES))
+def test_persistent_teacher_forced(name):
+    """Host-fed tokens, one launch per step; 70 steps cross the 64-key
+    boundaries of the attention splits."""
+    cfg = CASES[name]
+    params, m = model(cfg, 7)
+    T0, steps = 5, 70
+    seq = np.random.default_rng(3).integers(0, cfg.vocab_size, size=(1, T0 + steps),
+                                            dtype=np.int32)
+    ref = oracle.forward(ocfg(cfg), params, seq, oracle.ALL)[:, T0 - 1:]
+    with m:
+        m.set_decode_path(cngpt_amd.DECODE_PERSISTENT)
+        say(f"{name}: persistent teacher-forced, {steps} steps")
+        got = [m.decode_begin(seq[:, :T0], capacity=T0 + steps)]
+        for t in range(T0, T0 + steps):
+            got.append(m.decode_step(seq[:, t]))
+            assert m.decode_path() == cngpt_amd.DECODE_PERSISTENT
+        assert m.decode_length() == T0 + steps
+    compare(np.stack(got, 1), ref, what=f"{name} persistent")
+
+
+def test_persistent_generate_matches_steps_kernels_and_oracle():
+    """GPT-2 small width at 3 layers, a 900-token prompt (16 attention
+    splits): one launch of 99 steps = 99 launches of one step (bitwise),
+    = the kernel-per-stage decode and the oracle up to near-ties."""
+    cfg = CASES["c768_v50257"]
+    params, m = model(cfg, 11)
+    prompt = np.random.default_rng(5).integers(0, cfg.vocab_size, size=(1, 900), dtype=np.int32)
+    n = 100
+    with m:
+        m.set_decode_path(cngpt_amd.DECODE_PERSISTENT)
+        say("c768: generate 100 after a 900-token prompt, persistent")
+        m.decode_begin(prompt, capacity=900 + n - 1)
+        gen = m.generate(n)
+        assert m.decode_path() == cngpt_amd.DECODE_PERSISTENT
+        say("c768: the same, one step per launch")
+        m.decode_begin(prompt, capacity=900 + n - 1)
+        steps = [m.decode_step(None) for _ in range(n - 1)]
+        step_toks = np.concatenate([np.stack([s.argmax(-1) for s in steps], 1)], axis=1)
+        assert np.array_equal(gen[:, 1:], step_toks), "single-launch vs per-step tokens"
+        say("c768: the same on the kernel-per-stage path")
+        m.set_decode_path(cngpt_amd.DECODE_KERNELS)
+        m.decode_begin(prompt, capacity=900 + n - 1)
+        kern = m.generate(n)
+        assert m.decode_path() == cngpt_amd.DECODE_KERNELS
+    seq = np.concatenate([prompt, gen[:, :-1]], axis=1)
+    ref = oracle.forward(ocfg(cfg), params, seq, oracle.ALL)[:, 899:]
+    srt = np.sort(ref, axis=-1)
+    tie = (srt[..., -1] - srt[..., -2]) < 1e-4
+    first = np.argmax(gen != kern) if not np.array_equal(gen, kern) else n
+    # the streams agree up to the first near-tie (after one, they may diverge)
+    assert first == n or tie[0, first], ("persistent vs kernels diverge without a tie", first)
+    assert np.array_equal(np.where(tie, 0, ref.argmax(-1)), np.where(tie, 0, gen))
+    compare(np.stack(steps, 1), ref[:, 1:], what="c768 per-step logits")
+
+
+def test_persistent_gpt2_small_long_context():
+    """GPT-2 small at full depth, the last 24 positions of the 1024-token
+    window (keys up to 1023)."""
+    cfg = cngpt_amd.GPT2_SMALL
+    params = cngpt_amd.init_weights(cfg, 1234)
+    seq = oracle.lcg_tokens(1024, cfg.vocab_size, seed=21).reshape(1, 1024)
+    ref = oracle.forward(ocfg(cfg), params, seq, oracle.ALL)[:, 999:]
+    with cngpt_amd.Model(cfg, params) as m:
+        m.set_decode_path(cngpt_amd.DECODE_PERSISTENT)
+        say("small: persistent decode at positions 1000..1023")
+        got = [m.decode_begin(seq[:, :1000], capacity=1024)]
+        for t in range(1000, 1024):
+            got.append(m.decode_step(seq[:, t]))
+        assert m.decode_path() == cngpt_amd.DECODE_PERSISTENT
+    compare(np.stack(got, 1), ref, what="small long context")
+
+
+def test_persistent_refuses_batches():
+    cfg = CASES["c256_v1000"]
+    params, m = model(cfg, 3)
+    prompt = np.zeros((2, 4), np.int32)
+    with m:
+        m.decode_begin(prompt, capacity=16)
+        m.set_decode_path(cngpt_amd.DECODE_PERSISTENT)
+        with pytest.raises(cngpt_amd.CngptError, match="persistent"):
+            m.decode_step(None)
+        m.set_decode_path(cngpt_amd.DECODE_AUTO)
+        m.decode_step(None)
+        assert m.decode_path() == cngpt_amd.DECODE_KERNELS
+        with pytest.raises(cngpt_amd.CngptError):
+            m.set_decode_path(7)
