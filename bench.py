@@ -211,12 +211,9 @@ def main():
     if args.decode_only:
         dec_dt, dec_path = decode(m, cfg, dB, prompt, dsteps)
         dec_bytes = decode_bytes(cfg, params.size, dB, prompt, dsteps)
-        pers_ms = None
-        if dB == 1:
-            m.set_decode_path(cngpt_amd.DECODE_PERSISTENT)
-            pers_dt, _ = decode(m, cfg, dB, prompt, dsteps)
-            pers_ms = round(pers_dt * 1e3 / dsteps, 4)
-            m.set_decode_path(cngpt_amd.DECODE_AUTO)
+        m.set_decode_path(cngpt_amd.DECODE_KERNELS)
+        kern_dt, _ = decode(m, cfg, dB, prompt, dsteps)
+        m.set_decode_path(cngpt_amd.DECODE_AUTO)
         draws = np.random.default_rng(7).random((dsteps + 1) * dB).astype(np.float32)
         samp_dt, _ = decode(m, cfg, dB, prompt, dsteps, draws)
         # per-kernel-class split of the sampled steps (direct launches, HIP events)
@@ -231,7 +228,7 @@ def main():
                           "ms_per_step": round(dec_dt * 1e3 / n, 4),
                           "hbm_frac": round(dec_bytes / dec_dt / PEAK_HBM, 4),
                           "path": dec_path,
-                          "persistent_ms_per_step": pers_ms,
+                          "kernels_path_ms_per_step": round(kern_dt * 1e3 / n, 4),
                           "sampled_tok_s": round(n * dB / samp_dt, 1),
                           "graphs": os.environ.get("CNGPT_HIP_GRAPH", "1") != "0",
                           "evented_ms_per_step": round(prof_dt * 1e3 / n, 4),
@@ -251,6 +248,12 @@ def main():
 
     dec_dt, dec_path = decode(m, cfg, dB, prompt, dsteps)
     dec_bytes = decode_bytes(cfg, params.size, dB, prompt, dsteps)
+    kern_ms = None
+    if dec_path != "kernels":
+        m.set_decode_path(cngpt_amd.DECODE_KERNELS)
+        kern_dt, _ = decode(m, cfg, dB, prompt, dsteps)
+        kern_ms = round(kern_dt * 1e3 / dsteps, 4)
+        m.set_decode_path(cngpt_amd.DECODE_AUTO)
     draws = np.random.default_rng(7).random((dsteps + 1) * dB).astype(np.float32)
     samp_dt, _ = decode(m, cfg, dB, prompt, dsteps, draws)
     ref_shape = reference_shape(m) if name == "small" else None
@@ -293,6 +296,7 @@ def main():
         "decode": {"tok_s": round(dsteps * dB / dec_dt, 1),
                    "ms_per_step": round(dec_dt * 1e3 / dsteps, 4),
                    "prompt": prompt, "steps": dsteps, "B": dB, "sampling": "greedy", "path": dec_path,
+                   "kernels_path_ms_per_step": kern_ms,
                    "hbm": {"bound": "hbm", "achieved": round(dec_bytes / dec_dt / 1e9, 1),
                            "peak": PEAK_HBM / 1e9, "unit": "GB/s",
                            "frac": round(dec_bytes / dec_dt / PEAK_HBM, 4),

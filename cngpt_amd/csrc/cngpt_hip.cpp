@@ -84,7 +84,8 @@ struct cngpt_hip_ctx {
     float* prob = nullptr;       // [B][ldp] sampling scratch
     long ldp = 0;
     int pos_host = 0;            // staging for the position upload
-    unsigned* pbar = nullptr;    // grid-barrier counters of the persistent decode
+    unsigned long long* ptag = nullptr;  // exchange words of the persistent decode
+    unsigned ptag_next = 0;      // next unused tag (tags only grow until the words are cleared)
 
     // decode path: CNGPT_DECODE_AUTO / _KERNELS / _PERSISTENT (set_decode_path;
     // CNGPT_HIP_PERSIST=0 in the environment at create time selects _KERNELS)
@@ -336,7 +337,7 @@ int ensure_arena(cngpt_hip_ctx* h, int B, int T, int all, int kv) {
     const size_t rows = (size_t)nB * nT;
     const size_t qkv_rows = std::max(rows, L * nB * (size_t)nKV);
     const int kps = attn_dec_keys_per_split(c.n_embd / c.n_head);
-    const int splits = std::max((c.block_size + kps - 1) / kps, persist_max_splits());
+    const int splits = (c.block_size + kps - 1) / kps;
     size_t sz[24], total = 0;
     int n = 0;
     sz[n++] = rows * sizeof(int);             // tok
@@ -358,7 +359,7 @@ int ensure_arena(cngpt_hip_ctx* h, int B, int T, int all, int kv) {
     sz[n++] = nB * C * 4;                     // lnc
     sz[n++] = nB * C * 4;                     // aoutc
     sz[n++] = nB * 4 * C * 4;                 // hidc
-    sz[n++] = (size_t)persist_barrier_words() * sizeof(unsigned);  // pbar
+    sz[n++] = (size_t)persist_tagged_words(c.n_embd, c.n_head) * 8;  // ptag
     for (int i = 0; i < n; i++) total += align_up(sz[i]);
 
     if (h->d_act) {
@@ -403,7 +404,9 @@ int ensure_arena(cngpt_hip_ctx* h, int B, int T, int all, int kv) {
     h->lnc = (float*)take(sz[n++]);
     h->aoutc = (float*)take(sz[n++]);
     h->hidc = (float*)take(sz[n++]);
-    h->pbar = (unsigned*)take(sz[n++]);
+    h->ptag = (unsigned long long*)take(sz[n++]);
+    h->ptag_next = 0;
+    HIP_TRY(hipMemsetAsync(h->ptag, 0, sz[n - 1], h->stream));
     h->capB = nB; h->capT = nT; h->capAll = nAll; h->capKV = nKV;
     HIP_TRY(hipMemsetAsync(h->dev_err, 0, 4 * sizeof(int), h->stream));
     return 0;
@@ -564,7 +567,7 @@ int run_decode_step(cngpt_hip_ctx* h) {
 // Whether the next decode steps run as one persistent launch: one cached
 // sequence, head size 64, widths the kernel supports, cooperative launch.
 bool persist_usable(cngpt_hip_ctx* h) {
-    if (h->decode_path != CNGPT_DECODE_PERSISTENT || h->kvB != 1) return false;
+    if (h->decode_path == CNGPT_DECODE_KERNELS || h->kvB != 1) return false;
     if (h->persist_G < 0) h->persist_G = persist_workgroups(h->device);
     const cngpt_hip_config& c = h->cfg;
     return h->persist_G > 0 &&
@@ -573,7 +576,7 @@ bool persist_usable(cngpt_hip_ctx* h) {
 
 int persist_refused(cngpt_hip_ctx* h) {
     return fail("persistent decode needs one cached sequence (B=%d), head size 64, n_embd <= "
-                "1024 and a device with cooperative launch", h->kvB);
+                "768 and a device with cooperative launch", h->kvB);
 }
 
 // n greedy decode steps of the single cached sequence as one launch.
@@ -584,10 +587,19 @@ int run_persist(cngpt_hip_ctx* h, int n) {
     a.layers = h->d_layers;
     a.wte = h->wte; a.wpe = h->wpe; a.lnf_w = h->lnf_w; a.lnf_b = h->lnf_b;
     a.L = c.n_layer; a.C = c.n_embd; a.H = c.n_head; a.V = c.vocab_size; a.cap = h->capKV;
-    a.cache = h->qkv; a.x = h->xc; a.hid = h->hidc; a.apart = h->attn_part;
-    a.am_v = h->am_part_v; a.am_i = h->am_part_i; a.logits = h->logits; a.hist = h->hist;
-    a.pos = h->pos; a.tok = h->next_tok; a.bar = h->pbar; a.err = h->dev_err;
+    a.cache = h->qkv; a.tagged = h->ptag;
+    a.logits = h->logits; a.hist = h->hist;
+    a.pos = h->pos; a.tok = h->next_tok; a.err = h->dev_err;
     a.n_steps = n;
+    // tags only grow; before they would wrap, clear the words and restart
+    const unsigned need = persist_tags(c.n_layer, n);
+    if (h->ptag_next > 0xF0000000u - need) {
+        HIP_TRY(hipMemsetAsync(h->ptag, 0,
+                               (size_t)persist_tagged_words(c.n_embd, c.n_head) * 8, h->stream));
+        h->ptag_next = 0;
+    }
+    a.tag0 = h->ptag_next;
+    h->ptag_next += need;
     a.scale = 1.0f / sqrtf((float)(c.n_embd / c.n_head));
     // weights + K/V rows read per step (keys 0..t), summed over the steps
     double bytes = 0.0, flops = 0.0;
@@ -626,7 +638,7 @@ int check_dev_err(cngpt_hip_ctx* h) {
     HIP_TRY(hipStreamSynchronize(h->stream));
     if (e) {
         HIP_TRY(hipMemsetAsync(h->dev_err, 0, sizeof(int), h->stream));
-        if (e & 2) return fail("persistent decode: a grid barrier timed out");
+        if (e & 2) return fail("persistent decode: a wait for a value of another workgroup timed out");
         return fail("device-resident token ids outside [0, %d) were clamped", h->cfg.vocab_size);
     }
     return 0;

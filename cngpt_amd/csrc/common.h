@@ -30,6 +30,36 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// Sum / max over the 64 lanes with DPP lane moves inside each row of 16
+// (xor 1, xor 2, half-row mirror, row mirror) and the four row results read
+// as scalars: a few cycles per step instead of an LDS round trip per
+// shuffle. Every lane of the wavefront must be active. The result is the
+// same in every lane.
+#define CNGPT_DPP(v, ctrl)                                                                  \
+    __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, (v)), (ctrl), \
+                                                       0xF, 0xF, false))
+__device__ __forceinline__ float row_sum16(float v) {
+    v += CNGPT_DPP(v, 0xB1);   // quad_perm [1,0,3,2]
+    v += CNGPT_DPP(v, 0x4E);   // quad_perm [2,3,0,1]
+    v += CNGPT_DPP(v, 0x141);  // row_half_mirror
+    v += CNGPT_DPP(v, 0x140);  // row_mirror
+    return v;
+}
+__device__ __forceinline__ float lane_f(float v, int l) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    v = row_sum16(v);
+    return (lane_f(v, 0) + lane_f(v, 16)) + (lane_f(v, 32) + lane_f(v, 48));
+}
+__device__ __forceinline__ float wave_max_dpp(float v) {
+    v = fmaxf(v, CNGPT_DPP(v, 0xB1));
+    v = fmaxf(v, CNGPT_DPP(v, 0x4E));
+    v = fmaxf(v, CNGPT_DPP(v, 0x141));
+    v = fmaxf(v, CNGPT_DPP(v, 0x140));
+    return fmaxf(fmaxf(lane_f(v, 0), lane_f(v, 16)), fmaxf(lane_f(v, 32), lane_f(v, 48)));
+}
+
 // GELU, tanh form (the formula of the reference's ops.h:56-58), with the
 // device library's tanhf.
 __device__ __forceinline__ float gelu_tanh(float x) {

@@ -136,32 +136,31 @@ struct LayerW {
 // one cooperative launch: feeds *tok at position *pos, leaves the logits of
 // the last step in logits, the tokens fed in hist[pos..], the next token in
 // *tok and the next position in *pos. *err |= 1 for a token outside
-// [0, V) (clamped), |= 2 when a grid barrier timed out.
+// [0, V) (clamped), |= 2 when a wait for a value timed out.
 struct PersistArgs {
     const LayerW* layers;   // device array [L]
     const float *wte, *wpe, *lnf_w, *lnf_b;
     int L, C, H, V, cap;
     float* cache;           // KV cache rows [L][cap][3C]
-    float* x;               // [C] residual stream
-    float* hid;             // [4C]
-    float* apart;           // [H][persist_max_splits()][68] attention partials
-    float* am_v;            // [workgroups] argmax partials
-    int* am_i;
+    unsigned long long* tagged;  // persist_tagged_words(C, H) exchange words
+    unsigned tag0;          // tags of this launch: tag0 + 1 .. tag0 + persist_tags(L, n_steps)
     float* logits;          // [V]
     int* hist;              // [cap]
     int* pos;
     int* tok;
-    unsigned* bar;          // persist_barrier_words() words, zeroed by the launcher
     int* err;
     int n_steps;
     float scale;            // 1 / sqrt(head size)
 };
-// Workgroups of the launch (one per CU, a multiple of 8), 0 if the device
-// has no cooperative launch.
+// Workgroups of the launch (one per CU), 0 if the device has no
+// cooperative launch.
 int persist_workgroups(int device);
 bool persist_supported(int C, int H, int V, int cap, int G);
-int persist_max_splits();
-int persist_barrier_words();
+// Exchange words of the launch (zeroed once at allocation) and tags one
+// launch uses: tags only grow, so a word written by an earlier launch never
+// matches a tag this launch waits for.
+long persist_tagged_words(int C, int H);
+unsigned persist_tags(int L, int n_steps);
 hipError_t launch_decode_persist(const PersistArgs& a, int G, hipStream_t s);
 
 // attention.hip

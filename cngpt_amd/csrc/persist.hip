@@ -6,29 +6,33 @@
 // argmax (reference fast.c:245-329 at T = 1, with the KV cache). Launched
 // as separate kernels, every stage pays a kernel boundary plus the HBM
 // latency of its weights. Here the stages are phases of one cooperative
-// launch (one workgroup per CU) separated by grid barriers, and since no
-// weight depends on the data, each workgroup loads the next phase's weights
-// into registers as soon as the current phase's products are done: that
-// traffic overlaps the barrier. One launch runs any number of greedy steps
-// (the argmax of step s is the input of step s+1 without leaving the GPU).
+// launch (one workgroup per CU), and since no weight depends on the data,
+// each workgroup loads the next phase's weights into registers as soon as
+// the current phase's products are done, so that traffic overlaps the wait
+// for the next phase's input. One launch runs any number of greedy steps
+// (the argmax of step s feeds step s+1 without leaving the GPU).
 //
 // Workgroup: PW compute wavefronts + 1 control wavefront. The compute
 // wavefronts hold weights and form dot products; the control wavefront
-// sums their per-unit results in a fixed order, applies the epilogue,
-// stores, and runs the barrier (its own loads never wait behind weight
-// prefetches, which matters because loads complete in order).
+// sums their per-column results in a fixed order, applies the epilogue and
+// publishes the outputs.
 //
-// Grid barrier: each workgroup adds 1 (no return value) to the counter of
-// its XCD (blockIdx % 8); the control wavefront then polls all 8 counters
-// with 8 lanes until each reaches epoch * (workgroups per XCD). A poll
-// limit turns a stall into an error flag every workgroup sees and exits on.
+// Exchange between workgroups: every value a phase publishes is one 64-bit
+// word, the float in the low half and the tag of the phase that made it in
+// the high half, stored and loaded as agent-scope atomics (sc1: through
+// the XCD-private L2, which is not coherent across XCDs). A consumer reads
+// the words it needs until each carries the tag it expects, so there is no
+// grid barrier, no counter and no wait for store completion: a 64-bit word
+// is written whole, and the tag proves the value is the current one. Tags
+// grow monotonically over launches, and every buffer is rewritten only
+// after all consumers of its previous contents have provably read them (a
+// producer of version v+1 has consumed, through an all-to-all phase, data
+// made after every workgroup read version v). A poll limit turns a stall
+// into an error flag that every waiting workgroup sees and exits on.
 //
-// Coherence: the L2 of an XCD is not coherent with the others. Values made
-// and used inside the launch (x, hid, K/V/q row t, attention and argmax
-// partials) are stored and loaded with agent-scope atomics (sc1: through to
-// memory), and a producer waits for its stores to complete before it
-// arrives. Weights, and cache rows from before the launch or from earlier
-// steps (never read before they were written), use plain loads.
+// Cache rows written in a step are read by later steps with plain loads:
+// the writer's later loads wait for its stores, before it publishes the
+// values that the readers' progress depends on.
 #include <algorithm>
 
 #include "common.h"
@@ -38,25 +42,21 @@ namespace {
 
 constexpr int PW = 7;                  // compute wavefronts per workgroup
 constexpr int PT = (PW + 1) * 64;      // + the control wavefront: 2 per SIMD
-constexpr int NGRP = 8;                // barrier counters, one per XCD
-constexpr int CSTR = 32;               // counters 128 bytes apart
+constexpr int PHASES = 5;              // phases per layer
 constexpr int UPW = 4;                 // output columns per wavefront per phase
 constexpr int KPW = 16;                // attention keys per wavefront
 constexpr int LNE = 4;                 // LayerNorm elements per thread (C <= 4 * PT)
 constexpr int PMAXS = 16;              // attention splits per head
-constexpr long SPIN_LIMIT = 1L << 22;  // polls before a barrier gives up
-// Widths up to 256 * PMAXU channels (GPT-2 small and medium): the weights a
-// lane holds for one phase (UPW * U float4, U = ceil(C / 256)) then fit in
+constexpr long SPIN_LIMIT = 1L << 20;  // polls of one value before giving up
+// Widths up to 256 * PMAXU channels (GPT-2 small): the weights a lane holds
+// for two phases (2 * UPW * U float4, U = ceil(C / 256)) then fit in
 // registers beside the rest; wider models take the kernel-per-stage decode.
-constexpr int PMAXU = 4;
+constexpr int PMAXU = 3;
 
 __device__ __forceinline__ float ld_sc(const float* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ int ld_sc(const int* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ unsigned ld_sc(const unsigned* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void st_sc(float* p, float v) {
@@ -73,8 +73,54 @@ typedef __attribute__((address_space(1))) const f32x4 gf32x4;
 __device__ __forceinline__ float ldg(const float* p) { return *(gfloat*)p; }
 __device__ __forceinline__ f32x4 ldg4(const float* p) { return *(gf32x4*)p; }
 
-// Wait until this wavefront's stores have completed.
-__device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+typedef unsigned long long u64;
+// Exchange word: tag in the high half, the float's bits in the low half.
+__device__ __forceinline__ void put(u64* p, float v, unsigned tag) {
+    __hip_atomic_store(p, ((u64)tag << 32) | (u64)__float_as_uint(v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ u64 peek(const u64* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float wval(u64 w) { return __uint_as_float((unsigned)w); }
+__device__ __forceinline__ unsigned wtag(u64 w) { return (unsigned)(w >> 32); }
+
+// out[k] = value of base[idx[k]] once it carries `tag` (for k with need[k];
+// idx[k] is always a valid index). All first reads are in flight together;
+// only stragglers are read again. False after SPIN_LIMIT rounds or when
+// another workgroup has raised the abort word.
+// Only k < nk (uniform over the wavefront) are read at all.
+template <int N>
+__device__ __forceinline__ bool fetch(const u64* base, const int (&idx)[N], const bool (&need)[N],
+                                      unsigned tag, float (&out)[N], const u64* abortw,
+                                      int nk = N) {
+    u64 v[N];
+#pragma unroll
+    for (int k = 0; k < N; k++) v[k] = k < nk ? peek(base + idx[k]) : 0ull;
+    unsigned long long pend = 0;
+#pragma unroll
+    for (int k = 0; k < N; k++) {
+        out[k] = wval(v[k]);
+        if (need[k] && wtag(v[k]) != tag) pend |= 1ull << k;
+    }
+    long it = 0;
+    while (pend) {
+        // read the pending words again, all in flight before any is
+        // checked (a check in the same branch as its read would wait for
+        // each read in turn)
+#pragma unroll
+        for (int k = 0; k < N; k++)
+            if (pend & (1ull << k)) v[k] = peek(base + idx[k]);
+#pragma unroll
+        for (int k = 0; k < N; k++)
+            if ((pend & (1ull << k)) && wtag(v[k]) == tag) {
+                out[k] = wval(v[k]);
+                pend &= ~(1ull << k);
+            }
+        if (pend && (++it & 31) == 0 && (it > SPIN_LIMIT || peek(abortw) != 0)) return false;
+    }
+    return true;
+}
 
 // Values the compiler must treat as unknown at each use: keeps it from
 // hoisting every phase's (loop-invariant) column indices and lane offsets
@@ -103,14 +149,35 @@ struct Smem {
     float attn[PW][68];           // per-wavefront attention partials: m, l, -, -, o[64]
     float qkv_new[3][64];         // q, k, v of row t for this workgroup's head
     float ml[2][32 * PMAXS];      // m and l of every (head, split)
+    float obuf[PMAXS * 256 * U];  // o of every (split, channel)
     float bestv[PW + 1];
     int besti[PW + 1];
     int abort;
 };
 
+// Exchange words (offsets in u64 units).
+// Values read by many workgroups (x, hid, attention and argmax partials)
+// are published in REPL copies, each read by the workgroups of one XCD
+// (blockIdx % REPL): one copy read by every workgroup concentrates those
+// reads on the few memory channels that hold it.
+constexpr int REPL = 8;
+struct TagLayout {
+    int xs, hs, ps, as;  // copy strides
+    int x, q, hid, part, am, abortw;
+    __host__ __device__ TagLayout(int C, int H)
+        : xs(C + 512), hs(4 * C + 512), ps(H * PMAXS * 68 + 512), as(2 * PT + 512),
+          x(0), q(REPL * xs), hid(q + 3 * C + 512), part(hid + REPL * hs),
+          am(part + REPL * ps), abortw(am + REPL * as) {}
+    __host__ __device__ long words() const { return abortw + 32; }
+};
+__device__ __forceinline__ void put_all(u64* p, int stride, float v, unsigned tag) {
+#pragma unroll
+    for (int r = 0; r < REPL; r++) put(p + r * stride, v, tag);
+}
+
 // Sum over the workgroup, same value in every thread.
 __device__ __forceinline__ float block_sum(float v, float* wred, int wave, int lane) {
-    v = wave_sum(v);
+    v = wave_sum_dpp(v);
     if (lane == 0) wred[wave] = v;
     __syncthreads();
     float s = 0.f;
@@ -190,7 +257,7 @@ __device__ __forceinline__ void col_dots(float (&acc)[UPW], const f32x4 (&w)[NW]
         acc[j] = s;
     }
 #pragma unroll
-    for (int j = 0; j < NJ; j++) acc[j] = wave_sum(acc[j]);
+    for (int j = 0; j < NJ; j++) acc[j] = wave_sum_dpp(acc[j]);
 }
 
 // Column of control-wavefront lane `slot` (or -1): round j = slot / PW of
@@ -218,39 +285,33 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
     // register array left unwritten on the control path would stay live
     // across every phase)
     const int cw0 = ctrl ? (1 << 29) : blockIdx.x * PW + wave;
-    const int C = a.C, C3 = 3 * C, C4 = 4 * C, H = a.H, V = a.V;
+    const int C = a.C, C3 = 3 * C, C4 = 4 * C, H = a.H, V = a.V, L = a.L;
     float* actf = (float*)sm.act;
-    unsigned epoch = 0;
+    const TagLayout tl(C, H);
+    // published copies (written REPL times) and the copy this workgroup reads
+    const int rep = blockIdx.x % REPL;
+    u64* const tx = a.tagged + tl.x;      // x after c_proj / proj
+    u64* const tq = a.tagged + tl.q;      // q, k, v of row t (one copy)
+    u64* const th = a.tagged + tl.hid;    // GELU(fc)
+    u64* const tp = a.tagged + tl.part;   // attention partials [H][PMAXS][68]
+    u64* const tam = a.tagged + tl.am;    // argmax partials [G][2]
+    const u64* const rx = tx + rep * tl.xs;
+    const u64* const rh = th + rep * tl.hs;
+    const u64* const rp = tp + rep * tl.ps;
+    const u64* const ram = tam + rep * tl.as;
+    u64* const abortw = a.tagged + tl.abortw;
+    const unsigned per_step = PHASES * L + 1;
 
     if (tid == 0) sm.abort = 0;
     __syncthreads();
 
-    // Grid barrier. Called by every thread; the control wavefront has
-    // waited for its stores.
-    auto barrier = [&]() -> bool {
-        __syncthreads();
-        if (ctrl) {
-            ++epoch;
-            if (lane == 0)
-                __hip_atomic_fetch_add(a.bar + (blockIdx.x % NGRP) * CSTR, 1u, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-            const unsigned target = epoch * (unsigned)(G / NGRP);
-            long it = 0;
-            bool bad = false;
-            while (true) {
-                const unsigned v = lane < NGRP ? ld_sc(a.bar + lane * CSTR) : target;
-                if (__all(v >= target)) break;
-                if ((++it & 63) == 0 && (ld_sc(a.bar + NGRP * CSTR) != 0u || it > SPIN_LIMIT)) {
-                    bad = true;
-                    break;
-                }
-            }
-            if (bad && lane == 0) {
-                __hip_atomic_fetch_or(a.bar + NGRP * CSTR, 1u, __ATOMIC_RELAXED,
-                                      __HIP_MEMORY_SCOPE_AGENT);
-                if (a.err) atomicOr(a.err, 2);
-                sm.abort = 1;
-            }
+    // After the fetches of a phase: every thread learns whether one of the
+    // workgroup's waits gave up (then all return together).
+    auto settle = [&](bool ok) -> bool {
+        if (!ok) {
+            sm.abort = 1;
+            __hip_atomic_store(abortw, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (a.err) atomicOr(a.err, 2);
         }
         __syncthreads();
         return sm.abort == 0;
@@ -258,7 +319,13 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
 
     int t = *a.pos;
     int tok = *a.tok;
-    f32x4 w[NW];
+    // Two weight buffers: the weights of the next phase that has any are
+    // loaded at the start of the current one (as soon as its input has
+    // arrived), so they are in registers before the workgroup reads the
+    // next input; loads return in order, and a read queued behind a
+    // phase's worth of weight loads would wait for all of them.
+    // A and D use wa, C and E use wb, the lm_head streams through wa.
+    f32x4 wa[NW], wb[NW];
     f32x4 kq[4];             // attention prefetch: K, 16 dims of one key
     float vr[KPW];           // V of 16 keys, one dim
     float xv[LNE];           // LayerNorm input
@@ -277,21 +344,38 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
             lb[i] = ldg(gb + e);
         }
     };
-    auto load_x = [&]() {
+    // xv = x (tag `tag`), element tid + PT * i
+    auto fetch_x = [&](unsigned tag) -> bool {
         const int tt = opaque_v(tid);
+        int idx[LNE];
+        bool need[LNE];
 #pragma unroll
-        for (int i = 0; i < LNE; i++) xv[i] = ld_sc(a.x + min(tt + PT * i, C - 1));
+        for (int i = 0; i < LNE; i++) {
+            idx[i] = min(tt + PT * i, C - 1);
+            need[i] = tt + PT * i < C;
+        }
+        const int nk = min(LNE, (C - (tt & ~63) + PT - 1) / PT);
+        return fetch<LNE>(rx, idx, need, tag, xv, abortw,
+                          opaque_s(__builtin_amdgcn_readfirstlane(nk)));
+    };
+    // x[c] for the control lane's column c (or nothing for c < 0)
+    auto fetch_x1 = [&](int c, unsigned tag, float& out) -> bool {
+        int idx[1] = {max(c, 0)};
+        bool need[1] = {c >= 0};
+        float o[1];
+        const bool ok = fetch<1>(rx, idx, need, tag, o, abortw);
+        out = o[0];
+        return ok;
     };
     // Bias of this lane's output column in the next phase (control lanes;
-    // the others load b[0]). Issued by every wavefront before the current
-    // epilogue, so it completes under that epilogue's store wait.
+    // the others load b[0]). Issued before the current epilogue's stores.
     auto slot_bias = [&](const float* b, int N) -> float {
         int j, q;
         return ldg(b + max(slot_col(opaque_v(lane), N, CW, j, q), 0));
     };
 
     const LayerW* layers = a.layers;
-    load_cols<UPW, U>(w, layers[0].attn_w, C3, C, cw0, CW, lane);
+    load_cols<UPW, U>(wa, layers[0].attn_w, C3, C, cw0, CW, lane);
     ln_params(layers[0].ln1_w, layers[0].ln1_b);
     bo = slot_bias(layers[0].attn_b, C3);
 
@@ -299,6 +383,7 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
         // opaque copies per iteration (see opaque_s)
         const int lane1 = opaque_v(lane), cw1 = opaque_s(cw0);
         const int cw = cw1;
+        const unsigned sbase = a.tag0 + (unsigned)step * per_step;
         // ---------------- embedding x = wte[tok] + wpe[t] (fast.c:245-254)
         if (tok < 0 || tok >= V) {
             if (tid == 0 && a.err) atomicOr(a.err, 1);
@@ -307,39 +392,37 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
         {
             const float* er = a.wte + (long)tok * C;
             const float* pr = a.wpe + (long)t * C;
+            float ev[LNE], pv[LNE];
 #pragma unroll
             for (int i = 0; i < LNE; i++) {
                 const int e = min(tid + PT * i, C - 1);
-                xv[i] = ldg(er + e) + ldg(pr + e);
+                ev[i] = ldg(er + e);
+                pv[i] = ldg(pr + e);
             }
-            if (blockIdx.x == 0) {
 #pragma unroll
-                for (int i = 0; i < LNE; i++)
-                    if (tid + PT * i < C) st_sc(a.x + tid + PT * i, xv[i]);
-                if (tid == 0) a.hist[t] = tok;
-            }
+            for (int i = 0; i < LNE; i++) xv[i] = ev[i] + pv[i];
+            if (blockIdx.x == 0 && tid == 0) a.hist[t] = tok;
         }
 
-        for (int l = 0; l < a.L; l++) {
+        for (int l = 0; l < L; l++) {
             const int lane = opaque_v(lane1), cw = opaque_s(cw1);
             const LayerW P = layers[l];
-            const LayerW PN = layers[min(l + 1, a.L - 1)];
+            const LayerW PN = layers[min(l + 1, L - 1)];
             float* kvl = a.cache + (long)l * a.cap * C3;
             float* rowt = kvl + (long)t * C3;
+            // tags of the values this layer's phases publish; x enters the
+            // layer with the tag of the previous layer's proj (or as the
+            // embedding, computed in place, for layer 0)
+            const unsigned TA = sbase + PHASES * l + 1, TB = TA + 1, TC = TA + 2, TD = TA + 3,
+                           TE = TA + 4, TXIN = TA - 1;
 
-            // ---------------- phase A: LayerNorm 1 + QKV into cache row t
-            if (l > 0) load_x();
-            ln_to_act(xv, lw, lb, C, actf, sm.wred, tid, wave, lane);
-            if (!ctrl) {
-                float acc[UPW];
-                col_dots<UPW, U>(acc, w, sm.act, C3, C, cw, CW, lane);
-                if (lane == 0)
-#pragma unroll
-                    for (int j = 0; j < UPW; j++) sm.red[j][wave] = acc[j];
-            }
+            // ---------------- phase A: LayerNorm 1 + QKV into row t
+            if (l > 0 && !settle(fetch_x(TXIN))) return;
             // attention split layout for keys 0..t
             const int nk = t + 1;
-            int ns = (nk + 63) / 64;
+            // as few splits as the workgroup's PW * KPW keys allow (fewer
+            // partials to exchange)
+            int ns = (nk + PW * KPW - 1) / (PW * KPW);
             ns = min(ns, min(G / H, PMAXS));
             const int kps = (nk + ns - 1) / ns;
             const int kpw = (kps + PW - 1) / PW;
@@ -347,19 +430,9 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
             const int ih = blockIdx.x / ns, isp = blockIdx.x - (blockIdx.x / ns) * ns;
             const int k0 = isp * kps, k1 = min(k0 + kps, nk);
             const int kw0 = k0 + wave * kpw, kw1 = min(kw0 + kpw, k1);
-            __syncthreads();
-            {
-                const float bn = slot_bias(P.proj_b, C);
-                if (ctrl) {
-                    int j, q;
-                    const int c = slot_col(lane, C3, CW, j, q);
-                    if (c >= 0) st_sc(rowt + c, sm.red[j][q] + bo);
-                    wait_stores();
-                }
-                bo = bn;
-            }
+            // next weights (c_proj) and this workgroup's cached keys (< t)
+            load_cols<UPW, U>(wb, P.proj_w, C, C, cw, CW, lane);
             if (!ctrl && has_item) {
-                // prefetch this wavefront's cached keys (< t) of head ih
                 const int kk = kw0 + (lane >> 2), dq = lane & 3;
                 const int kc = min(kk, max(t - 1, 0));
                 const float* kr = kvl + (long)kc * C3 + C + ih * 64 + dq * 16;
@@ -376,143 +449,192 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
 #pragma unroll
                 for (int jj = 0; jj < KPW; jj++) vr[jj] = 0.f;
             }
-            if (!barrier()) return;
+            ln_to_act(xv, lw, lb, C, actf, sm.wred, tid, wave, lane);
+            if (!ctrl) {
+                float acc[UPW];
+                col_dots<UPW, U>(acc, wa, sm.act, C3, C, cw, CW, lane);
+                if (lane == 0)
+#pragma unroll
+                    for (int j = 0; j < UPW; j++) sm.red[j][wave] = acc[j];
+            }
+            __syncthreads();
+            {
+                const float bn = slot_bias(P.proj_b, C);
+                if (ctrl) {
+                    int j, q;
+                    const int c = slot_col(lane, C3, CW, j, q);
+                    if (c >= 0) {
+                        const float v = sm.red[j][q] + bo;
+                        put(tq + c, v, TA);
+                        st_sc(rowt + c, v);  // the cache row, for later steps
+                    }
+                }
+                bo = bn;
+            }
 
             // ---------------- phase B: attention, one (head, key split) per workgroup
-            if (ctrl && has_item) {
-                // all three loads before the LDS stores (atomic loads are
-                // not reordered past other memory operations)
-                float nv[3];
+            if (has_item) {
+                bool ok = true;
+                if (ctrl) {
+                    int idx[3];
+                    bool need[3];
+                    float nv[3];
 #pragma unroll
-                for (int m = 0; m < 3; m++) nv[m] = ld_sc(rowt + m * C + ih * 64 + lane);
+                    for (int m = 0; m < 3; m++) {
+                        idx[m] = m * C + ih * 64 + lane;
+                        need[m] = true;
+                    }
+                    ok = fetch<3>(tq, idx, need, TA, nv, abortw);
 #pragma unroll
-                for (int m = 0; m < 3; m++) sm.qkv_new[m][lane] = nv[m];
-            }
-            __syncthreads();
-            if (!ctrl && has_item) {
-                const int kk = kw0 + (lane >> 2), dq = lane & 3;
-                const bool valid = kk < kw1;
-                const f32x4* qn = (const f32x4*)&sm.qkv_new[0][dq * 16];
-                const f32x4* kn = (const f32x4*)&sm.qkv_new[1][dq * 16];
-                float d = 0.f;
-#pragma unroll
-                for (int i = 0; i < 4; i++) d += dot4(qn[i], kk == t ? kn[i] : kq[i]);
-                d += __shfl_xor(d, 1, 64);
-                d += __shfl_xor(d, 2, 64);
-                const float sc = valid ? d * a.scale : -INFINITY;
-                const float m = wave_max(sc);
-                const float e = valid ? expf(sc - m) : 0.f;
-                const float ls = wave_sum(dq == 0 ? e : 0.f);
-                float o = 0.f;
-#pragma unroll
-                for (int jj = 0; jj < KPW; jj++) {
-                    const float pj = __shfl(e, 4 * jj, 64);
-                    const int kj = kw0 + jj;
-                    if (kj < kw1) o += pj * (kj == t ? sm.qkv_new[2][lane] : vr[jj]);
+                    for (int m = 0; m < 3; m++) sm.qkv_new[m][lane] = nv[m];
                 }
-                if (lane == 0) {
-                    sm.attn[wave][0] = m;
-                    sm.attn[wave][1] = ls;
+                if (!settle(ok)) return;
+                if (!ctrl) {
+                    const int kk = kw0 + (lane >> 2), dq = lane & 3;
+                    const bool valid = kk < kw1;
+                    const f32x4* qn = (const f32x4*)&sm.qkv_new[0][dq * 16];
+                    const f32x4* kn = (const f32x4*)&sm.qkv_new[1][dq * 16];
+                    float d = 0.f;
+#pragma unroll
+                    for (int i = 0; i < 4; i++) d += dot4(qn[i], kk == t ? kn[i] : kq[i]);
+                    d += CNGPT_DPP(d, 0xB1);  // the 4 lanes of a key: xor 1, xor 2
+                    d += CNGPT_DPP(d, 0x4E);
+                    const float sc = valid ? d * a.scale : -INFINITY;
+                    const float m = wave_max_dpp(sc);
+                    const float e = valid ? expf(sc - m) : 0.f;
+                    const float ls = wave_sum_dpp(dq == 0 ? e : 0.f);
+                    float o = 0.f;
+#pragma unroll
+                    for (int jj = 0; jj < KPW; jj++) {
+                        const float pj = lane_f(e, 4 * jj);
+                        const int kj = kw0 + jj;
+                        if (kj < kw1) o += pj * (kj == t ? sm.qkv_new[2][lane] : vr[jj]);
+                    }
+                    if (lane == 0) {
+                        sm.attn[wave][0] = m;
+                        sm.attn[wave][1] = ls;
+                    }
+                    sm.attn[wave][4 + lane] = o;
                 }
-                sm.attn[wave][4 + lane] = o;
-            }
-            __syncthreads();
-            if (ctrl) {
-                if (has_item) {
+                __syncthreads();
+                if (ctrl) {
                     float M = -INFINITY;
 #pragma unroll
                     for (int v = 0; v < PW; v++) M = fmaxf(M, sm.attn[v][0]);
-                    float L = 0.f, O = 0.f;
+                    float Ls = 0.f, O = 0.f;
 #pragma unroll
                     for (int v = 0; v < PW; v++) {
                         const float mv = sm.attn[v][0];
                         const float f = mv == -INFINITY ? 0.f : expf(mv - M);
-                        L += sm.attn[v][1] * f;
+                        Ls += sm.attn[v][1] * f;
                         O += sm.attn[v][4 + lane] * f;
                     }
-                    float* part = a.apart + ((long)ih * PMAXS + isp) * 68;
-                    st_sc(part + 4 + lane, O);
+                    u64* part = tp + ((long)ih * PMAXS + isp) * 68;
+                    put_all(part + 4 + lane, tl.ps, O, TB);
                     if (lane == 0) {
-                        st_sc(part, M);
-                        st_sc(part + 1, L);
+                        put_all(part, tl.ps, M, TB);
+                        put_all(part + 1, tl.ps, Ls, TB);
                     }
                 }
-                wait_stores();
             }
-            load_cols<UPW, U>(w, P.proj_w, C, C, cw, CW, lane);
-            if (!barrier()) return;
 
             // ---------------- phase C: merge the splits, c_proj, x += . + b
-            {
+            // (only workgroups that own one of its C columns take part)
+            const bool has_cols = blockIdx.x * PW < C;
+            if (has_cols) {
                 int j = 0, q = 0;
                 const int c = ctrl ? slot_col(lane, C, CW, j, q) : -1;
-                const float xo = ctrl ? ld_sc(a.x + max(c, 0)) : 0.f;
-                // m and l of every (head, split) into LDS; each thread loads
-                // the o of its channels from every split (all loads in
-                // flight) and merges them (online softmax merge)
-                const int tt = opaque_v(tid);
-                const int hsi = min(tt, H * ns - 1);
-                const float* pm = a.apart + ((long)(hsi / ns) * PMAXS + hsi % ns) * 68;
-                const float m_r = ld_sc(pm), l_r = ld_sc(pm + 1);
-                constexpr int CPT = (256 * U + PT - 1) / PT;  // channels per thread
-                float ov[CPT][PMAXS];
-#pragma unroll
-                for (int i = 0; i < CPT; i++) {
-                    const int e = min(tt + PT * i, C - 1);
-                    const float* pb = a.apart + (long)(e >> 6) * PMAXS * 68 + 4 + (e & 63);
-#pragma unroll
-                    for (int sp = 0; sp < PMAXS; sp++)
-                        ov[i][sp] = sp < ns ? ld_sc(pb + sp * 68) : 0.f;
-                }
-                if (tid < H * ns) {
-                    sm.ml[0][tid] = m_r;
-                    sm.ml[1][tid] = l_r;
-                }
-                __syncthreads();
-#pragma unroll
-                for (int i = 0; i < CPT; i++) {
-                    const int e = tid + PT * i;
-                    const int h = min(e, C - 1) >> 6;
-                    float mx = -INFINITY, L = 0.f, acc = 0.f;
-#pragma unroll
-                    for (int sp = 0; sp < PMAXS; sp++) {
-                        if (sp < ns) {
-                            const float ms = sm.ml[0][h * ns + sp], lsum = sm.ml[1][h * ns + sp];
-                            const float mn = fmaxf(mx, ms);
-                            const float fa = expf(mx - mn), fb = expf(ms - mn);
-                            acc = acc * fa + ov[i][sp] * fb;
-                            L = L * fa + lsum * fb;
-                            mx = mn;
-                        }
+                float xo = 0.f;
+                bool ok = true;
+                if (ctrl) {
+                    if (l == 0) {
+                        const int cc = max(c, 0);
+                        xo = ldg(a.wte + (long)tok * C + cc) + ldg(a.wpe + (long)t * C + cc);
+                    } else {
+                        ok = fetch_x1(c, TXIN, xo);
                     }
-                    if (e < C) actf[e] = acc * (1.0f / L);
+                }
+                // m and l of every (head, split), and the o of this thread's
+                // channels from every split (all first reads in flight)
+                const int tt = opaque_v(tid);
+                {
+                    const int hsi = min(tt, H * ns - 1);
+                    const int pb = ((hsi / ns) * PMAXS + hsi % ns) * 68;
+                    int idx[2] = {pb, pb + 1};
+                    bool need[2] = {tt < H * ns, tt < H * ns};
+                    float mlv[2];
+                    const bool ok2 = fetch<2>(rp, idx, need, TB, mlv, abortw);
+                    ok = ok && ok2;
+                    if (tt < H * ns) {
+                        sm.ml[0][tt] = mlv[0];
+                        sm.ml[1][tt] = mlv[1];
+                    }
+                }
+                // o of every (split, channel) into LDS: flattened index
+                // f = split * C + channel, 8 words per thread in flight
+                {
+                    const int tot = C * ns;
+                    for (int f0 = 0; f0 < tot; f0 += PT * 8) {
+                        int idx[8];
+                        bool need[8];
+                        float o8[8];
+#pragma unroll
+                        for (int k = 0; k < 8; k++) {
+                            const int f = f0 + tt + PT * k;
+                            const int fc = min(f, tot - 1);
+                            const int sp = fc / C, e = fc - sp * C;
+                            idx[k] = ((e >> 6) * PMAXS + sp) * 68 + 4 + (e & 63);
+                            need[k] = f < tot;
+                        }
+                        // slots past the end for this whole wavefront are not read
+                        const int nk = min(8, (tot - f0 - (tt & ~63) + PT - 1) / PT);
+                        const bool ok2 = fetch<8>(rp, idx, need, TB, o8, abortw,
+                                                  opaque_s(__builtin_amdgcn_readfirstlane(nk)));
+                        ok = ok && ok2;
+#pragma unroll
+                        for (int k = 0; k < 8; k++)
+                            if (need[k]) sm.obuf[f0 + tt + PT * k] = o8[k];
+                    }
+                }
+                if (!settle(ok)) return;
+                load_cols<UPW, U>(wa, P.fc_w, C4, C, cw, CW, lane);
+                for (int e = tid; e < C; e += PT) {
+                    const int h = e >> 6;
+                    float mx = -INFINITY, Ls = 0.f, acc = 0.f;
+                    for (int sp = 0; sp < ns; sp++) {
+                        const float ms = sm.ml[0][h * ns + sp], lsum = sm.ml[1][h * ns + sp];
+                        const float mn = fmaxf(mx, ms);
+                        const float fa = expf(mx - mn), fb = expf(ms - mn);
+                        acc = acc * fa + sm.obuf[sp * C + e] * fb;
+                        Ls = Ls * fa + lsum * fb;
+                        mx = mn;
+                    }
+                    actf[e] = acc * (1.0f / Ls);
                 }
                 __syncthreads();
                 if (!ctrl) {
                     float acc[UPW];
-                    col_dots<UPW, U>(acc, w, sm.act, C, C, cw, CW, lane);
+                    col_dots<UPW, U>(acc, wb, sm.act, C, C, cw, CW, lane);
                     if (lane == 0)
 #pragma unroll
                         for (int jj = 0; jj < UPW; jj++) sm.red[jj][wave] = acc[jj];
                 }
                 __syncthreads();
-                const float bn = slot_bias(P.fc_b, C4);
-                if (ctrl) {
-                    if (c >= 0) st_sc(a.x + c, (xo + sm.red[j][q]) + bo);
-                    wait_stores();
-                }
-                bo = bn;
-                load_cols<UPW, U>(w, P.fc_w, C4, C, cw, CW, lane);
-                ln_params(P.ln2_w, P.ln2_b);
+                if (ctrl && c >= 0) put_all(tx + c, tl.xs, (xo + sm.red[j][q]) + bo, TC);
+            } else {
+                load_cols<UPW, U>(wa, P.fc_w, C4, C, cw, CW, lane);
             }
-            if (!barrier()) return;
+            bo = slot_bias(P.fc_b, C4);
+            ln_params(P.ln2_w, P.ln2_b);
 
             // ---------------- phase D: LayerNorm 2, fc + b, GELU into hid
-            load_x();
+            if (!settle(fetch_x(TC))) return;
+            // proj: one column of depth 4C per wavefront
+            load_cols<1, 4 * U>(wb, P.mlp_w, C, C4, cw, CW, lane);
             ln_to_act(xv, lw, lb, C, actf, sm.wred, tid, wave, lane);
             if (!ctrl) {
                 float acc[UPW];
-                col_dots<UPW, U>(acc, w, sm.act, C4, C, cw, CW, lane);
+                col_dots<UPW, U>(acc, wa, sm.act, C4, C, cw, CW, lane);
                 if (lane == 0)
 #pragma unroll
                     for (int j = 0; j < UPW; j++) sm.red[j][wave] = acc[j];
@@ -523,59 +645,66 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
                 if (ctrl) {
                     int j, q;
                     const int c = slot_col(lane, C4, CW, j, q);
-                    if (c >= 0) st_sc(a.hid + c, gelu_tanh(sm.red[j][q] + bo));
-                    wait_stores();
+                    if (c >= 0) put_all(th + c, tl.hs, gelu_tanh(sm.red[j][q] + bo), TD);
                 }
                 bo = bn;
             }
-            // proj: one column of depth 4C per wavefront
-            load_cols<1, 4 * U>(w, P.mlp_w, C, C4, cw, CW, lane);
-            if (!barrier()) return;
 
-            // ---------------- phase E: proj, x += . + b
-            {
+            // ---------------- phase E: proj, x += . + b (column owners only)
+            if (has_cols) {
                 int j = 0, q = 0;
                 const int c = ctrl ? slot_col(lane, C, CW, j, q) : -1;
-                const float xo = ctrl ? ld_sc(a.x + max(c, 0)) : 0.f;
+                float xo = 0.f;
+                bool ok = true;
+                if (ctrl) ok = fetch_x1(c, TC, xo);
                 {
                     constexpr int NH = (1024 * U + PT - 1) / PT;
-                    float hv[NH];
                     const int tt = opaque_v(tid);
+                    int idx[NH];
+                    bool need[NH];
+                    float hv[NH];
 #pragma unroll
-                    for (int k = 0; k < NH; k++) hv[k] = ld_sc(a.hid + min(tt + PT * k, C4 - 1));
+                    for (int k = 0; k < NH; k++) {
+                        idx[k] = min(tt + PT * k, C4 - 1);
+                        need[k] = tt + PT * k < C4;
+                    }
+                    const int nk = min(NH, (C4 - (tt & ~63) + PT - 1) / PT);
+                    const bool ok2 = fetch<NH>(rh, idx, need, TD, hv, abortw,
+                                               opaque_s(__builtin_amdgcn_readfirstlane(nk)));
+                    ok = ok && ok2;
 #pragma unroll
                     for (int k = 0; k < NH; k++)
-                        if (tid + PT * k < C4) actf[tid + PT * k] = hv[k];
+                        if (need[k]) actf[tt + PT * k] = hv[k];
                 }
-                __syncthreads();
+                if (!settle(ok)) return;
+                if (l + 1 < L)
+                    load_cols<UPW, U>(wa, PN.attn_w, C3, C, cw, CW, lane);
+                else  // the first UPW rounds of lm_head columns (tied wte)
+                    load_cols<UPW, U>(wa, a.wte, V, C, cw, CW, lane);
                 if (!ctrl) {
                     float acc[UPW];
-                    col_dots<1, 4 * U>(acc, w, sm.act, C, C4, cw, CW, lane);
+                    col_dots<1, 4 * U>(acc, wb, sm.act, C, C4, cw, CW, lane);
                     if (lane == 0)
 #pragma unroll
                         for (int jj = 0; jj < UPW; jj++) sm.red[jj][wave] = acc[jj];
                 }
                 __syncthreads();
-                const float bn = slot_bias(PN.attn_b, C3);
-                if (ctrl) {
-                    if (c >= 0) st_sc(a.x + c, (xo + sm.red[j][q]) + bo);
-                    wait_stores();
-                }
-                bo = bn;
-                if (l + 1 < a.L) {
-                    load_cols<UPW, U>(w, PN.attn_w, C3, C, cw, CW, lane);
-                    ln_params(PN.ln1_w, PN.ln1_b);
-                } else {
-                    // the first UPW rounds of lm_head columns (tied wte)
-                    load_cols<UPW, U>(w, a.wte, V, C, cw, CW, lane);
-                    ln_params(a.lnf_w, a.lnf_b);
-                }
+                if (ctrl && c >= 0) put_all(tx + c, tl.xs, (xo + sm.red[j][q]) + bo, TE);
+            } else if (l + 1 < L) {
+                load_cols<UPW, U>(wa, PN.attn_w, C3, C, cw, CW, lane);
+            } else {
+                load_cols<UPW, U>(wa, a.wte, V, C, cw, CW, lane);
             }
-            if (!barrier()) return;
+            bo = slot_bias(PN.attn_b, C3);
+            if (l + 1 < L)
+                ln_params(PN.ln1_w, PN.ln1_b);
+            else
+                ln_params(a.lnf_w, a.lnf_b);
         }
 
         // ---------------- phase F: final LayerNorm, lm_head (tied wte), argmax partials
-        load_x();
+        const unsigned TF = sbase + PHASES * L + 1;
+        if (!settle(fetch_x(TF - 1))) return;
         ln_to_act(xv, lw, lb, C, actf, sm.wred, tid, wave, lane1);
         if (!ctrl) {
             const int ln = opaque_v(lane1);
@@ -593,19 +722,19 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
 #pragma unroll
                         for (int i = 0; i < U; i++) {
                             const int f = i * 64 + ln;
-                            if (f < K4) s += dot4(w[k * U + i], sm.act[f]);
+                            if (f < K4) s += dot4(wa[k * U + i], sm.act[f]);
                         }
                         const int nc = col + CW * UPW;
                         if (nc < V) {
                             const float* row = a.wte + (long)nc * C;
 #pragma unroll
                             for (int i = 0; i < U; i++)
-                                w[k * U + i] = ldg4(row + 4 * min(i * 64 + ln, K4 - 1));
+                                wa[k * U + i] = ldg4(row + 4 * min(i * 64 + ln, K4 - 1));
                         } else {
 #pragma unroll
-                            for (int i = 0; i < U; i++) w[k * U + i] = f32x4{0.f, 0.f, 0.f, 0.f};
+                            for (int i = 0; i < U; i++) wa[k * U + i] = f32x4{0.f, 0.f, 0.f, 0.f};
                         }
-                        s = wave_sum(s);
+                        s = wave_sum_dpp(s);
                         if (ln == 0 && a.logits) a.logits[col] = s;
                         if (better(s, col, best, bi)) {
                             best = s;
@@ -621,33 +750,33 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
         }
         __syncthreads();
         bo = slot_bias(layers[0].attn_b, C3);
-        if (ctrl) {
-            if (lane1 == 0) {
-                float b = sm.bestv[0];
-                int bi = sm.besti[0];
-                for (int v = 1; v < PW; v++)
-                    if (better(sm.bestv[v], sm.besti[v], b, bi)) {
-                        b = sm.bestv[v];
-                        bi = sm.besti[v];
-                    }
-                st_sc(a.am_v + blockIdx.x, b);
-                st_sc(a.am_i + blockIdx.x, bi);
-            }
-            wait_stores();
+        if (ctrl && lane1 == 0) {
+            float b = sm.bestv[0];
+            int bi = sm.besti[0];
+            for (int v = 1; v < PW; v++)
+                if (better(sm.bestv[v], sm.besti[v], b, bi)) {
+                    b = sm.bestv[v];
+                    bi = sm.besti[v];
+                }
+            put_all(tam + 2 * blockIdx.x, tl.as, b, TF);
+            put_all(tam + 2 * blockIdx.x + 1, tl.as, __int_as_float(bi), TF);
         }
         if (step + 1 < a.n_steps) {
-            load_cols<UPW, U>(w, layers[0].attn_w, C3, C, cw, CW, lane1);
+            load_cols<UPW, U>(wa, layers[0].attn_w, C3, C, cw, CW, lane1);
             ln_params(layers[0].ln1_w, layers[0].ln1_b);
         }
-        if (!barrier()) return;
 
         // ---------------- phase G: every workgroup reduces the argmax partials
         {
-            const int g = min(tid, G - 1);
-            const float pv = ld_sc(a.am_v + g);
-            const int pi = ld_sc(a.am_i + g);
-            float b = tid < G ? pv : -INFINITY;
-            int bi = tid < G ? pi : 0x7fffffff;
+            const int tt = opaque_v(tid);
+            const int g = min(tt, G - 1);
+            int idx[2] = {2 * g, 2 * g + 1};
+            bool need[2] = {tt < G, tt < G};
+            float pv[2];
+            const bool ok = fetch<2>(ram, idx, need, TF, pv, abortw);
+            if (!settle(ok)) return;
+            float b = tt < G ? pv[0] : -INFINITY;
+            int bi = tt < G ? __float_as_int(pv[1]) : 0x7fffffff;
 #pragma unroll
             for (int o = 32; o > 0; o >>= 1) {
                 const float ov = __shfl_xor(b, o, 64);
@@ -697,19 +826,19 @@ int persist_workgroups(int device) {
     if (hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, device) != hipSuccess ||
         !coop)
         return 0;
-    return cus / NGRP * NGRP;
+    return std::min(cus, PT);
 }
 
-int persist_max_splits() { return PMAXS; }
+long persist_tagged_words(int C, int H) { return TagLayout(C, H).words(); }
 
-int persist_barrier_words() { return NGRP * CSTR + 32; }
+unsigned persist_tags(int L, int n_steps) { return (unsigned)n_steps * (PHASES * L + 1) + 1; }
 
 bool persist_supported(int C, int H, int V, int cap, int G) {
-    if (G < NGRP || G > PT || C % 64 || C != 64 * H || C > 256 * PMAXU || H > 32 || C > LNE * PT)
+    if (G < 1 || G > PT || C % 64 || C != 64 * H || C > 256 * PMAXU || H > 32 || C > LNE * PT)
         return false;
     const long CW = (long)PW * G;
     // columns per wavefront: QKV and fc at most UPW, proj one
-    if (4L * C > UPW * CW || C > CW || V < 32) return false;
+    if (4L * C > UPW * CW || C > CW || V < 1) return false;
     // attention: H * splits workgroups, at most PW * KPW keys per split
     const int ns = std::min(G / H, PMAXS);
     if (ns < 1 || (long)ns * PW * KPW < cap) return false;
@@ -717,13 +846,14 @@ bool persist_supported(int C, int H, int V, int cap, int G) {
 }
 
 hipError_t launch_decode_persist(const PersistArgs& a, int G, hipStream_t s) {
-    hipError_t e = hipMemsetAsync(a.bar, 0, (size_t)persist_barrier_words() * sizeof(unsigned), s);
+    // clear the abort word (left set by a launch that gave up)
+    const TagLayout tl(a.C, a.H);
+    hipError_t e = hipMemsetAsync(a.tagged + tl.abortw, 0, sizeof(u64), s);
     if (e != hipSuccess) return e;
     switch ((a.C + 255) / 256) {
         case 1: return launch_u<1>(a, G, s);
         case 2: return launch_u<2>(a, G, s);
         case 3: return launch_u<3>(a, G, s);
-        case 4: return launch_u<4>(a, G, s);
         default: return hipErrorInvalidValue;
     }
 }

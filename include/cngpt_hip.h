@@ -55,8 +55,8 @@ enum {
 /* How decode steps run. KERNELS: one replayed graph of per-stage kernels
  * per step (any batch). PERSISTENT: the greedy steps of one sequence as one
  * cooperative launch whose workgroups meet at grid barriers between stages
- * (B = 1, head size 64, n_embd <= 1024). AUTO: KERNELS (the persistent
- * launch is opt-in while it is slower on GPT-2 small). */
+ * (B = 1, head size 64, n_embd <= 768). AUTO: PERSISTENT where it
+ * applies (greedy decode_step / generate), else KERNELS. */
 enum { CNGPT_DECODE_AUTO = 0, CNGPT_DECODE_KERNELS = 1, CNGPT_DECODE_PERSISTENT = 2 };
 
 /* Last error message of the calling thread ("" if none). */

@@ -15,12 +15,11 @@ from test_parity_gpu import compare, ocfg, randomize, say
 
 pytestmark = pytest.mark.gpu
 
-# widths 256 / 512 / 768 / 1024 take 1 / 2 / 3 / 4 float4 per lane per column
+# widths 256 / 512 / 768 take 1 / 2 / 3 float4 per lane per column
 CASES = {
     "c256_v1000": cngpt_amd.Config(2, 4, 256, 1000, 128),
     "c512_v3000": cngpt_amd.Config(2, 8, 512, 3000, 256),
     "c768_v50257": cngpt_amd.Config(3, 12, 768, 50257, 1024),
-    "c1024_v50257": cngpt_amd.Config(2, 16, 1024, 50257, 1024),
 }
 
 
@@ -116,3 +115,11 @@ def test_persistent_refuses_batches():
         assert m.decode_path() == cngpt_amd.DECODE_KERNELS
         with pytest.raises(cngpt_amd.CngptError):
             m.set_decode_path(7)
+    # widths above 768 take the kernel-per-stage decode only
+    cfg = cngpt_amd.Config(1, 16, 1024, 1000, 64)
+    params, m = model(cfg, 4)
+    with m:
+        m.decode_begin(np.zeros((1, 4), np.int32), capacity=16)
+        m.set_decode_path(cngpt_amd.DECODE_PERSISTENT)
+        with pytest.raises(cngpt_amd.CngptError, match="persistent"):
+            m.decode_step(None)
