@@ -53,16 +53,7 @@ constexpr long SPIN_LIMIT = 1L << 20;  // polls of one value before giving up
 // registers beside the rest; wider models take the kernel-per-stage decode.
 constexpr int PMAXU = 3;
 
-__device__ __forceinline__ float ld_sc(const float* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ int ld_sc(const int* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 __device__ __forceinline__ void st_sc(float* p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_sc(int* p, int v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 // Loads through the global address space: pointers taken from the layer
@@ -89,22 +80,27 @@ __device__ __forceinline__ unsigned wtag(u64 w) { return (unsigned)(w >> 32); }
 // idx[k] is always a valid index). All first reads are in flight together;
 // only stragglers are read again. False after SPIN_LIMIT rounds or when
 // another workgroup has raised the abort word.
-// Only k < nk (uniform over the wavefront) are read at all.
+// Only slots k with bit k of en (uniform over the wavefront) are read at
+// all, and slots with bit k of t2 wait for tag2 instead of tag. One call
+// waits for all its words, so a phase gathers every input in one call (one
+// round trip, not one per input).
 template <int N>
 __device__ __forceinline__ bool fetch(const u64* base, const int (&idx)[N], const bool (&need)[N],
                                       unsigned tag, float (&out)[N], const u64* abortw,
-                                      int nk = N) {
+                                      unsigned en = ~0u, unsigned t2 = 0u, unsigned tag2 = 0u) {
     u64 v[N];
 #pragma unroll
-    for (int k = 0; k < N; k++) v[k] = k < nk ? peek(base + idx[k]) : 0ull;
+    for (int k = 0; k < N; k++) v[k] = ((en >> k) & 1u) ? peek(base + idx[k]) : 0ull;
     unsigned long long pend = 0;
 #pragma unroll
     for (int k = 0; k < N; k++) {
         out[k] = wval(v[k]);
-        if (need[k] && wtag(v[k]) != tag) pend |= 1ull << k;
+        const unsigned want = ((t2 >> k) & 1u) ? tag2 : tag;
+        if (((en >> k) & 1u) && need[k] && wtag(v[k]) != want) pend |= 1ull << k;
     }
     long it = 0;
     while (pend) {
+        __builtin_amdgcn_s_sleep(1);  // a short back-off between rounds
         // read the pending words again, all in flight before any is
         // checked (a check in the same branch as its read would wait for
         // each read in turn)
@@ -113,7 +109,7 @@ __device__ __forceinline__ bool fetch(const u64* base, const int (&idx)[N], cons
             if (pend & (1ull << k)) v[k] = peek(base + idx[k]);
 #pragma unroll
         for (int k = 0; k < N; k++)
-            if ((pend & (1ull << k)) && wtag(v[k]) == tag) {
+            if ((pend & (1ull << k)) && wtag(v[k]) == (((t2 >> k) & 1u) ? tag2 : tag)) {
                 out[k] = wval(v[k]);
                 pend &= ~(1ull << k);
             }
@@ -139,6 +135,13 @@ __device__ __forceinline__ float dot4(f32x4 a, f32x4 b) {
 }
 __device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
     return v > bv || (v == bv && i < bi);
+}
+
+// Enable mask of slots k whose word tid + PT * k (for some lane of this
+// wavefront) is below n.
+__device__ __forceinline__ unsigned slots_below(int n, int tt) {
+    const int k = min(31, max(0, (n - (tt & ~63) + PT - 1) / PT));
+    return (unsigned)opaque_s(__builtin_amdgcn_readfirstlane((int)((1u << k) - 1u)));
 }
 
 template <int U>
@@ -354,18 +357,7 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
             idx[i] = min(tt + PT * i, C - 1);
             need[i] = tt + PT * i < C;
         }
-        const int nk = min(LNE, (C - (tt & ~63) + PT - 1) / PT);
-        return fetch<LNE>(rx, idx, need, tag, xv, abortw,
-                          opaque_s(__builtin_amdgcn_readfirstlane(nk)));
-    };
-    // x[c] for the control lane's column c (or nothing for c < 0)
-    auto fetch_x1 = [&](int c, unsigned tag, float& out) -> bool {
-        int idx[1] = {max(c, 0)};
-        bool need[1] = {c >= 0};
-        float o[1];
-        const bool ok = fetch<1>(rx, idx, need, tag, o, abortw);
-        out = o[0];
-        return ok;
+        return fetch<LNE>(rx, idx, need, tag, xv, abortw, slots_below(C, tt));
     };
     // Bias of this lane's output column in the next phase (control lanes;
     // the others load b[0]). Issued before the current epilogue's stores.
@@ -545,59 +537,57 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
                 int j = 0, q = 0;
                 const int c = ctrl ? slot_col(lane, C, CW, j, q) : -1;
                 float xo = 0.f;
-                bool ok = true;
-                if (ctrl) {
-                    if (l == 0) {
-                        const int cc = max(c, 0);
-                        xo = ldg(a.wte + (long)tok * C + cc) + ldg(a.wpe + (long)t * C + cc);
-                    } else {
-                        ok = fetch_x1(c, TXIN, xo);
-                    }
+                if (ctrl && l == 0) {
+                    const int cc = max(c, 0);
+                    xo = ldg(a.wte + (long)tok * C + cc) + ldg(a.wpe + (long)t * C + cc);
                 }
-                // m and l of every (head, split), and the o of this thread's
-                // channels from every split (all first reads in flight)
+                // one wait for: the o of every (split, channel) (flattened
+                // f = split * C + channel, 8 per thread per round, into
+                // LDS), m and l of every (head, split) (first round), and
+                // the control lane's x (first round, layers > 0)
                 const int tt = opaque_v(tid);
-                {
+                const int tot = C * ns;
+                bool ok = true;
+                for (int f0 = 0; f0 < tot; f0 += PT * 8) {
+                    int idx[11];
+                    bool need[11];
+                    float o[11];
+#pragma unroll
+                    for (int k = 0; k < 8; k++) {
+                        const int f = f0 + tt + PT * k;
+                        const int fc = min(f, tot - 1);
+                        const int sp = fc / C, e = fc - sp * C;
+                        idx[k] = ((e >> 6) * PMAXS + sp) * 68 + 4 + (e & 63);
+                        need[k] = f < tot;
+                    }
                     const int hsi = min(tt, H * ns - 1);
                     const int pb = ((hsi / ns) * PMAXS + hsi % ns) * 68;
-                    int idx[2] = {pb, pb + 1};
-                    bool need[2] = {tt < H * ns, tt < H * ns};
-                    float mlv[2];
-                    const bool ok2 = fetch<2>(rp, idx, need, TB, mlv, abortw);
-                    ok = ok && ok2;
-                    if (tt < H * ns) {
-                        sm.ml[0][tt] = mlv[0];
-                        sm.ml[1][tt] = mlv[1];
+                    idx[8] = pb;
+                    idx[9] = pb + 1;
+                    need[8] = need[9] = tt < H * ns;
+                    idx[10] = (int)((rx + max(c, 0)) - rp);
+                    need[10] = c >= 0;
+                    unsigned en = slots_below(tot - f0, tt) & 0xFFu;
+                    if (f0 == 0) {
+                        if ((tt & ~63) < H * ns) en |= 3u << 8;
+                        if (ctrl && l > 0) en |= 1u << 10;
                     }
-                }
-                // o of every (split, channel) into LDS: flattened index
-                // f = split * C + channel, 8 words per thread in flight
-                {
-                    const int tot = C * ns;
-                    for (int f0 = 0; f0 < tot; f0 += PT * 8) {
-                        int idx[8];
-                        bool need[8];
-                        float o8[8];
+                    const bool ok2 = fetch<11>(rp, idx, need, TB, o, abortw, en, 1u << 10, TXIN);
+                    ok = ok && ok2;
 #pragma unroll
-                        for (int k = 0; k < 8; k++) {
-                            const int f = f0 + tt + PT * k;
-                            const int fc = min(f, tot - 1);
-                            const int sp = fc / C, e = fc - sp * C;
-                            idx[k] = ((e >> 6) * PMAXS + sp) * 68 + 4 + (e & 63);
-                            need[k] = f < tot;
+                    for (int k = 0; k < 8; k++)
+                        if (need[k]) sm.obuf[f0 + tt + PT * k] = o[k];
+                    if (f0 == 0) {
+                        if (tt < H * ns) {
+                            sm.ml[0][tt] = o[8];
+                            sm.ml[1][tt] = o[9];
                         }
-                        // slots past the end for this whole wavefront are not read
-                        const int nk = min(8, (tot - f0 - (tt & ~63) + PT - 1) / PT);
-                        const bool ok2 = fetch<8>(rp, idx, need, TB, o8, abortw,
-                                                  opaque_s(__builtin_amdgcn_readfirstlane(nk)));
-                        ok = ok && ok2;
-#pragma unroll
-                        for (int k = 0; k < 8; k++)
-                            if (need[k]) sm.obuf[f0 + tt + PT * k] = o8[k];
+                        if (ctrl && l > 0) xo = o[10];
                     }
                 }
                 if (!settle(ok)) return;
                 load_cols<UPW, U>(wa, P.fc_w, C4, C, cw, CW, lane);
+                ln_params(P.ln2_w, P.ln2_b);
                 for (int e = tid; e < C; e += PT) {
                     const int h = e >> 6;
                     float mx = -INFINITY, Ls = 0.f, acc = 0.f;
@@ -623,9 +613,9 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
                 if (ctrl && c >= 0) put_all(tx + c, tl.xs, (xo + sm.red[j][q]) + bo, TC);
             } else {
                 load_cols<UPW, U>(wa, P.fc_w, C4, C, cw, CW, lane);
+                ln_params(P.ln2_w, P.ln2_b);
             }
             bo = slot_bias(P.fc_b, C4);
-            ln_params(P.ln2_w, P.ln2_b);
 
             // ---------------- phase D: LayerNorm 2, fc + b, GELU into hid
             if (!settle(fetch_x(TC))) return;
@@ -656,31 +646,36 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
                 const int c = ctrl ? slot_col(lane, C, CW, j, q) : -1;
                 float xo = 0.f;
                 bool ok = true;
-                if (ctrl) ok = fetch_x1(c, TC, xo);
                 {
+                    // one wait for hid and the control lane's x
                     constexpr int NH = (1024 * U + PT - 1) / PT;
                     const int tt = opaque_v(tid);
-                    int idx[NH];
-                    bool need[NH];
-                    float hv[NH];
+                    int idx[NH + 1];
+                    bool need[NH + 1];
+                    float hv[NH + 1];
 #pragma unroll
                     for (int k = 0; k < NH; k++) {
                         idx[k] = min(tt + PT * k, C4 - 1);
                         need[k] = tt + PT * k < C4;
                     }
-                    const int nk = min(NH, (C4 - (tt & ~63) + PT - 1) / PT);
-                    const bool ok2 = fetch<NH>(rh, idx, need, TD, hv, abortw,
-                                               opaque_s(__builtin_amdgcn_readfirstlane(nk)));
-                    ok = ok && ok2;
+                    idx[NH] = (int)((rx + max(c, 0)) - rh);
+                    need[NH] = c >= 0;
+                    const unsigned en = (slots_below(C4, tt) & ((1u << NH) - 1u)) |
+                                        (ctrl ? 1u << NH : 0u);
+                    ok = fetch<NH + 1>(rh, idx, need, TD, hv, abortw, en, 1u << NH, TC);
 #pragma unroll
                     for (int k = 0; k < NH; k++)
                         if (need[k]) actf[tt + PT * k] = hv[k];
+                    if (ctrl) xo = hv[NH];
                 }
                 if (!settle(ok)) return;
-                if (l + 1 < L)
+                if (l + 1 < L) {
                     load_cols<UPW, U>(wa, PN.attn_w, C3, C, cw, CW, lane);
-                else  // the first UPW rounds of lm_head columns (tied wte)
+                    ln_params(PN.ln1_w, PN.ln1_b);
+                } else {  // the first UPW rounds of lm_head columns (tied wte)
                     load_cols<UPW, U>(wa, a.wte, V, C, cw, CW, lane);
+                    ln_params(a.lnf_w, a.lnf_b);
+                }
                 if (!ctrl) {
                     float acc[UPW];
                     col_dots<1, 4 * U>(acc, wb, sm.act, C, C4, cw, CW, lane);
@@ -692,14 +687,12 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
                 if (ctrl && c >= 0) put_all(tx + c, tl.xs, (xo + sm.red[j][q]) + bo, TE);
             } else if (l + 1 < L) {
                 load_cols<UPW, U>(wa, PN.attn_w, C3, C, cw, CW, lane);
+                ln_params(PN.ln1_w, PN.ln1_b);
             } else {
                 load_cols<UPW, U>(wa, a.wte, V, C, cw, CW, lane);
+                ln_params(a.lnf_w, a.lnf_b);
             }
             bo = slot_bias(PN.attn_b, C3);
-            if (l + 1 < L)
-                ln_params(PN.ln1_w, PN.ln1_b);
-            else
-                ln_params(a.lnf_w, a.lnf_b);
         }
 
         // ---------------- phase F: final LayerNorm, lm_head (tied wte), argmax partials
