@@ -27,8 +27,23 @@
 // grow monotonically over launches, and every buffer is rewritten only
 // after all consumers of its previous contents have provably read them (a
 // producer of version v+1 has consumed, through an all-to-all phase, data
-// made after every workgroup read version v). A poll limit turns a stall
-// into an error flag that every waiting workgroup sees and exits on.
+// made after every workgroup read version v). Per buffer (every workgroup
+// owns QKV and fc columns, so their outputs come from all workgroups):
+//   q/k/v of row t: written in A(l+1) after reading x(E(l)), made from
+//     hid(l) of every workgroup, made after x(C(l)), made after every
+//     attention partial of B(l), made after the reads of A(l)'s words.
+//   attention partials: written in B(l+1) after q/k/v of A(l+1), made after
+//     x(E(l)), made from hid(l) of every workgroup, each of which read its
+//     partials of C(l) before it made hid(l).
+//   x: C(l) and E(l) rewrite it; a writer has read inputs made by every
+//     workgroup after that workgroup's last read of x (hid(l) for E, the
+//     partials of B(l+1) from q/k/v of every workgroup for C(l+1)).
+//   hid: written in D(l+1) after x(C(l+1)), made after the partials of
+//     B(l+1), made after q/k/v from every workgroup, each of which read
+//     its hid(l) in E(l) before A(l+1).
+//   argmax partials: rewritten a whole step later, after the same chains.
+// A poll limit turns a stall into an error flag that every waiting
+// workgroup sees and exits on.
 //
 // Cache rows written in a step are read by later steps with plain loads:
 // the writer's later loads wait for its stores, before it publishes the
