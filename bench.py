@@ -6,8 +6,11 @@ logits [16, 1024, 50257] left in HBM. Prints one JSON line:
   roofline  the MFMA GEMM kernels (all linear layers and the lm_head), each
             launch timed with a HIP event pair on the library's stream during
             the same steps, against MI355X's dense fp32 matrix peak;
-  decode    greedy single-token steps with the KV cache (one replayed HIP
-            graph per step), tok/s and algorithmic HBM bytes / time;
+  loss      cross-entropy of those logits against next-token targets, on
+            the device (HBM-bound; GB/s of one read of the logits);
+  decode    greedy single-token steps with the KV cache (B=1: all steps in
+            one persistent launch; otherwise one replayed HIP graph per
+            step), tok/s and algorithmic HBM bytes / time;
   cpu_baseline  the oracle (C restatement of the reference's fast path with
             OpenBLAS) timed on this host on a bounded sample.
 --workload medium / xl measures GPT-2 medium (prefill B=8, decode B=8 after a
@@ -82,6 +85,35 @@ def prefill(m: cngpt_amd.Model, cfg, B: int, T: int, steps: int, warmup: int):
     prof = m.profile_read()
     m.profile_reset()
     return dt, prof
+
+
+def loss_leg(m: cngpt_amd.Model, cfg, B: int, T: int, steps: int):
+    """Cross-entropy (cross_entropy_fwd semantics) of the [B, T, V] logits the
+    last forward left in HBM against next-token targets: `steps` launches,
+    each timed with a HIP event pair on the library's stream. Algorithmic
+    bytes per launch: every logit once, plus the target and row term of
+    each row."""
+    tokens = lcg_tokens(B * T, cfg.vocab_size, 12345)
+    m.upload_targets(np.roll(tokens, -1).reshape(B, T))
+    m.cross_entropy_resident(B, T)
+    loss = m.read_loss()
+    m.profile_reset()
+    m.profile(True)
+    for _ in range(steps):
+        m.cross_entropy_resident(B, T)
+    m.synchronize()
+    m.profile(False)
+    p = m.profile_read()["loss"]
+    m.profile_reset()
+    ms = p["ms"] / p["launches"]
+    nbytes = 4.0 * B * T * cfg.vocab_size + 8.0 * B * T
+    return {"loss": round(loss, 6), "ms_per_launch": round(ms, 4),
+            "hbm": {"bound": "hbm", "achieved": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                    "peak": PEAK_HBM / 1e9, "unit": "GB/s",
+                    "frac": round(nbytes / (ms * 1e-3) / PEAK_HBM, 4),
+                    "bytes_per_launch": nbytes},
+            "kernel": "k_ce_rows + k_ce_mean", "launches": p["launches"],
+            "targets": "next token of the same LCG stream"}
 
 
 def decode_bytes(cfg, params_n: int, B: int, first_pos: int, steps: int) -> float:
@@ -245,6 +277,7 @@ def main():
     gemm_ms_avg = g["ms"] / g["launches"]
     achieved = g["flops"] / (g["ms"] * 1e-3)
     gemm_share = g["ms"] / (dt * 1e3)
+    loss = loss_leg(m, cfg, B, T, args.steps)
 
     dec_dt, dec_path = decode(m, cfg, dB, prompt, dsteps)
     dec_bytes = decode_bytes(cfg, params.size, dB, prompt, dsteps)
@@ -293,6 +326,7 @@ def main():
                      "avg_launch_ms": round(gemm_ms_avg, 4),
                      "launches": g["launches"], "share_of_step": round(gemm_share, 4)},
         "gemm_mfma_util_pct": round(100 * achieved / PEAK_FP32_MFMA, 2),
+        "loss": loss,
         "decode": {"tok_s": round(dsteps * dB / dec_dt, 1),
                    "ms_per_step": round(dec_dt * 1e3 / dsteps, 4),
                    "prompt": prompt, "steps": dsteps, "B": dB, "sampling": "greedy", "path": dec_path,

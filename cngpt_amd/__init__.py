@@ -8,6 +8,8 @@ There is no CPU fallback: if the library is missing, loading it raises.
 Mirrors the reference's inference interface:
   ``Model.forward(tokens)``           gpt_forward_fast (src/fast.c:227-333)
   ``Model.forward(tokens, ALL)``      all-position logits (src/model.c:612-614)
+  ``Model.loss(tokens, targets)``     gpt_forward with targets: logits and the
+                                      cross_entropy_fwd loss (src/model.c:617-623)
   ``init_weights(cfg, seed)``         gpt_init_weights after srand(seed)
   ``load_weights / save_weights``     the weight file of src/model.c:177-231
 """
@@ -25,9 +27,9 @@ LIB_PATH = os.path.join(_HERE, "libcngpt_hip.so")
 
 LAST, ALL = 0, 1
 (K_GEMM, K_GEMV, K_ATTN, K_ATTN_ROW, K_LAYERNORM, K_EMBED, K_GATHER, K_ARGMAX,
- K_SAMPLE, K_STEP) = range(10)
+ K_SAMPLE, K_STEP, K_LOSS) = range(11)
 KERNEL_CLASSES = ["gemm", "gemv", "attn", "attn_row", "layernorm", "embed", "gather", "argmax",
-                  "sample", "step"]
+                  "sample", "step", "loss"]
 # decode paths (include/cngpt_hip.h)
 DECODE_AUTO, DECODE_KERNELS, DECODE_PERSISTENT = 0, 1, 2
 
@@ -74,7 +76,9 @@ EXPORTS = [
     "cngpt_hip_last_error", "cngpt_hip_create", "cngpt_hip_destroy", "cngpt_hip_num_params",
     "cngpt_hip_load_params", "cngpt_hip_reserve", "cngpt_hip_forward",
     "cngpt_hip_upload_tokens", "cngpt_hip_forward_resident", "cngpt_hip_synchronize",
-    "cngpt_hip_read_logits", "cngpt_hip_logits_device", "cngpt_hip_decode_begin",
+    "cngpt_hip_read_logits", "cngpt_hip_logits_device", "cngpt_hip_cross_entropy",
+    "cngpt_hip_upload_targets", "cngpt_hip_cross_entropy_resident", "cngpt_hip_read_loss",
+    "cngpt_hip_decode_begin",
     "cngpt_hip_decode_step", "cngpt_hip_generate", "cngpt_hip_argmax", "cngpt_hip_sample",
     "cngpt_hip_decode_length", "cngpt_hip_set_decode_path", "cngpt_hip_decode_path",
     "cngpt_hip_profile_enable", "cngpt_hip_profile_reset", "cngpt_hip_profile_read",
@@ -110,6 +114,12 @@ def lib():
     L.cngpt_hip_read_logits.argtypes = [_VP, ctypes.c_size_t, ctypes.c_size_t, _F]
     L.cngpt_hip_logits_device.argtypes = [_VP]
     L.cngpt_hip_logits_device.restype = _VP
+    L.cngpt_hip_cross_entropy.argtypes = [_VP, _I, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                          _F, _F]
+    L.cngpt_hip_upload_targets.argtypes = [_VP, _I, ctypes.c_int, ctypes.c_int]
+    L.cngpt_hip_cross_entropy_resident.argtypes = [_VP, ctypes.c_int, ctypes.c_int,
+                                                   ctypes.c_int]
+    L.cngpt_hip_read_loss.argtypes = [_VP, _F, _F]
     L.cngpt_hip_decode_begin.argtypes = [_VP, _I, ctypes.c_int, ctypes.c_int, ctypes.c_int, _F]
     L.cngpt_hip_decode_step.argtypes = [_VP, _I, _F]
     L.cngpt_hip_generate.argtypes = [_VP, ctypes.c_int, ctypes.c_float, ctypes.c_int, _F, _I]
@@ -253,6 +263,51 @@ class Model:
         out = np.empty(count, dtype=np.float32)
         _check(lib().cngpt_hip_read_logits(self._h, offset, count, _fp(out)), "read_logits")
         return out
+
+    # -- loss -----------------------------------------------------------
+    def cross_entropy(self, targets, probs: bool = False, rows: bool = False):
+        """Cross-entropy of the held logits against targets [B, T] ([B] after a
+        LAST forward or a decode step): the mean loss, and with rows=True also
+        the [B, T] row terms. probs=True replaces the held logits by their
+        softmax (cross_entropy_fwd's probs_out, src/ops.c:499-574)."""
+        targets = np.ascontiguousarray(targets, dtype=np.int32)
+        if targets.ndim == 1:
+            targets = targets.reshape(-1, 1)
+        B, T = targets.shape
+        loss = ctypes.c_float()
+        per_row = np.empty((B, T), np.float32) if rows else None
+        _check(lib().cngpt_hip_cross_entropy(self._h, _ip(targets), B, T, int(probs),
+                                             ctypes.byref(loss),
+                                             _fp(per_row) if rows else None), "cross_entropy")
+        return (loss.value, per_row) if rows else loss.value
+
+    def loss(self, tokens, targets, copy_logits: bool = False):
+        """gpt_forward(m, tokens, targets, B, T) (src/model.c:442-625): the
+        all-position forward, then the mean cross-entropy over its logits,
+        which stay on the device unless copy_logits. Returns the loss, or
+        (loss, logits [B, T, V])."""
+        logits = self.forward(tokens, ALL, copy=copy_logits)
+        loss = self.cross_entropy(targets)
+        return (loss, logits) if copy_logits else loss
+
+    def upload_targets(self, targets) -> None:
+        targets = np.ascontiguousarray(targets, dtype=np.int32)
+        _check(lib().cngpt_hip_upload_targets(self._h, _ip(targets), *targets.shape),
+               "upload_targets")
+
+    def cross_entropy_resident(self, B: int, T: int, probs: bool = False) -> None:
+        _check(lib().cngpt_hip_cross_entropy_resident(self._h, B, T, int(probs)),
+               "cross_entropy_resident")
+        self._loss_rows = B * T
+
+    def read_loss(self, rows: bool = False):
+        """Mean of the last cross_entropy_resident, and with rows=True its
+        B*T row terms."""
+        loss = ctypes.c_float()
+        per_row = np.empty(getattr(self, "_loss_rows", 0), np.float32) if rows else None
+        _check(lib().cngpt_hip_read_loss(self._h, ctypes.byref(loss),
+                                         _fp(per_row) if rows else None), "read_loss")
+        return (loss.value, per_row) if rows else loss.value
 
     # -- decode ---------------------------------------------------------
     def decode_begin(self, prompt, capacity: int) -> np.ndarray:

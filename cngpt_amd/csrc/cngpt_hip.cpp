@@ -82,6 +82,10 @@ struct cngpt_hip_ctx {
     int attn_splits = 0;
     float* draws = nullptr;      // [capKV+1][B] uniform draws for sampling
     float* prob = nullptr;       // [B][ldp] sampling scratch
+    int* tgt = nullptr;          // [B*T] cross-entropy targets
+    float* row_loss = nullptr;   // [B*T] cross-entropy row terms
+    float* loss = nullptr;       // mean cross-entropy
+    long loss_rows = 0;          // rows of the last cross-entropy (0: none)
     long ldp = 0;
     int pos_host = 0;            // staging for the position upload
     unsigned long long* ptag = nullptr;  // exchange words of the persistent decode
@@ -338,7 +342,7 @@ int ensure_arena(cngpt_hip_ctx* h, int B, int T, int all, int kv) {
     const size_t qkv_rows = std::max(rows, L * nB * (size_t)nKV);
     const int kps = attn_dec_keys_per_split(c.n_embd / c.n_head);
     const int splits = (c.block_size + kps - 1) / kps;
-    size_t sz[24], total = 0;
+    size_t sz[32], total = 0;
     int n = 0;
     sz[n++] = rows * sizeof(int);             // tok
     sz[n++] = 4 * sizeof(int);                // dev_err, pos
@@ -360,6 +364,9 @@ int ensure_arena(cngpt_hip_ctx* h, int B, int T, int all, int kv) {
     sz[n++] = nB * C * 4;                     // aoutc
     sz[n++] = nB * 4 * C * 4;                 // hidc
     sz[n++] = (size_t)persist_tagged_words(c.n_embd, c.n_head) * 8;  // ptag
+    sz[n++] = rows * sizeof(int);             // tgt
+    sz[n++] = rows * sizeof(float);           // row_loss
+    sz[n++] = sizeof(float);                  // loss
     for (int i = 0; i < n; i++) total += align_up(sz[i]);
 
     if (h->d_act) {
@@ -407,6 +414,10 @@ int ensure_arena(cngpt_hip_ctx* h, int B, int T, int all, int kv) {
     h->ptag = (unsigned long long*)take(sz[n++]);
     h->ptag_next = 0;
     HIP_TRY(hipMemsetAsync(h->ptag, 0, sz[n - 1], h->stream));
+    h->tgt = (int*)take(sz[n++]);
+    h->row_loss = (float*)take(sz[n++]);
+    h->loss = (float*)take(sz[n++]);
+    h->loss_rows = 0;
     h->capB = nB; h->capT = nT; h->capAll = nAll; h->capKV = nKV;
     HIP_TRY(hipMemsetAsync(h->dev_err, 0, 4 * sizeof(int), h->stream));
     return 0;
@@ -639,6 +650,7 @@ int check_dev_err(cngpt_hip_ctx* h) {
     if (e) {
         HIP_TRY(hipMemsetAsync(h->dev_err, 0, sizeof(int), h->stream));
         if (e & 2) return fail("persistent decode: a wait for a value of another workgroup timed out");
+        if (e & 4) return fail("cross-entropy targets outside [0, %d) were clamped", h->cfg.vocab_size);
         return fail("device-resident token ids outside [0, %d) were clamped", h->cfg.vocab_size);
     }
     return 0;
@@ -843,6 +855,64 @@ int cngpt_hip_read_logits(cngpt_hip_ctx* h, size_t offset, size_t count, float* 
 }
 
 const float* cngpt_hip_logits_device(cngpt_hip_ctx* h) { return h ? h->logits : nullptr; }
+
+int cngpt_hip_upload_targets(cngpt_hip_ctx* h, const int* targets, int B, int T) {
+    if (need_params(h)) return -1;
+    if (!targets) return fail("null targets");
+    if (B <= 0 || T <= 0) return fail("B=%d T=%d must be positive", B, T);
+    if (!h->tgt || (long)B * T > (long)h->capB * h->capT)
+        return fail("targets [%d, %d] exceed the reserved %d x %d rows", B, T, h->capB, h->capT);
+    for (long i = 0; i < (long)B * T; i++)
+        if (targets[i] < 0 || targets[i] >= h->cfg.vocab_size)
+            return fail("target %d at index %ld outside [0, %d)", targets[i], i,
+                        h->cfg.vocab_size);
+    HIP_TRY(hipSetDevice(h->device));
+    HIP_TRY(hipMemcpyAsync(h->tgt, targets, (size_t)B * T * sizeof(int), hipMemcpyHostToDevice,
+                           h->stream));
+    HIP_TRY(hipStreamSynchronize(h->stream));
+    return 0;
+}
+
+int cngpt_hip_cross_entropy_resident(cngpt_hip_ctx* h, int B, int T, int probs) {
+    if (need_params(h)) return -1;
+    if (B <= 0 || T <= 0) return fail("B=%d T=%d must be positive", B, T);
+    const long rows = (long)B * T;
+    const int V = h->cfg.vocab_size;
+    if (!h->logits || (size_t)rows * V != h->logits_count)
+        return fail("cross_entropy: %ld rows of %d logits, but %zu logits are held", rows, V,
+                    h->logits_count);
+    if (rows > (long)h->capB * h->capT)
+        return fail("targets [%d, %d] exceed the reserved %d x %d rows", B, T, h->capB, h->capT);
+    HIP_TRY(hipSetDevice(h->device));
+    {
+        Timed t(h, CNGPT_K_LOSS, 0.0, 4.0 * rows * V * (probs ? 3 : 1) + 8.0 * rows);
+        HIP_TRY(launch_cross_entropy(h->logits, rows, V, h->tgt, h->row_loss, h->loss, probs,
+                                     h->dev_err, h->stream));
+    }
+    h->loss_rows = rows;
+    return 0;
+}
+
+int cngpt_hip_read_loss(cngpt_hip_ctx* h, float* loss_out, float* row_loss) {
+    if (!h) return fail("null handle");
+    if (h->loss_rows <= 0) return fail("no cross-entropy has been computed");
+    HIP_TRY(hipSetDevice(h->device));
+    if (loss_out)
+        HIP_TRY(hipMemcpyAsync(loss_out, h->loss, sizeof(float), hipMemcpyDeviceToHost,
+                               h->stream));
+    if (row_loss)
+        HIP_TRY(hipMemcpyAsync(row_loss, h->row_loss, (size_t)h->loss_rows * sizeof(float),
+                               hipMemcpyDeviceToHost, h->stream));
+    HIP_TRY(hipStreamSynchronize(h->stream));
+    return check_dev_err(h);
+}
+
+int cngpt_hip_cross_entropy(cngpt_hip_ctx* h, const int* targets, int B, int T, int probs,
+                            float* loss_out, float* row_loss) {
+    if (cngpt_hip_upload_targets(h, targets, B, T)) return -1;
+    if (cngpt_hip_cross_entropy_resident(h, B, T, probs)) return -1;
+    return cngpt_hip_read_loss(h, loss_out, row_loss);
+}
 
 int cngpt_hip_decode_begin(cngpt_hip_ctx* h, const int* prompt, int B, int T, int capacity,
                            float* logits_out) {

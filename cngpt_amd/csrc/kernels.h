@@ -168,3 +168,11 @@ hipError_t launch_decode_persist(const PersistArgs& a, int G, hipStream_t s);
 // qkv + (b * seq_stride + t) * 3C. out row (b*T + t) gets the merged heads.
 hipError_t launch_attention_causal(const float* qkv, long seq_stride, float* out, int B, int T,
                                    int C, int H, hipStream_t s);
+
+// loss.hip
+// Cross-entropy of rows x V logits against targets [rows]: row_loss[r] =
+// log(sum_v exp(x_v - max)) - (x[target] - max), loss[0] = their mean.
+// probs != 0 overwrites the logits with their softmax. Targets outside
+// [0, V) are clamped and reported through *err (bit 2).
+hipError_t launch_cross_entropy(float* logits, long rows, int V, const int* targets,
+                                float* row_loss, float* loss, int probs, int* err, hipStream_t s);

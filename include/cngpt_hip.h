@@ -49,7 +49,8 @@ enum {
     CNGPT_K_ARGMAX = 7,
     CNGPT_K_SAMPLE = 8,      /* top-k sampling */
     CNGPT_K_STEP = 9,        /* whole decode steps in one persistent launch */
-    CNGPT_K_COUNT = 10
+    CNGPT_K_LOSS = 10,       /* cross-entropy over the held logits */
+    CNGPT_K_COUNT = 11
 };
 
 /* How decode steps run. KERNELS: one replayed graph of per-stage kernels
@@ -102,6 +103,28 @@ int  cngpt_hip_synchronize(cngpt_hip_ctx *h);
 int  cngpt_hip_read_logits(cngpt_hip_ctx *h, size_t offset, size_t count, float *dst);
 /* Device address of the logits of the last forward / decode step. */
 const float *cngpt_hip_logits_device(cngpt_hip_ctx *h);
+
+/* Cross-entropy of the logits held on the device against targets [B, T]
+ * (host ids, validated 0 <= id < vocab_size): cross_entropy_fwd
+ * (src/ops.c:499-574) as gpt_forward calls it after the lm_head
+ * (src/model.c:617-623). The held logits must be B*T rows: the [B, T, V]
+ * of a CNGPT_ALL forward, or with T = 1 the [B, V] of a CNGPT_LAST forward
+ * or a decode step. Row r's term is log(sum_v exp(logit_v - max)) -
+ * (logit[target] - max); *loss_out (may be NULL) receives their mean over
+ * the B*T rows, row_loss (may be NULL) the B*T terms. probs != 0 also
+ * replaces the held logits by their softmax, in place (probs_out of
+ * cross_entropy_fwd, same [B*T, V] layout; read_logits then returns
+ * probabilities). Blocks until done. */
+int  cngpt_hip_cross_entropy(cngpt_hip_ctx *h, const int *targets, int B, int T, int probs,
+                             float *loss_out, float *row_loss);
+/* Split form: upload targets [B, T] once (validated as above; the
+ * activation allocation must hold B*T rows, see cngpt_hip_reserve), enqueue
+ * the loss on the handle's stream without blocking, then read the mean and
+ * (optionally) the row terms of the last cross-entropy (row_loss must hold
+ * the B*T floats of that call). */
+int  cngpt_hip_upload_targets(cngpt_hip_ctx *h, const int *targets, int B, int T);
+int  cngpt_hip_cross_entropy_resident(cngpt_hip_ctx *h, int B, int T, int probs);
+int  cngpt_hip_read_loss(cngpt_hip_ctx *h, float *loss_out, float *row_loss);
 
 /* Incremental decode with a device KV cache (no reference counterpart:
  * gpt_sample, src/model.c:991-1016, recomputes the whole prefix).

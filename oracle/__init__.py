@@ -112,6 +112,9 @@ def lib():
     L.orc_sample_top_k.argtypes = [_F, ctypes.c_int, ctypes.c_float, ctypes.c_int,
                                    ctypes.c_float]
     L.orc_sample_top_k.restype = ctypes.c_int
+    L.orc_cross_entropy.argtypes = [_F, _I, _F, _F, ctypes.c_int, ctypes.c_int,
+                                    ctypes.c_int]
+    L.orc_cross_entropy.restype = ctypes.c_float
     L.orc_srand.argtypes = [ctypes.c_uint]
     L.orc_rand_uniform.restype = ctypes.c_float
     blas = os.environ.get("CNGPT_ORACLE_BLAS") or find_openblas()
@@ -230,6 +233,21 @@ def linear(X, W, b=None):
 def sample_top_k(logits, temp: float, top_k: int, r: float) -> int:
     logits = np.ascontiguousarray(logits, np.float32)
     return lib().orc_sample_top_k(_fp(logits), logits.size, temp, top_k, r)
+
+
+def cross_entropy(logits, targets, want_probs: bool = False):
+    """cross_entropy_fwd (src/ops.c:499-574) over logits [..., V] and
+    targets [...]: (mean loss, per-row loss, probs or None)."""
+    logits = np.ascontiguousarray(logits, np.float32)
+    V = logits.shape[-1]
+    rows = logits.size // V
+    targets = np.ascontiguousarray(targets, np.int32).reshape(-1)
+    assert targets.size == rows and (rows == 0 or (targets.min() >= 0 and targets.max() < V))
+    row_loss = np.empty(rows, np.float32)
+    probs = np.empty((rows, V), np.float32) if want_probs else None
+    loss = lib().orc_cross_entropy(_fp(logits), _ip(targets),
+                                   _fp(probs) if want_probs else None, _fp(row_loss), 1, rows, V)
+    return float(loss), row_loss, probs
 
 
 def srand(seed: int) -> None:

@@ -6,7 +6,8 @@
  *
  * Restates, with file:line of the reference at each function:
  *   src/model.c  parameter count/layout, seeded init, sample_top_k
- *   src/ops.c    layernorm / gelu / softmax / causal mask / linear (scalar)
+ *   src/ops.c    layernorm / gelu / softmax / causal mask / linear /
+ *                cross-entropy (scalar paths)
  *   src/fast.c   gpt_forward_fast, its column-split products, its threads
  * The matrix products are cblas_sgemm calls, as in the reference; the CBLAS
  * is bound at run time (orc_use_blas) and a blocked C product stands in
@@ -494,4 +495,35 @@ int orc_sample_top_k(const float *logits, int V, float temp, int top_k, float r)
     }
     free(p);
     return tok;
+}
+
+/* ------------------------------------------------------------------ */
+/* Cross-entropy (src/ops.c:499-574, the scalar branch 549-573)        */
+/* ------------------------------------------------------------------ */
+
+float orc_cross_entropy(const float *logits, const int *targets, float *probs,
+                        float *row_loss, int B, int T, int V)
+{
+    const int BT = B * T;
+    float loss = 0.0f;
+    for (int bt = 0; bt < BT; bt++) {
+        const float *lg = logits + (size_t)bt * V;
+        float mx = -FLT_MAX;                              /* ops.c:553-555 */
+        for (int v = 0; v < V; v++) if (lg[v] > mx) mx = lg[v];
+        float sum = 0.0f;                                 /* ops.c:557-561 */
+        for (int v = 0; v < V; v++) {
+            float e = expf(lg[v] - mx);
+            if (probs) probs[(size_t)bt * V + v] = e;
+            sum += e;
+        }
+        const float log_sum = logf(sum);                  /* ops.c:562-565 */
+        if (probs) {
+            const float inv = 1.0f / sum;
+            for (int v = 0; v < V; v++) probs[(size_t)bt * V + v] *= inv;
+        }
+        const float term = (lg[targets[bt]] - mx) - log_sum;  /* ops.c:567-568 */
+        if (row_loss) row_loss[bt] = -term;
+        loss -= term;
+    }
+    return loss / (float)BT;                              /* ops.c:573 */
 }

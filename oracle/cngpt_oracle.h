@@ -77,6 +77,15 @@ int  orc_forward(const orc_cfg *c, const float *params, const int *tokens,
  * passed in instead of taken from rand(). */
 int  orc_sample_top_k(const float *logits, int V, float temp, int top_k, float r);
 
+/* cross_entropy_fwd, src/ops.c:499-574 (its scalar branch): per row the
+ * max, the sum of expf(logit - max), log_sum = logf(sum), and the loss
+ * term (logit[target] - max) - log_sum, subtracted from an fp32
+ * accumulator in row order; returns the accumulator / (B*T). probs
+ * (may be NULL) receives the softmax [B*T, V]; row_loss (may be NULL)
+ * the negated term of each row. */
+float orc_cross_entropy(const float *logits, const int *targets, float *probs,
+                        float *row_loss, int B, int T, int V);
+
 /* The draw sample_top_k makes (src/model.c:979): rand()/(RAND_MAX+1.0f). */
 void  orc_srand(unsigned seed);
 float orc_rand_uniform(void);

@@ -99,6 +99,70 @@ def test_softmax_and_mask():
     assert np.abs(p - ref).max() < 1e-6
 
 
+# ---------------------------------------------------------------- cross-entropy
+
+def test_cross_entropy_kat():                # check_ops.c:191-210
+    tg = np.array([0, 1], np.int32)
+    loss, rows, probs = oracle.cross_entropy(np.array([[10, 0], [0, 10]], np.float32), tg, True)
+    assert abs(loss) < 0.01
+    assert abs(probs[0, 0] - 1) < 0.01 and abs(probs[1, 1] - 1) < 0.01
+    loss2, _, _ = oracle.cross_entropy(np.array([[0, 10], [10, 0]], np.float32), tg)
+    assert loss2 > 5.0
+    # the closed forms of both cases: log(1 + e^-10) and log(1 + e^10)
+    assert abs(loss - math.log1p(math.exp(-10))) < 1e-6
+    assert abs(loss2 - math.log1p(math.exp(10))) < 1e-5
+
+
+def test_cross_entropy_vs_torch_float64():
+    """torch's cross_entropy in float64, the loss verify_forward.py:110-112
+    checks cngpt against; per row against scipy's logsumexp."""
+    rng = np.random.default_rng(4)
+    for rows, V, scale in [(1, 2, 1.0), (37, 1000, 5.0), (6, 50257, 3.0)]:
+        lg = (rng.standard_normal((rows, V)) * scale + 40).astype(np.float32)
+        tg = rng.integers(0, V, size=rows, dtype=np.int32)
+        loss, per_row, probs = oracle.cross_entropy(lg, tg, True)
+        l64 = lg.astype(np.float64)
+        ref = float(torch.nn.functional.cross_entropy(torch.from_numpy(l64),
+                                                      torch.from_numpy(tg.astype(np.int64))))
+        # a running fp32 sum of V positive terms is within V * 2^-24 of the
+        # exact one, relatively, which bounds the error of log(sum)
+        tol = 4e-6 * abs(ref) + V * 2.0**-24
+        assert abs(loss - ref) <= tol, (rows, V, loss, ref)
+        ref_rows = scipy.special.logsumexp(l64, axis=1) - l64[np.arange(rows), tg]
+        assert np.abs(per_row - ref_rows).max() <= tol
+        np.testing.assert_allclose(probs, scipy.special.softmax(l64, axis=1),
+                                   rtol=4e-6 + V * 2.0**-24, atol=1e-9)
+        assert np.array_equal(probs, oracle.softmax(lg))  # same arithmetic as ops.c:424-482
+
+
+def test_cross_entropy_closed_forms():
+    # V equal logits: log V whatever the level (expf(125) overflows without
+    # the max subtraction)
+    for V in (1, 7, 50257):
+        for c in (0.0, 125.0, -300.0):
+            loss, _, _ = oracle.cross_entropy(np.full((3, V), c, np.float32),
+                                              np.array([0, V // 2, V - 1], np.int32))
+            assert abs(loss - math.log(V)) <= 1e-6 * max(1.0, math.log(V)), (V, c, loss)
+    # the mean is over all B*T rows: rows with losses log(1+e^-d) for d = 0..5
+    d = np.arange(6, dtype=np.float32)
+    lg = np.stack([d, np.zeros(6, np.float32)], 1).reshape(2, 3, 2)
+    loss, per_row, _ = oracle.cross_entropy(lg, np.zeros((2, 3), np.int32))
+    want = np.log1p(np.exp(-d.astype(np.float64)))
+    np.testing.assert_allclose(per_row, want, rtol=1e-6, atol=1e-7)
+    assert abs(loss - want.mean()) < 1e-6
+    # a per-row shift leaves the loss unchanged; the target's logit enters
+    # with a minus sign
+    rng = np.random.default_rng(8)
+    lg = rng.standard_normal((4, 300)).astype(np.float32)
+    tg = rng.integers(0, 300, size=4, dtype=np.int32)
+    base, _, _ = oracle.cross_entropy(lg, tg)
+    shifted, _, _ = oracle.cross_entropy(lg + np.float32(64), tg)
+    assert abs(base - shifted) < 1e-5
+    up = lg.copy()
+    up[np.arange(4), tg] += 1
+    assert oracle.cross_entropy(up, tg)[0] < base
+
+
 # ---------------------------------------------------------------- whole forward
 
 def _hf_logits(cfg: oracle.Cfg, params: np.ndarray, tokens: np.ndarray) -> np.ndarray:
