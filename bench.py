@@ -8,6 +8,7 @@ logits [16, 1024, 50257] left in HBM. Prints one JSON line:
             the same steps, against MI355X's dense fp32 matrix peak;
   loss      cross-entropy of those logits against next-token targets, on
             the device (HBM-bound; GB/s of one read of the logits);
+  load      the weights as a weight file streamed to the device;
   decode    greedy single-token steps with the KV cache (B=1: all steps in
             one persistent launch; otherwise one replayed HIP graph per
             step), tok/s and algorithmic HBM bytes / time;
@@ -114,6 +115,34 @@ def loss_leg(m: cngpt_amd.Model, cfg, B: int, T: int, steps: int):
                     "bytes_per_launch": nbytes},
             "kernel": "k_ce_rows + k_ce_mean", "launches": p["launches"],
             "targets": "next token of the same LCG stream"}
+
+
+def load_leg(m: cngpt_amd.Model, cfg, params) -> dict:
+    """The weight file of these parameters streamed into the handle's
+    parameter allocation (cngpt_hip_load_file), from a warm page cache:
+    file written first, then timed loads."""
+    import tempfile
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "weights.bin")
+        cngpt_amd.save_weights(path, cfg, params)
+        m.load_file(path)
+        t, th = [], []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            m.load_file(path)
+            t.append(time.perf_counter() - t0)
+        for _ in range(2):
+            # the host-buffer route: whole file into host memory, then one upload
+            t0 = time.perf_counter()
+            _, p = cngpt_amd.load_weights(path)
+            m.load_params(p)
+            th.append(time.perf_counter() - t0)
+            del p
+    best = min(t)
+    nbytes = 4.0 * params.size
+    return {"bytes": nbytes, "s": round(best, 4), "gb_s": round(nbytes / best / 1e9, 2),
+            "host_buffer_s": round(min(th), 4),
+            "source": "page cache (file just written), pinned 16 MB chunks, 4 reader threads"}
 
 
 def decode_bytes(cfg, params_n: int, B: int, first_pos: int, steps: int) -> float:
@@ -290,6 +319,7 @@ def main():
     draws = np.random.default_rng(7).random((dsteps + 1) * dB).astype(np.float32)
     samp_dt, _ = decode(m, cfg, dB, prompt, dsteps, draws)
     ref_shape = reference_shape(m) if name == "small" else None
+    load = load_leg(m, cfg, params)
     m.close()
 
     # HBM-side bytes per GEMM launch from the committed rocprofv3 --pmc
@@ -327,6 +357,7 @@ def main():
                      "launches": g["launches"], "share_of_step": round(gemm_share, 4)},
         "gemm_mfma_util_pct": round(100 * achieved / PEAK_FP32_MFMA, 2),
         "loss": loss,
+        "load": load,
         "decode": {"tok_s": round(dsteps * dB / dec_dt, 1),
                    "ms_per_step": round(dec_dt * 1e3 / dsteps, 4),
                    "prompt": prompt, "steps": dsteps, "B": dB, "sampling": "greedy", "path": dec_path,

@@ -74,7 +74,8 @@ _VP = ctypes.c_void_p
 # Every symbol include/cngpt_hip.h, fast.h and model.h declare.
 EXPORTS = [
     "cngpt_hip_last_error", "cngpt_hip_create", "cngpt_hip_destroy", "cngpt_hip_num_params",
-    "cngpt_hip_load_params", "cngpt_hip_reserve", "cngpt_hip_forward",
+    "cngpt_hip_load_params", "cngpt_hip_file_config", "cngpt_hip_load_file",
+    "cngpt_hip_reserve", "cngpt_hip_forward",
     "cngpt_hip_upload_tokens", "cngpt_hip_forward_resident", "cngpt_hip_synchronize",
     "cngpt_hip_read_logits", "cngpt_hip_logits_device", "cngpt_hip_cross_entropy",
     "cngpt_hip_upload_targets", "cngpt_hip_cross_entropy_resident", "cngpt_hip_read_loss",
@@ -106,6 +107,8 @@ def lib():
     L.cngpt_hip_num_params.argtypes = [ctypes.POINTER(_Cfg)]
     L.cngpt_hip_num_params.restype = ctypes.c_long
     L.cngpt_hip_load_params.argtypes = [_VP, ctypes.POINTER(_Cfg), _F, ctypes.c_long]
+    L.cngpt_hip_file_config.argtypes = [ctypes.c_char_p, ctypes.POINTER(_Cfg), _Lp]
+    L.cngpt_hip_load_file.argtypes = [_VP, ctypes.c_char_p, ctypes.POINTER(_Cfg)]
     L.cngpt_hip_reserve.argtypes = [_VP, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int]
     L.cngpt_hip_forward.argtypes = [_VP, _I, ctypes.c_int, ctypes.c_int, ctypes.c_int, _F]
     L.cngpt_hip_upload_tokens.argtypes = [_VP, _I, ctypes.c_int, ctypes.c_int]
@@ -198,17 +201,47 @@ def load_weights(path: str) -> tuple[Config, np.ndarray]:
     return cfg, np.ascontiguousarray(p[:n])
 
 
+def file_config(path: str) -> tuple[Config, int]:
+    """Shape and parameter count of a weight file, validated without a GPU
+    (cngpt_hip_file_config)."""
+    c = _Cfg()
+    n = ctypes.c_long()
+    _check(lib().cngpt_hip_file_config(os.fsencode(path), ctypes.byref(c), ctypes.byref(n)),
+           "file_config")
+    return Config(c.n_layer, c.n_head, c.n_embd, c.vocab_size, c.block_size), n.value
+
+
 class Model:
     """One device handle: parameters in one allocation, activations in another."""
 
-    def __init__(self, cfg: Config, params: np.ndarray, device: int = 0):
+    def __init__(self, cfg: Config | None, params: np.ndarray | None, device: int = 0):
         L = lib()
         h = _VP()
         _check(L.cngpt_hip_create(device, ctypes.byref(h)), "create")
         self._h = h
         self.cfg = cfg
         self.decode_batch = 0
-        self.load_params(params)
+        if params is not None:
+            self.load_params(params)
+
+    @classmethod
+    def from_file(cls, path: str, device: int = 0) -> "Model":
+        """A handle whose parameters are streamed from a weight file straight
+        to the device (cngpt_hip_load_file; no host copy of the buffer)."""
+        m = cls(None, None, device)
+        try:
+            m.load_file(path)
+        except Exception:
+            m.close()
+            raise
+        return m
+
+    def load_file(self, path: str) -> Config:
+        c = _Cfg()
+        _check(lib().cngpt_hip_load_file(self._h, os.fsencode(path), ctypes.byref(c)),
+               "load_file")
+        self.cfg = Config(c.n_layer, c.n_head, c.n_embd, c.vocab_size, c.block_size)
+        return self.cfg
 
     def load_params(self, params: np.ndarray) -> None:
         params = np.ascontiguousarray(params, dtype=np.float32)

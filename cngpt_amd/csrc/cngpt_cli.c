@@ -218,16 +218,20 @@ static int cmd_sample(int argc, char **argv)
     if (!path) { fprintf(stderr, "sample: --weights is required\n"); return 1; }
     if (n_new <= 0) { fprintf(stderr, "sample: --tokens must be positive\n"); return 1; }
 
-    GPT m;
-    memset(&m, 0, sizeof(m));
-    if (gpt_load(&m, path) != 0) return 1;
-    const int V = m.cfg.vocab_size, Tmax = m.cfg.block_size;
+    /* The weights go from the file straight to the device (no host copy of
+     * the parameters); the header is validated first, without a GPU. */
+    cngpt_hip_config cfg;
+    if (cngpt_hip_file_config(path, &cfg, NULL) != 0) {
+        fprintf(stderr, "sample: %s\n", cngpt_hip_last_error());
+        return 1;
+    }
+    const int V = cfg.vocab_size, Tmax = cfg.block_size;
 
     int n_prompt = 1;
     for (const char *p = prompt_s; p && *p; p++) n_prompt += *p == ',';
     int *seq = malloc((size_t)(n_prompt + n_new) * sizeof(int));
     float *draws = malloc((size_t)n_new * sizeof(float));
-    if (!seq || !draws) { gpt_free(&m); return 1; }
+    if (!seq || !draws) { free(seq); free(draws); return 1; }
     if (prompt_s && *prompt_s) {
         int k = 0;
         const char *p = prompt_s;
@@ -236,7 +240,7 @@ static int cmd_sample(int argc, char **argv)
             long v = strtol(p, &end, 10);
             if (end == p || v < 0 || v >= V) {
                 fprintf(stderr, "sample: bad prompt token near \"%s\" (ids in [0, %d))\n", p, V);
-                free(seq); free(draws); gpt_free(&m);
+                free(seq); free(draws);
                 return 1;
             }
             seq[k++] = (int)v;
@@ -249,7 +253,7 @@ static int cmd_sample(int argc, char **argv)
     }
     if (n_prompt > Tmax) {
         fprintf(stderr, "sample: prompt of %d tokens exceeds block_size %d\n", n_prompt, Tmax);
-        free(seq); free(draws); gpt_free(&m);
+        free(seq); free(draws);
         return 1;
     }
 
@@ -259,15 +263,14 @@ static int cmd_sample(int argc, char **argv)
     Vocab vb;
     memset(&vb, 0, sizeof(vb));
     if (vocab_path && vocab_load(&vb, vocab_path) != 0) {
-        free(seq); free(draws); gpt_free(&m);
+        free(seq); free(draws);
         return 1;
     }
 
     cngpt_hip_ctx *h = NULL;
     const char *dev = getenv("CNGPT_HIP_DEVICE");
-    cngpt_hip_config cfg = { m.cfg.n_layer, m.cfg.n_head, m.cfg.n_embd, V, Tmax };
     int rc = cngpt_hip_create(dev && *dev ? atoi(dev) : 0, &h);
-    if (!rc) rc = cngpt_hip_load_params(h, &cfg, m.param_buf, m.n_params);
+    if (!rc) rc = cngpt_hip_load_file(h, path, NULL);
 
     /* New token i sees a context of n_prompt + i tokens; while that fits
      * block_size it comes from the KV cache. */
@@ -303,7 +306,6 @@ static int cmd_sample(int argc, char **argv)
     vocab_free(&vb);
     free(seq);
     free(draws);
-    gpt_free(&m);
     return rc ? 1 : 0;
 }
 

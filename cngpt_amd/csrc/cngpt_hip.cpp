@@ -9,12 +9,19 @@
 // and the rest of that layer on the B gathered rows (fast.c:287-311).
 #include <hip/hip_runtime.h>
 
+#include <fcntl.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
 #include <algorithm>
+#include <atomic>
+#include <cerrno>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <thread>
 #include <vector>
 
 #include "../../include/cngpt_hip.h"
@@ -656,6 +663,235 @@ int check_dev_err(cngpt_hip_ctx* h) {
     return 0;
 }
 
+// ---------------------------------------------------------------- parameters
+
+// Shapes the kernels take (on top of valid_cfg).
+int check_shape(const cngpt_hip_config* cfg) {
+    if (!valid_cfg(cfg)) return fail("invalid model shape");
+    if (cfg->n_embd % 4) return fail("n_embd %d must be a multiple of 4", cfg->n_embd);
+    const int hs = cfg->n_embd / cfg->n_head;
+    if (hs != 8 && hs != 16 && hs != 32 && hs != 64 && hs != 128)
+        return fail("head size %d not supported (8, 16, 32, 64, 128)", hs);
+    if (cfg->n_embd > 2048) return fail("n_embd %d above 2048", cfg->n_embd);
+    return 0;
+}
+
+long params_of(const cngpt_hip_config* c) {
+    const long C = c->n_embd, V = c->vocab_size, T = c->block_size, L = c->n_layer;
+    return V * C + T * C + L * (12 * C * C + 13 * C) + 2 * C;  // model.c:20-48
+}
+
+// Make h->d_params hold the parameters of shape cfg: reuse the allocation
+// when the shape is unchanged, else free it (and the activations, which
+// depend on the shape) and allocate anew.
+int params_prepare(cngpt_hip_ctx* h, const cngpt_hip_config* cfg, bool* same_shape) {
+    HIP_TRY(hipSetDevice(h->device));
+    *same_shape = h->d_params && memcmp(&h->cfg, cfg, sizeof(*cfg)) == 0;
+    if (*same_shape) return 0;
+    if (h->d_params) {
+        HIP_TRY(hipStreamSynchronize(h->stream));
+        HIP_TRY(hipFree(h->d_params));
+        h->d_params = nullptr;
+    }
+    if (h->d_act) {
+        drop_graph(h);
+        HIP_TRY(hipFree(h->d_act));
+        h->d_act = nullptr;
+        h->capB = h->capT = h->capAll = h->capKV = 0;
+        h->kvB = h->kvLen = 0;
+    }
+    h->have_params = false;
+    const long want = params_of(cfg);
+    if (hipMalloc(&h->d_params, (size_t)want * sizeof(float)) != hipSuccess) {
+        (void)hipGetLastError();
+        h->d_params = nullptr;
+        return fail("parameter allocation of %ld floats failed", want);
+    }
+    h->cfg = *cfg;  // the allocation now has this shape
+    return 0;
+}
+
+// Views of the uploaded parameters, carved like assign_weights
+// (src/model.c:54-83), and their device table for the persistent decode.
+int params_commit(cngpt_hip_ctx* h, const cngpt_hip_config* cfg, bool same_shape) {
+    h->cfg = *cfg;
+    h->n_params = params_of(cfg);
+    const long C = cfg->n_embd, V = cfg->vocab_size, T = cfg->block_size;
+    const float* p = h->d_params;
+    h->wte = p; p += V * C;
+    h->wpe = p; p += T * C;
+    h->layers.assign(cfg->n_layer, LayerW{});
+    for (int l = 0; l < cfg->n_layer; l++) {
+        LayerW& w = h->layers[l];
+        w.ln1_w = p; p += C;
+        w.ln1_b = p; p += C;
+        w.attn_w = p; p += 3 * C * C;
+        w.attn_b = p; p += 3 * C;
+        w.proj_w = p; p += C * C;
+        w.proj_b = p; p += C;
+        w.ln2_w = p; p += C;
+        w.ln2_b = p; p += C;
+        w.fc_w = p; p += 4 * C * C;
+        w.fc_b = p; p += 4 * C;
+        w.mlp_w = p; p += C * 4 * C;
+        w.mlp_b = p; p += C;
+    }
+    h->lnf_w = p; p += C;
+    h->lnf_b = p;
+    const size_t lbytes = (size_t)cfg->n_layer * sizeof(LayerW);
+    if (!same_shape || !h->d_layers) {
+        if (h->d_layers) HIP_TRY(hipFree(h->d_layers));
+        h->d_layers = nullptr;
+        if (hipMalloc(&h->d_layers, lbytes) != hipSuccess) {
+            (void)hipGetLastError();
+            h->d_layers = nullptr;
+            return fail("layer table allocation failed");
+        }
+    }
+    HIP_TRY(hipMemcpy(h->d_layers, h->layers.data(), lbytes, hipMemcpyHostToDevice));
+    h->have_params = true;
+    return 0;
+}
+
+// ---------------------------------------------------------------- weight file
+
+// The weight file: a 7 x int32 header (GPTHeader, src/model.h:19-30) and the
+// flat fp32 parameters in assign_weights order (src/model.c:177-231).
+constexpr int FILE_MAGIC = 0x434E4750;  // "CNGP"
+constexpr int FILE_VERSION = 1;
+constexpr size_t FILE_HEADER = 7 * sizeof(int);
+
+struct WeightFile {
+    int fd = -1;
+    cngpt_hip_config cfg{};
+    long n_params = 0;
+};
+
+// Open and validate: header present, magic and version, a valid shape and
+// at least n_params floats after the header (the reference's gpt_load
+// checks the magic and the data length, model.c:185-207).
+int open_weight_file(const char* path, WeightFile* wf) {
+    if (!path) return fail("null path");
+    const int fd = open(path, O_RDONLY | O_CLOEXEC);
+    if (fd < 0) return fail("%s: %s", path, strerror(errno));
+    struct stat st;
+    int hdr[7];
+    int rc = 0;
+    if (fstat(fd, &st) != 0) {
+        rc = fail("%s: %s", path, strerror(errno));
+    } else if ((size_t)st.st_size < FILE_HEADER ||
+               pread(fd, hdr, FILE_HEADER, 0) != (ssize_t)FILE_HEADER) {
+        rc = fail("%s: short header", path);
+    } else if (hdr[0] != FILE_MAGIC) {
+        rc = fail("%s: bad magic 0x%X", path, (unsigned)hdr[0]);
+    } else if (hdr[1] != FILE_VERSION) {
+        rc = fail("%s: unsupported version %d (this build reads version %d)", path, hdr[1],
+                  FILE_VERSION);
+    } else {
+        wf->cfg = cngpt_hip_config{hdr[2], hdr[3], hdr[4], hdr[5], hdr[6]};
+        // bounds far above any GPT-2 shape keep the size arithmetic exact
+        const bool in_range = hdr[2] <= 4096 && hdr[3] <= 4096 && hdr[4] <= 65536 &&
+                              hdr[5] <= (1 << 24) && hdr[6] <= (1 << 20);
+        if (!valid_cfg(&wf->cfg) || !in_range) {
+            rc = fail("%s: invalid shape in header (n_layer %d, n_head %d, n_embd %d, vocab %d, "
+                      "block %d)", path, hdr[2], hdr[3], hdr[4], hdr[5], hdr[6]);
+        } else {
+            wf->n_params = params_of(&wf->cfg);
+            const double need = (double)FILE_HEADER + 4.0 * (double)wf->n_params;
+            if ((double)st.st_size < need)
+                rc = fail("%s: short param data (%lld bytes, the header's shape needs %.0f)", path,
+                          (long long)st.st_size, need);
+        }
+    }
+    if (rc) {
+        close(fd);
+        return -1;
+    }
+    wf->fd = fd;
+    return 0;
+}
+
+// Copy the file's parameters into h->d_params without a host copy of the
+// whole buffer: READERS threads each pread chunks of CHUNK bytes into their
+// own pinned staging buffers (NSTAGE per thread, reused once the copy out of
+// them has completed) and enqueue the host-to-device copy of each chunk on
+// the handle's stream, so reading, page-cache copies and DMA overlap.
+constexpr size_t CHUNK = 16u << 20;
+constexpr int NSTAGE = 2;
+constexpr int MAX_READERS = 4;
+
+int stream_to_device(cngpt_hip_ctx* h, const WeightFile& wf, const char* path) {
+    const size_t total = (size_t)wf.n_params * sizeof(float);
+    const size_t nchunks = (total + CHUNK - 1) / CHUNK;
+    const int readers = (int)std::max<size_t>(1, std::min<size_t>(MAX_READERS, nchunks));
+    struct Stage {
+        void* buf = nullptr;
+        hipEvent_t done = nullptr;
+        bool used = false;
+    };
+    std::vector<Stage> st((size_t)readers * NSTAGE);
+    int rc = 0;
+    for (Stage& s : st) {
+        if (hipHostMalloc(&s.buf, CHUNK, hipHostMallocDefault) != hipSuccess ||
+            hipEventCreateWithFlags(&s.done, hipEventDisableTiming) != hipSuccess) {
+            (void)hipGetLastError();
+            rc = fail("pinned staging allocation of %zu bytes failed", CHUNK);
+            break;
+        }
+    }
+    std::atomic<int> err{0};
+    std::atomic<long> bad_chunk{-1};
+    std::atomic<int> bad_errno{0};
+    auto worker = [&](int r) {
+        int k = 0;
+        for (size_t c = r; c < nchunks && !err.load(); c += readers, k++) {
+            Stage& s = st[(size_t)r * NSTAGE + k % NSTAGE];
+            if (s.used && hipEventSynchronize(s.done) != hipSuccess) { err = 2; return; }
+            const size_t off = c * CHUNK, len = std::min(CHUNK, total - off);
+            size_t got = 0;
+            while (got < len) {
+                const ssize_t n = pread(wf.fd, (char*)s.buf + got, len - got,
+                                        (off_t)(FILE_HEADER + off + got));
+                if (n < 0 && errno == EINTR) continue;
+                if (n <= 0) {
+                    bad_chunk = (long)c;
+                    bad_errno = n < 0 ? errno : 0;
+                    err = 1;
+                    return;
+                }
+                got += (size_t)n;
+            }
+            if (hipMemcpyAsync((char*)h->d_params + off, s.buf, len, hipMemcpyHostToDevice,
+                               h->stream) != hipSuccess ||
+                hipEventRecord(s.done, h->stream) != hipSuccess) {
+                err = 2;
+                return;
+            }
+            s.used = true;
+        }
+    };
+    if (!rc) {
+        std::vector<std::thread> pool;
+        for (int r = 1; r < readers; r++) pool.emplace_back(worker, r);
+        worker(0);
+        for (std::thread& t : pool) t.join();
+        const hipError_t se = hipStreamSynchronize(h->stream);
+        if (err.load() == 1)
+            rc = fail("%s: read failed at chunk %ld: %s", path, bad_chunk.load(),
+                      bad_errno.load() ? strerror(bad_errno.load()) : "unexpected end of file");
+        else if (err.load() == 2 || se != hipSuccess)
+            rc = fail("%s: host-to-device copy failed: %s", path,
+                      hipGetErrorString(se != hipSuccess ? se : hipGetLastError()));
+    } else {
+        (void)hipStreamSynchronize(h->stream);
+    }
+    for (Stage& s : st) {
+        if (s.done) (void)hipEventDestroy(s.done);
+        if (s.buf) (void)hipHostFree(s.buf);
+    }
+    return rc;
+}
+
 }  // namespace
 
 // ==================================================================== C ABI
@@ -666,10 +902,7 @@ const char* cngpt_hip_last_error(void) { return g_err; }
 
 long cngpt_hip_num_params(const cngpt_hip_config* c) {
     if (!valid_cfg(c)) return -1;
-    long C = c->n_embd, V = c->vocab_size, T = c->block_size, L = c->n_layer;
-    long per_layer = 2 * C + 3 * C * C + 3 * C + C * C + C + 2 * C + 4 * C * C + 4 * C +
-                     4 * C * C + C;
-    return V * C + T * C + L * per_layer + 2 * C;
+    return params_of(c);
 }
 
 int cngpt_hip_create(int device, cngpt_hip_ctx** out) {
@@ -709,77 +942,43 @@ void cngpt_hip_destroy(cngpt_hip_ctx* h) {
 int cngpt_hip_load_params(cngpt_hip_ctx* h, const cngpt_hip_config* cfg, const float* params,
                           long n_params) {
     if (!h) return fail("null handle");
-    if (!valid_cfg(cfg)) return fail("invalid model shape");
-    if (cfg->n_embd % 4) return fail("n_embd %d must be a multiple of 4", cfg->n_embd);
-    const int hs = cfg->n_embd / cfg->n_head;
-    if (hs != 8 && hs != 16 && hs != 32 && hs != 64 && hs != 128)
-        return fail("head size %d not supported (8, 16, 32, 64, 128)", hs);
-    if (cfg->n_embd > 2048) return fail("n_embd %d above 2048", cfg->n_embd);
+    if (check_shape(cfg)) return -1;
     const long want = cngpt_hip_num_params(cfg);
     if (!params || n_params != want)
         return fail("parameter count %ld does not match the shape (%ld)", n_params, want);
-    HIP_TRY(hipSetDevice(h->device));
-    const bool same_shape = h->have_params && memcmp(&h->cfg, cfg, sizeof(*cfg)) == 0;
-    if (!same_shape) {
-        if (h->d_params) {
-            HIP_TRY(hipStreamSynchronize(h->stream));
-            HIP_TRY(hipFree(h->d_params));
-            h->d_params = nullptr;
-        }
-        if (h->d_act) {
-            drop_graph(h);
-            HIP_TRY(hipFree(h->d_act));
-            h->d_act = nullptr;
-            h->capB = h->capT = h->capAll = h->capKV = 0;
-            h->kvB = h->kvLen = 0;
-        }
-        h->have_params = false;
-        if (hipMalloc(&h->d_params, (size_t)want * sizeof(float)) != hipSuccess) {
-            (void)hipGetLastError();
-            h->d_params = nullptr;
-            return fail("parameter allocation of %ld floats failed", want);
-        }
-    }
+    bool same_shape = false;
+    if (params_prepare(h, cfg, &same_shape)) return -1;
     HIP_TRY(hipMemcpyAsync(h->d_params, params, (size_t)want * sizeof(float),
                            hipMemcpyHostToDevice, h->stream));
     HIP_TRY(hipStreamSynchronize(h->stream));
-    h->cfg = *cfg;
-    h->n_params = want;
-    // Carve like assign_weights (src/model.c:54-83).
-    const long C = cfg->n_embd, V = cfg->vocab_size, T = cfg->block_size;
-    const float* p = h->d_params;
-    h->wte = p; p += V * C;
-    h->wpe = p; p += T * C;
-    h->layers.assign(cfg->n_layer, LayerW{});
-    for (int l = 0; l < cfg->n_layer; l++) {
-        LayerW& w = h->layers[l];
-        w.ln1_w = p; p += C;
-        w.ln1_b = p; p += C;
-        w.attn_w = p; p += 3 * C * C;
-        w.attn_b = p; p += 3 * C;
-        w.proj_w = p; p += C * C;
-        w.proj_b = p; p += C;
-        w.ln2_w = p; p += C;
-        w.ln2_b = p; p += C;
-        w.fc_w = p; p += 4 * C * C;
-        w.fc_b = p; p += 4 * C;
-        w.mlp_w = p; p += C * 4 * C;
-        w.mlp_b = p; p += C;
+    return params_commit(h, cfg, same_shape);
+}
+
+int cngpt_hip_file_config(const char* path, cngpt_hip_config* cfg, long* n_params) {
+    WeightFile wf;
+    if (open_weight_file(path, &wf)) return -1;
+    close(wf.fd);
+    if (cfg) *cfg = wf.cfg;
+    if (n_params) *n_params = wf.n_params;
+    return 0;
+}
+
+int cngpt_hip_load_file(cngpt_hip_ctx* h, const char* path, cngpt_hip_config* cfg_out) {
+    if (!h) return fail("null handle");
+    WeightFile wf;
+    if (open_weight_file(path, &wf)) return -1;
+    bool same_shape = false;
+    int rc = check_shape(&wf.cfg);
+    if (!rc) rc = params_prepare(h, &wf.cfg, &same_shape);
+    if (!rc) rc = stream_to_device(h, wf, path);
+    close(wf.fd);
+    if (rc) {
+        // the device copy is incomplete: the handle holds no parameters
+        h->have_params = false;
+        return -1;
     }
-    h->lnf_w = p; p += C;
-    h->lnf_b = p;
-    const size_t lbytes = (size_t)cfg->n_layer * sizeof(LayerW);
-    if (!same_shape || !h->d_layers) {
-        if (h->d_layers) HIP_TRY(hipFree(h->d_layers));
-        h->d_layers = nullptr;
-        if (hipMalloc(&h->d_layers, lbytes) != hipSuccess) {
-            (void)hipGetLastError();
-            h->d_layers = nullptr;
-            return fail("layer table allocation failed");
-        }
-    }
-    HIP_TRY(hipMemcpy(h->d_layers, h->layers.data(), lbytes, hipMemcpyHostToDevice));
-    h->have_params = true;
+    if (params_commit(h, &wf.cfg, same_shape)) return -1;
+    if (cfg_out) *cfg_out = wf.cfg;
     return 0;
 }
 

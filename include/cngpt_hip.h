@@ -81,6 +81,21 @@ long cngpt_hip_num_params(const cngpt_hip_config *cfg);
 int  cngpt_hip_load_params(cngpt_hip_ctx *h, const cngpt_hip_config *cfg,
                            const float *params, long n_params);
 
+/* Shape and parameter count in the header of a weight file (GPTHeader,
+ * src/model.h:19-30), validated as cngpt_hip_load_file does: magic, version
+ * 1, a valid shape, and at least n_params floats after the 28-byte header
+ * (gpt_load's checks, src/model.c:185-207, plus the version and shape).
+ * Touches no GPU. cfg and n_params may be NULL. */
+int  cngpt_hip_file_config(const char *path, cngpt_hip_config *cfg, long *n_params);
+/* Load a weight file straight into the handle's parameter allocation:
+ * the header is validated as above, then the parameters are read in
+ * chunks into pinned staging buffers by a few reader threads and copied to
+ * the device as they arrive, with no host copy of the whole buffer (gpt_load,
+ * src/model.c:177-211, reads it into the host param_buf, and gpt_init,
+ * model.c:120-135, allocates four such buffers first). cfg_out (may be NULL)
+ * receives the shape. On failure the handle holds no parameters. */
+int  cngpt_hip_load_file(cngpt_hip_ctx *h, const char *path, cngpt_hip_config *cfg_out);
+
 /* Size the activation allocation for B sequences of T tokens (and a decode
  * KV cache of kv_capacity positions per sequence; 0 = none). Replaces
  * fast_resize (src/fast.c:140-168). forward/decode call it as needed. */

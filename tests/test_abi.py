@@ -70,6 +70,47 @@ def test_weight_file_roundtrip_and_errors(tmp_path):
         cngpt_amd.load_weights(str(short))
 
 
+def test_file_config_validates_header_without_gpu(tmp_path):
+    """cngpt_hip_file_config: the header checks cngpt_hip_load_file makes
+    before any device work (GPTHeader, src/model.h:19-30; gpt_load's magic
+    and length checks, src/model.c:185-207)."""
+    cfg = cngpt_amd.Config(2, 4, 64, 97, 32)
+    p = cngpt_amd.init_weights(cfg, 3)
+    f = tmp_path / "m.bin"
+    cngpt_amd.save_weights(str(f), cfg, p)
+    assert cngpt_amd.file_config(str(f)) == (cfg, p.size)
+    raw = f.read_bytes()
+    # trailing bytes are ignored, as gpt_load reads exactly n_params floats
+    (tmp_path / "long.bin").write_bytes(raw + b"\0" * 12)
+    assert cngpt_amd.file_config(str(tmp_path / "long.bin")) == (cfg, p.size)
+
+    def bad(name, data, match):
+        g = tmp_path / name
+        g.write_bytes(data)
+        with pytest.raises(cngpt_amd.CngptError, match=match):
+            cngpt_amd.file_config(str(g))
+
+    hdr = list(struct.unpack("<7i", raw[:28]))
+
+    def with_hdr(**kw):
+        h = hdr.copy()
+        for i, k in enumerate(("magic", "version", "L", "H", "C", "V", "T")):
+            h[i] = kw.get(k, h[i])
+        return struct.pack("<7i", *h) + raw[28:]
+
+    bad("empty.bin", b"", "short header")
+    bad("hdr.bin", raw[:27], "short header")
+    bad("magic.bin", with_hdr(magic=0x12345678), "bad magic 0x12345678")
+    bad("version.bin", with_hdr(version=2), "unsupported version 2")
+    bad("heads.bin", with_hdr(H=5), "invalid shape")          # 64 % 5 != 0
+    bad("zero.bin", with_hdr(L=0), "invalid shape")
+    bad("huge.bin", with_hdr(C=1 << 30, H=1), "invalid shape")
+    bad("short.bin", raw[:-4], "short param data")
+    bad("bigger.bin", with_hdr(L=3), "short param data")      # header promises more
+    with pytest.raises(cngpt_amd.CngptError, match="No such file"):
+        cngpt_amd.file_config(str(tmp_path / "missing.bin"))
+
+
 class _GPTConfig(ctypes.Structure):
     _fields_ = [("n_layer", ctypes.c_int), ("n_head", ctypes.c_int),
                 ("n_embd", ctypes.c_int), ("vocab_size", ctypes.c_int),

@@ -47,6 +47,11 @@ def test_usage_and_errors(tmp_path):
     bad.write_bytes(b"\0" * 64)
     r = run("bench", f"--weights={bad}")
     assert r.returncode == 1 and "bad magic" in r.stderr
+    # sample validates the file header before it touches a device
+    r = run("sample", f"--weights={bad}")
+    assert r.returncode == 1 and "bad magic" in r.stderr
+    r = run("sample", f"--weights={tmp_path / 'missing.bin'}")
+    assert r.returncode == 1 and "No such file" in r.stderr
 
 
 @pytest.mark.skipif(os.path.exists("/dev/kfd"), reason="checks the no-device path")
