@@ -89,6 +89,7 @@ struct cngpt_hip_ctx {
     int attn_splits = 0;
     float* draws = nullptr;      // [capKV+1][B] uniform draws for sampling
     float* prob = nullptr;       // [B][ldp] sampling scratch
+    float* samp_part = nullptr;  // [B][TOPK_PART_WORDS] split-sampling partials
     int* tgt = nullptr;          // [B*T] cross-entropy targets
     float* row_loss = nullptr;   // [B*T] cross-entropy row terms
     float* loss = nullptr;       // mean cross-entropy
@@ -360,6 +361,7 @@ int ensure_arena(cngpt_hip_ctx* h, int B, int T, int all, int kv) {
     sz[n++] = (size_t)nB * H * splits * (C / H + 4) * sizeof(float);  // attn_part
     sz[n++] = (size_t)nB * (nKV + 1) * sizeof(float);              // draws
     sz[n++] = (size_t)nB * ((V + 3) / 4 * 4) * sizeof(float);      // prob
+    sz[n++] = (size_t)nB * TOPK_PART_WORDS * sizeof(float);        // samp_part
     sz[n++] = rows * C * 4;                   // x
     sz[n++] = rows * C * 4;                   // ln
     sz[n++] = qkv_rows * 3 * C * 4;           // qkv / KV cache
@@ -407,6 +409,7 @@ int ensure_arena(cngpt_hip_ctx* h, int B, int T, int all, int kv) {
     h->attn_splits = splits;
     h->draws = (float*)take(sz[n++]);
     h->prob = (float*)take(sz[n++]);
+    h->samp_part = (float*)take(sz[n++]);
     h->ldp = (long)((V + 3) / 4 * 4);
     h->x = (float*)take(sz[n++]);
     h->ln = (float*)take(sz[n++]);
@@ -640,7 +643,7 @@ int run_persist(cngpt_hip_ctx* h, int n) {
 int run_sample(cngpt_hip_ctx* h, const float* draws, float temp, int top_k) {
     Timed t(h, CNGPT_K_SAMPLE, 0.0, 4.0 * h->kvB * h->cfg.vocab_size);
     HIP_TRY(launch_sample(h->logits, h->kvB, h->cfg.vocab_size, temp, top_k, draws, h->prob,
-                          h->ldp, h->next_tok, h->stream));
+                          h->ldp, h->samp_part, h->next_tok, h->stream));
     return 0;
 }
 
@@ -1184,10 +1187,18 @@ int cngpt_hip_generate(cngpt_hip_ctx* h, int n_new, float temperature, int top_k
         HIP_TRY(hipMemcpyAsync(h->draws, draws, (size_t)n_new * B * sizeof(float),
                                hipMemcpyHostToDevice, h->stream));
     if (draws && run_sample(h, h->draws, temperature, top_k)) return -1;
-    const bool persist = !draws && persist_usable(h);
-    if (!draws && !persist && h->decode_path == CNGPT_DECODE_PERSISTENT) return persist_refused(h);
-    if (persist) {
+    const bool persist = persist_usable(h);
+    if (!persist && h->decode_path == CNGPT_DECODE_PERSISTENT) return persist_refused(h);
+    if (persist && !draws) {
+        // greedy: every step in one launch, the argmax fed back on the device
         if (n_new > 1 && run_persist(h, n_new - 1)) return -1;
+    } else if (persist) {
+        // sampled: one persistent step per launch, then the sampler replaces
+        // the step's argmax by the sampled token the next launch embeds
+        for (int i = 1; i < n_new; i++) {
+            if (run_persist(h, 1)) return -1;
+            if (run_sample(h, h->draws + (size_t)i * B, temperature, top_k)) return -1;
+        }
     } else {
         for (int i = 1; i < n_new; i++) {
             if (run_decode_step(h)) return -1;
@@ -1229,7 +1240,7 @@ int cngpt_hip_sample(cngpt_hip_ctx* h, float temperature, int top_k, const float
     HIP_TRY(hipMemcpyAsync(h->draws, draws, (size_t)h->curB * sizeof(float),
                            hipMemcpyHostToDevice, h->stream));
     HIP_TRY(launch_sample(h->logits, h->curB, h->cfg.vocab_size, temperature, top_k, h->draws,
-                          h->prob, h->ldp, h->next_tok, h->stream));
+                          h->prob, h->ldp, h->samp_part, h->next_tok, h->stream));
     HIP_TRY(hipMemcpyAsync(out_tokens, h->next_tok, (size_t)h->curB * sizeof(int),
                            hipMemcpyDeviceToHost, h->stream));
     HIP_TRY(hipStreamSynchronize(h->stream));

@@ -1,7 +1,7 @@
 // decode.hip - kernels of the single-token decode step and the last-position
 // pass: products over a few rows with the LayerNorm (or the merge of the
 // split attention) folded into the input staging, split-key attention for
-// one query row, the argmax of the lm_head, and top-k sampling.
+// one query row and the argmax of the lm_head (sampling: sample.hip).
 //
 // A decode step of GPT-2 small reads ~0.5 GB of weights once; every kernel
 // here is HBM- or latency-bound. The layout rules: each output column's
@@ -431,273 +431,6 @@ __global__ void __launch_bounds__(1024) k_argmax_rows(const float* __restrict__ 
     }
 }
 
-// ---------------------------------------------------------------- sampling
-
-constexpr int ST = 1024;      // threads of the sampling workgroup
-constexpr int SLIST = 2048;   // survivors of the top-k cut kept in index order
-
-// Block-wide reductions over ST threads (fixed order: deterministic).
-__device__ float block_max(float v, float* sh) {
-    v = wave_max(v);
-    const int w = threadIdx.x >> 6;
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) sh[w] = v;
-    __syncthreads();
-    float r = sh[0];
-    for (int i = 1; i < ST / 64; i++) r = fmaxf(r, sh[i]);
-    return r;
-}
-__device__ float block_sum(float v, float* sh) {
-    v = wave_sum(v);
-    const int w = threadIdx.x >> 6;
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) sh[w] = v;
-    __syncthreads();
-    float r = 0.f;
-    for (int i = 0; i < ST / 64; i++) r += sh[i];
-    return r;
-}
-// Exclusive prefix over the threads in thread order; *total = the sum.
-template <typename TV>
-__device__ TV block_excl_scan(TV v, TV* sh, TV* total) {
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    TV x = v;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const TV y = __shfl_up(x, o, 64);
-        if (lane >= o) x += y;
-    }
-    __syncthreads();
-    if (lane == 63) sh[w] = x;
-    __syncthreads();
-    TV before = 0, all = 0;
-    for (int i = 0; i < ST / 64; i++) {
-        if (i < w) before += sh[i];
-        all += sh[i];
-    }
-    *total = all;
-    return before + (x - v);
-}
-// hist[bin] += 1 for every lane with ok set; lanes of a wavefront that share
-// a bin are counted with one LDS atomic (the high bits of nearby
-// probabilities mostly coincide).
-__device__ __forceinline__ void hist_add(int* hist, unsigned bin, bool ok) {
-    unsigned long long act = __ballot(ok);
-    while (act) {
-        const int leader = __ffsll((long long)act) - 1;
-        const unsigned lb = __shfl(bin, leader, 64);
-        const unsigned long long peers = __ballot(ok && bin == lb) & act;
-        if ((int)(threadIdx.x & 63) == leader) atomicAdd(&hist[lb], __popcll(peers));
-        act &= ~peers;
-    }
-}
-
-// One token per row from logits [rows, V], with the arithmetic of the
-// reference's sample_top_k (src/model.c:927-989): scaled = logit / temp
-// (temp <= 0 -> 1), softmax, keep the values >= the top_k-th largest
-// (ties kept), renormalise, then the first index whose running sum exceeds
-// the uniform draw r[row]; V - 1 if none does. prob [rows, ldp] is scratch
-// (ldp a multiple of 4). Thread i owns the float4 groups [i*ch4, (i+1)*ch4),
-// so thread order is index order. When at most SLIST values survive the
-// cut, the renormalising sum and the running sum are taken sequentially in
-// index order, as the reference does; otherwise (top_k off, or a huge tie
-// at the threshold) each thread sums its range and the ranges are prefixed,
-// which can differ from a sequential sum in the last bits, so the token can
-// differ only when r lies within rounding of a boundary.
-__global__ void __launch_bounds__(ST) k_sample(const float* __restrict__ logits, int V, float temp,
-                                               int top_k, const float* __restrict__ r_draw,
-                                               float* __restrict__ prob, long ldp,
-                                               int* __restrict__ out) {
-    __shared__ float shf[ST / 64];
-    __shared__ int shi[ST / 64];
-    __shared__ int hist[256];
-    __shared__ int chosen, kk_left;
-    __shared__ float lv[SLIST];
-    __shared__ int li[SLIST];
-    __shared__ int tok_sh;
-
-    const int row = blockIdx.x, tid = threadIdx.x;
-    const float* lg = logits + (long)row * V;
-    float* p = prob + (long)row * ldp;
-    f32x4* p4 = (f32x4*)p;
-    const int V4 = (V + 3) / 4;
-    const int ch4 = (V4 + ST - 1) / ST;
-    const int g0 = min(tid * ch4, V4), g1 = min(g0 + ch4, V4);
-    const float tdiv = temp > 0.0f ? temp : 1.0f;
-    const int NP = V4 * 4;  // padded length of the scratch row
-    constexpr int U = 8;    // loads in flight per thread in the strided passes
-
-    // scaled values (coalesced reads of the logits) and their max
-    float mx = -INFINITY;
-    for (int i0 = 0; i0 < NP; i0 += ST * U) {
-        float v[U];
-#pragma unroll
-        for (int u = 0; u < U; u++) {
-            const int i = i0 + u * ST + tid;
-            const float x = lg[min(i, V - 1)] / tdiv;
-            v[u] = i < V ? x : -INFINITY;
-        }
-#pragma unroll
-        for (int u = 0; u < U; u++) {
-            const int i = i0 + u * ST + tid;
-            if (i < NP) p[i] = v[u];
-            mx = fmaxf(mx, v[u]);
-        }
-    }
-    mx = block_max(mx, shf);
-    float s = 0.f;
-    for (int i0 = 0; i0 < NP; i0 += ST * U) {
-        float v[U];
-#pragma unroll
-        for (int u = 0; u < U; u++) {
-            const int i = i0 + u * ST + tid;
-            const float x = p[min(i, NP - 1)];
-            v[u] = i < V ? expf(x - mx) : 0.f;
-        }
-#pragma unroll
-        for (int u = 0; u < U; u++) {
-            const int i = i0 + u * ST + tid;
-            if (i < NP) p[i] = v[u];
-            s += v[u];
-        }
-    }
-    const float sum = block_sum(s, shf);
-    for (int i0 = 0; i0 < NP; i0 += ST * U) {
-        float v[U];
-#pragma unroll
-        for (int u = 0; u < U; u++) v[u] = p[min(i0 + u * ST + tid, NP - 1)];
-#pragma unroll
-        for (int u = 0; u < U; u++) {
-            const int i = i0 + u * ST + tid;
-            if (i < NP) p[i] = i < V ? v[u] / sum : 0.f;
-        }
-    }
-    __syncthreads();
-
-    // k-th largest probability (with multiplicity) by MSB-first radix
-    // select on the bit patterns (non-negative floats order as integers).
-    const bool cut = top_k > 0 && top_k < V;
-    float thr = 0.f;
-    if (cut) {
-        unsigned prefix = 0, mask = 0;
-        if (tid == 0) kk_left = top_k;
-        for (int shift = 24; shift >= 0; shift -= 8) {
-            for (int i = tid; i < 256; i += ST) hist[i] = 0;
-            __syncthreads();
-            for (int i0 = 0; i0 < NP; i0 += ST * U) {
-                unsigned uv[U];
-#pragma unroll
-                for (int u = 0; u < U; u++) uv[u] = __float_as_uint(p[min(i0 + u * ST + tid, NP - 1)]);
-#pragma unroll
-                for (int u = 0; u < U; u++) {
-                    const int i = i0 + u * ST + tid;
-                    hist_add(hist, (uv[u] >> shift) & 255u, i < V && (uv[u] & mask) == prefix);
-                }
-            }
-            __syncthreads();
-            if (tid == 0) {
-                int cum = 0, kk = kk_left, d = 255;
-                for (; d > 0; d--) {
-                    if (cum + hist[d] >= kk) break;
-                    cum += hist[d];
-                }
-                chosen = d;
-                kk_left = kk - cum;
-            }
-            __syncthreads();
-            prefix |= (unsigned)chosen << shift;
-            mask |= 255u << shift;
-        }
-        thr = __uint_as_float(prefix);
-    }
-
-    // Survivors (all values when there is no cut) in index order. Thread
-    // ranges: float4 groups g0 + j, j < ch4 (a uniform trip count).
-    auto keep = [&](int i, float v) { return i < V && (!cut || v >= thr); };
-    int cnt = 0;
-#pragma unroll 4
-    for (int j = 0; j < ch4; j++) {
-        const int g = g0 + j;
-        const f32x4 v = ld4_or0(p4 + min(g, V4 - 1), g < g1);
-        if (g < g1)
-            cnt += keep(4 * g, v.x) + keep(4 * g + 1, v.y) + keep(4 * g + 2, v.z) +
-                   keep(4 * g + 3, v.w);
-    }
-    int total;
-    const int base = block_excl_scan<int>(cnt, shi, &total);
-    const float r = r_draw[row];
-    if (cut && total <= SLIST) {
-        int k = base;
-        for (int j = 0; j < ch4; j++) {
-            const int g = g0 + j;
-            const f32x4 v = ld4_or0(p4 + min(g, V4 - 1), g < g1);
-            const float vv[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-            for (int e = 0; e < 4; e++)
-                if (g < g1 && keep(4 * g + e, vv[e])) {
-                    lv[k] = vv[e];
-                    li[k] = 4 * g + e;
-                    k++;
-                }
-        }
-        __syncthreads();
-        if (tid == 0) {
-            float ns = 0.f;
-            for (int q = 0; q < total; q++) ns += lv[q];
-            int tok = V - 1;
-            float cdf = 0.f;
-            for (int q = 0; q < total; q++) {
-                cdf += ns > 0.0f ? lv[q] / ns : lv[q];
-                if (r < cdf) { tok = li[q]; break; }
-            }
-            out[row] = tok;
-        }
-        return;
-    }
-    // Blocked form: zero the cut values, renormalise, prefix by ranges
-    // (scratch padding past V holds 0).
-    float ps = 0.f;
-    for (int j = 0; j < ch4; j++) {
-        const int g = g0 + j;
-        f32x4 v = ld4_or0(p4 + min(g, V4 - 1), g < g1);
-        if (cut) {
-            v.x = v.x < thr ? 0.f : v.x;
-            v.y = v.y < thr ? 0.f : v.y;
-            v.z = v.z < thr ? 0.f : v.z;
-            v.w = v.w < thr ? 0.f : v.w;
-            if (g < g1) p4[g] = v;
-        }
-        ps += ((v.x + v.y) + v.z) + v.w;
-    }
-    if (cut) {
-        const float ns = block_sum(ps, shf);
-        if (ns > 0.0f) {
-            ps = 0.f;
-            for (int j = 0; j < ch4; j++) {
-                const int g = g0 + j;
-                f32x4 v = ld4_or0(p4 + min(g, V4 - 1), g < g1);
-                v.x /= ns; v.y /= ns; v.z /= ns; v.w /= ns;
-                if (g < g1) p4[g] = v;
-                ps += ((v.x + v.y) + v.z) + v.w;
-            }
-        }
-    }
-    float all;
-    float cdf = block_excl_scan<float>(ps, shf, &all);
-    if (tid == 0) tok_sh = V - 1;
-    __syncthreads();
-    // Every thread scans its own range from its prefix; the smallest index
-    // whose running sum exceeds r wins (robust to rounding gaps between
-    // neighbouring ranges). Zero-probability values are never chosen.
-    for (int i = g0 * 4; i < g1 * 4 && i < V; i++) {
-        const float v = p[i];
-        cdf += v;
-        if (v > 0.0f && r < cdf) { atomicMin(&tok_sh, i); break; }
-    }
-    __syncthreads();
-    if (tid == 0) out[row] = tok_sh;
-}
-
 // ---------------------------------------------------------------- launchers
 
 template <int EPI, int MR, int SRC, int WPC, bool ARGMAX>
@@ -818,10 +551,3 @@ hipError_t launch_argmax_rows(const float* logits, int rows, int V, int* out, in
     return hipGetLastError();
 }
 
-hipError_t launch_sample(const float* logits, int rows, int V, float temp, int top_k,
-                         const float* r_draw, float* prob, long ldp, int* out, hipStream_t s) {
-    if (rows <= 0) return hipSuccess;
-    if ((ldp & 3) || ldp < V) return hipErrorInvalidValue;
-    k_sample<<<rows, ST, 0, s>>>(logits, V, temp, top_k, r_draw, prob, ldp, out);
-    return hipGetLastError();
-}

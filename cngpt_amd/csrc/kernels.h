@@ -123,8 +123,15 @@ hipError_t launch_argmax_rows(const float* logits, int rows, int V, int* out, in
 // One token per row with the reference's sample_top_k arithmetic, the
 // uniform draw of row r in r_draw[r]; prob [rows, ldp] is scratch
 // (ldp >= V, a multiple of 4).
+// sample.hip
+// Top-k sampling of one token per row (sample_top_k's arithmetic). prob
+// [rows, ldp] is scratch for the one-workgroup-per-row path; part (may be
+// NULL: that path only) holds TOPK_PART_WORDS floats per row for the split
+// path (top_k <= 64, V <= 65536).
+constexpr long TOPK_PART_WORDS = 4 * 64 + 2 * 64 * 64;
 hipError_t launch_sample(const float* logits, int rows, int V, float temp, int top_k,
-                         const float* r_draw, float* prob, long ldp, int* out, hipStream_t s);
+                         const float* r_draw, float* prob, long ldp, float* part, int* out,
+                         hipStream_t s);
 
 // persist.hip
 // Parameter pointers of one layer (the carve order of assign_weights).

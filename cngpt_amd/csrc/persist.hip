@@ -94,7 +94,8 @@ __device__ __forceinline__ unsigned wtag(u64 w) { return (unsigned)(w >> 32); }
 // out[k] = value of base[idx[k]] once it carries `tag` (for k with need[k];
 // idx[k] is always a valid index). All first reads are in flight together;
 // only stragglers are read again. False after SPIN_LIMIT rounds or when
-// another workgroup has raised the abort word.
+// another workgroup of this launch has raised the abort word (to amark; a
+// smaller value is an earlier launch's, as tags only grow).
 // Only slots k with bit k of en (uniform over the wavefront) are read at
 // all, and slots with bit k of t2 wait for tag2 instead of tag. One call
 // waits for all its words, so a phase gathers every input in one call (one
@@ -102,7 +103,8 @@ __device__ __forceinline__ unsigned wtag(u64 w) { return (unsigned)(w >> 32); }
 template <int N>
 __device__ __forceinline__ bool fetch(const u64* base, const int (&idx)[N], const bool (&need)[N],
                                       unsigned tag, float (&out)[N], const u64* abortw,
-                                      unsigned en = ~0u, unsigned t2 = 0u, unsigned tag2 = 0u) {
+                                      u64 amark, unsigned en = ~0u, unsigned t2 = 0u,
+                                      unsigned tag2 = 0u) {
     u64 v[N];
 #pragma unroll
     for (int k = 0; k < N; k++) v[k] = ((en >> k) & 1u) ? peek(base + idx[k]) : 0ull;
@@ -128,7 +130,7 @@ __device__ __forceinline__ bool fetch(const u64* base, const int (&idx)[N], cons
                 out[k] = wval(v[k]);
                 pend &= ~(1ull << k);
             }
-        if (pend && (++it & 31) == 0 && (it > SPIN_LIMIT || peek(abortw) != 0)) return false;
+        if (pend && (++it & 31) == 0 && (it > SPIN_LIMIT || peek(abortw) >= amark)) return false;
     }
     return true;
 }
@@ -318,6 +320,7 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
     const u64* const rp = tp + rep * tl.ps;
     const u64* const ram = tam + rep * tl.as;
     u64* const abortw = a.tagged + tl.abortw;
+    const u64 amark = (u64)a.tag0 + 1;  // the abort word's value for this launch
     const unsigned per_step = PHASES * L + 1;
 
     if (tid == 0) sm.abort = 0;
@@ -328,7 +331,7 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
     auto settle = [&](bool ok) -> bool {
         if (!ok) {
             sm.abort = 1;
-            __hip_atomic_store(abortw, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(abortw, amark, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if (a.err) atomicOr(a.err, 2);
         }
         __syncthreads();
@@ -372,7 +375,7 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
             idx[i] = min(tt + PT * i, C - 1);
             need[i] = tt + PT * i < C;
         }
-        return fetch<LNE>(rx, idx, need, tag, xv, abortw, slots_below(C, tt));
+        return fetch<LNE>(rx, idx, need, tag, xv, abortw, amark, slots_below(C, tt));
     };
     // Bias of this lane's output column in the next phase (control lanes;
     // the others load b[0]). Issued before the current epilogue's stores.
@@ -491,7 +494,7 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
                         idx[m] = m * C + ih * 64 + lane;
                         need[m] = true;
                     }
-                    ok = fetch<3>(tq, idx, need, TA, nv, abortw);
+                    ok = fetch<3>(tq, idx, need, TA, nv, abortw, amark);
 #pragma unroll
                     for (int m = 0; m < 3; m++) sm.qkv_new[m][lane] = nv[m];
                 }
@@ -587,7 +590,7 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
                         if ((tt & ~63) < H * ns) en |= 3u << 8;
                         if (ctrl && l > 0) en |= 1u << 10;
                     }
-                    const bool ok2 = fetch<11>(rp, idx, need, TB, o, abortw, en, 1u << 10, TXIN);
+                    const bool ok2 = fetch<11>(rp, idx, need, TB, o, abortw, amark, en, 1u << 10, TXIN);
                     ok = ok && ok2;
 #pragma unroll
                     for (int k = 0; k < 8; k++)
@@ -677,7 +680,7 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
                     need[NH] = c >= 0;
                     const unsigned en = (slots_below(C4, tt) & ((1u << NH) - 1u)) |
                                         (ctrl ? 1u << NH : 0u);
-                    ok = fetch<NH + 1>(rh, idx, need, TD, hv, abortw, en, 1u << NH, TC);
+                    ok = fetch<NH + 1>(rh, idx, need, TD, hv, abortw, amark, en, 1u << NH, TC);
 #pragma unroll
                     for (int k = 0; k < NH; k++)
                         if (need[k]) actf[tt + PT * k] = hv[k];
@@ -781,7 +784,7 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
             int idx[2] = {2 * g, 2 * g + 1};
             bool need[2] = {tt < G, tt < G};
             float pv[2];
-            const bool ok = fetch<2>(ram, idx, need, TF, pv, abortw);
+            const bool ok = fetch<2>(ram, idx, need, TF, pv, abortw, amark);
             if (!settle(ok)) return;
             float b = tt < G ? pv[0] : -INFINITY;
             int bi = tt < G ? __float_as_int(pv[1]) : 0x7fffffff;
@@ -854,10 +857,8 @@ bool persist_supported(int C, int H, int V, int cap, int G) {
 }
 
 hipError_t launch_decode_persist(const PersistArgs& a, int G, hipStream_t s) {
-    // clear the abort word (left set by a launch that gave up)
-    const TagLayout tl(a.C, a.H);
-    hipError_t e = hipMemsetAsync(a.tagged + tl.abortw, 0, sizeof(u64), s);
-    if (e != hipSuccess) return e;
+    // No clearing before a launch: an abort word left by an earlier launch
+    // holds a smaller value than this launch's mark.
     switch ((a.C + 255) / 256) {
         case 1: return launch_u<1>(a, G, s);
         case 2: return launch_u<2>(a, G, s);

@@ -54,10 +54,12 @@ enum {
 };
 
 /* How decode steps run. KERNELS: one replayed graph of per-stage kernels
- * per step (any batch). PERSISTENT: the greedy steps of one sequence as one
- * cooperative launch whose workgroups meet at grid barriers between stages
- * (B = 1, head size 64, n_embd <= 768). AUTO: PERSISTENT where it
- * applies (greedy decode_step / generate), else KERNELS. */
+ * per step (any batch). PERSISTENT: the steps of one sequence as a
+ * cooperative launch whose workgroups exchange each stage's outputs
+ * through tagged words (B = 1, head size 64, n_embd <= 768): all greedy
+ * steps of a generate call in one launch, sampled steps one launch each
+ * followed by the sampler. AUTO: PERSISTENT where it applies, else
+ * KERNELS. */
 enum { CNGPT_DECODE_AUTO = 0, CNGPT_DECODE_KERNELS = 1, CNGPT_DECODE_PERSISTENT = 2 };
 
 /* Last error message of the calling thread ("" if none). */

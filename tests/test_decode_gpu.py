@@ -184,6 +184,104 @@ def test_device_sampling_matches_oracle():
             assert g == ref or cdf_gap(row2, 1.0, 40, float(r)) < 1e-5, (r, g, ref)
 
 
+def survivors(logits, temp, top_k):
+    """Number of values sample_top_k keeps (float64)."""
+    x = logits.astype(np.float64) / (temp if temp > 0 else 1.0)
+    if not 0 < top_k < x.size:
+        return x.size
+    return int((x >= np.sort(x)[-top_k]).sum())
+
+
+def consistent(logits, temp, top_k, r, tok, tol):
+    """tok is the token sample_top_k returns for draw r when its CDF is
+    exact (float64) up to tol: r falls in tok's CDF step widened by tol."""
+    x = logits.astype(np.float64) / (temp if temp > 0 else 1.0)
+    p = np.exp(x - x.max())
+    p /= p.sum()
+    if 0 < top_k < p.size:
+        p = np.where(p < np.sort(p)[-top_k], 0.0, p)
+        p /= p.sum()
+    c = np.cumsum(p)
+    if tok == p.size - 1 and p[tok] == 0:
+        return r >= c[-1] - tol  # the fallback when the running sum stays <= r
+    return p[tok] > 0 and c[tok] - p[tok] - tol <= r < c[tok] + tol
+
+
+def designed_logits_model(V=50257):
+    """A model whose last-position logits are wte[:, 0] exactly, whatever
+    the tokens: the final LayerNorm has gain 0 and bias e_0, so its output
+    is e_0 and the lm_head row of token v is 1 * wte[v, 0] + 0 * ...."""
+    cfg = cngpt_amd.Config(1, 4, 256, V, 64)
+    params = cngpt_amd.init_weights(cfg, 5)
+    w = oracle.unpack(ocfg(cfg), params)
+    w["ln_f_w"][:] = 0.0
+    w["ln_f_b"][:] = 0.0
+    w["ln_f_b"][0] = 1.0
+    return cfg, params, w
+
+
+def test_split_sampling_designed_rows():
+    """The split top-k path (top_k <= 64: chunk lists, then one pick per
+    row) on logits rows built exactly (designed_logits_model): top values
+    all in the first chunk (its list full, so the chunk is rescanned), exact
+    ties at the cut inside one chunk and across chunks, a tie wider than
+    the survivor list (blocked form), negative logits, top_k 1 / 40 / 64 and
+    65 (the one-workgroup path), 8 rows at once."""
+    V = 50257
+    cfg, params, w = designed_logits_model(V)
+    rng = np.random.default_rng(12)
+    rows = {}
+    base = (rng.standard_normal(V) * 3).astype(np.float32)
+    rows["random"] = base
+    r = base.copy()
+    r[:100] = 20 + np.sort(rng.standard_normal(100)).astype(np.float32)  # all top-64 in chunk 0
+    rows["first_chunk"] = r
+    r = base.copy()
+    r[:30] = 30 + rng.random(30).astype(np.float32)
+    r[100:220] = np.float32(25.0)                 # 120 tied at the cut, one chunk
+    rows["tie_one_chunk"] = r
+    r = base.copy()
+    r[rng.choice(V, 30, replace=False)] = 30 + rng.random(30).astype(np.float32)
+    spread = np.arange(50) * 1000 + 7             # 50 tied at the cut, many chunks
+    r[spread] = np.float32(25.0)
+    rows["tie_spread"] = r
+    r = base.copy()
+    r[5000:8000] = np.float32(12.5)               # 3000 tied at the top: > 2048 survive
+    rows["wide_tie"] = r
+    rows["negative"] = (base - 200).astype(np.float32)
+    prompt = np.tile(oracle.lcg_tokens(8, V, seed=3), (8, 1))
+    checked = skipped = 0
+    with cngpt_amd.Model(cfg, params) as m:
+        for name, row in rows.items():
+            near = 0
+            w["wte"][:, 0] = row
+            m.load_params(params)
+            got_row = m.decode_begin(prompt, capacity=16)
+            assert np.array_equal(got_row, np.tile(row, (8, 1))), name
+            say(f"split sampling: {name}")
+            for temp, k in ((1.0, 40), (0.8, 1), (1.3, 64), (1.0, 65), (0.0, 40)):
+                draws = rng.random(16).astype(np.float32)
+                draws[:2] = [0.0, np.float32(0.99999994)]
+                for i in range(0, 16, 8):
+                    got = m.sample(8, temp, k, draws[i:i + 8])
+                    for rr, g in zip(draws[i:i + 8], got):
+                        ref = oracle.sample_top_k(row, temp, k, float(rr))
+                        checked += 1
+                        if g != ref:
+                            # both running sums are fp32: each is within n * 2^-24 of the
+                            # exact CDF after n survivors (3000 tie in "wide_tie"), so
+                            # the device token must be the exact CDF's token up to that
+                            tol = 1e-5 + 2 * survivors(row, temp, k) * 2.0**-24
+                            assert consistent(row, temp, k, float(rr), g, tol), (
+                                name, temp, k, rr, g, ref)
+                            near += rr < 0.9999  # draws next to 1 sit at the last step
+            say(f"  {near} draws at a boundary")
+            skipped += near
+            # a 3000-way tie spaces the CDF steps 3.3e-4 apart: any draw is near one
+            assert name == "wide_tie" or near <= 2, name
+    say(f"split sampling: {checked} draws, {skipped} at a boundary")
+
+
 def test_generate_sampling_gpt2_small_rand_stream():
     """The sampling loop of gpt_sample (src/model.c:991-1016) with the KV
     cache: draws from the reference's rand() stream after srand(7), temp 0.8,

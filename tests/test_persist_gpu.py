@@ -1,5 +1,5 @@
-"""Single-sequence greedy decode as one persistent launch (the stages of a
-step as phases separated by grid barriers) vs the oracle and vs the
+"""Single-sequence decode as persistent launches (the stages of a step as
+phases whose outputs travel as tagged words) vs the oracle and vs the
 kernel-per-stage decode.
 
 Reference values as in test_decode_gpu.py: without window truncation the
@@ -82,6 +82,42 @@ def test_persistent_generate_matches_steps_kernels_and_oracle():
     assert first == n or tie[0, first], ("persistent vs kernels diverge without a tie", first)
     assert np.array_equal(np.where(tie, 0, ref.argmax(-1)), np.where(tie, 0, gen))
     compare(np.stack(steps, 1), ref[:, 1:], what="c768 per-step logits")
+
+
+def test_persistent_sampled_generate():
+    """Sampled generate on the persistent path (one launch per step, then
+    the sampler): temp 0.8, top-k 40; every token is sample_top_k of the
+    oracle's logits of the sequence generated so far (until a draw falls
+    within the logits' error of a CDF boundary, after which the streams
+    may part), and the same draws on the kernel path give the same tokens
+    up to that point."""
+    from test_decode_gpu import cdf_gap
+    cfg = CASES["c768_v50257"]
+    params, m = model(cfg, 13)
+    prompt = np.random.default_rng(6).integers(0, cfg.vocab_size, size=(1, 40), dtype=np.int32)
+    n = 60
+    draws = np.random.default_rng(8).random(n).astype(np.float32)
+    with m:
+        say("c768: sampled generate, persistent")
+        m.decode_begin(prompt, capacity=40 + n - 1)
+        gen = m.generate(n, 0.8, 40, draws)[0]
+        assert m.decode_path() == cngpt_amd.DECODE_PERSISTENT
+        say("c768: sampled generate, kernel path")
+        m.set_decode_path(cngpt_amd.DECODE_KERNELS)
+        m.decode_begin(prompt, capacity=40 + n - 1)
+        kern = m.generate(n, 0.8, 40, draws)[0]
+        assert m.decode_path() == cngpt_amd.DECODE_KERNELS
+    seq = np.concatenate([prompt[0], gen[:-1]]).reshape(1, -1)
+    ref = oracle.forward(ocfg(cfg), params, seq, oracle.ALL)[0, 39:]
+    for i in range(n):
+        want = oracle.sample_top_k(ref[i], 0.8, 40, float(draws[i]))
+        if want != gen[i]:
+            assert cdf_gap(ref[i], 0.8, 40, float(draws[i])) < 1e-3, (i, gen[i], want)
+            say(f"  diverged at a CDF boundary at token {i}")
+            break
+        assert kern[i] == gen[i] or cdf_gap(ref[i], 0.8, 40, float(draws[i])) < 1e-3, i
+        if kern[i] != gen[i]:
+            break
 
 
 def test_persistent_gpt2_small_long_context():
