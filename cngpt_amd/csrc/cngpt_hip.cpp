@@ -55,6 +55,8 @@ struct ProfRec {
 };
 
 constexpr size_t ALIGN = 256;
+// split-K partials of the products over <= 64 rows (16 MB)
+constexpr long GEMM_PART_FLOATS = 1l << 22;
 size_t align_up(size_t n) { return (n + ALIGN - 1) & ~(ALIGN - 1); }
 
 }  // namespace
@@ -90,6 +92,7 @@ struct cngpt_hip_ctx {
     float* draws = nullptr;      // [capKV+1][B] uniform draws for sampling
     float* prob = nullptr;       // [B][ldp] sampling scratch
     float* samp_part = nullptr;  // [B][TOPK_PART_WORDS] split-sampling partials
+    float* gemm_part = nullptr;  // split-K partials of the few-row products
     int* tgt = nullptr;          // [B*T] cross-entropy targets
     float* row_loss = nullptr;   // [B*T] cross-entropy row terms
     float* loss = nullptr;       // mean cross-entropy
@@ -199,6 +202,7 @@ int run_gemm(cngpt_hip_ctx* h, const float* X, const float* W, const float* bias
     a.seg = seg; a.seg_stride = seg_stride;
     a.row_off = row_off; a.row_off_dev = row_off_dev;
     a.epi = epi;
+    a.part = h->gemm_part; a.part_cap = GEMM_PART_FLOATS;
     Timed t(h, CNGPT_K_GEMM, flops, bytes);
     HIP_TRY(launch_gemm(a, h->stream));
     return 0;
@@ -362,6 +366,7 @@ int ensure_arena(cngpt_hip_ctx* h, int B, int T, int all, int kv) {
     sz[n++] = (size_t)nB * (nKV + 1) * sizeof(float);              // draws
     sz[n++] = (size_t)nB * ((V + 3) / 4 * 4) * sizeof(float);      // prob
     sz[n++] = (size_t)nB * TOPK_PART_WORDS * sizeof(float);        // samp_part
+    sz[n++] = (size_t)GEMM_PART_FLOATS * sizeof(float);            // gemm_part
     sz[n++] = rows * C * 4;                   // x
     sz[n++] = rows * C * 4;                   // ln
     sz[n++] = qkv_rows * 3 * C * 4;           // qkv / KV cache
@@ -410,6 +415,7 @@ int ensure_arena(cngpt_hip_ctx* h, int B, int T, int all, int kv) {
     h->draws = (float*)take(sz[n++]);
     h->prob = (float*)take(sz[n++]);
     h->samp_part = (float*)take(sz[n++]);
+    h->gemm_part = (float*)take(sz[n++]);
     h->ldp = (long)((V + 3) / 4 * 4);
     h->x = (float*)take(sz[n++]);
     h->ln = (float*)take(sz[n++]);

@@ -20,9 +20,11 @@
 // wavefront). Ragged M and N edges (e.g. the 50257-wide vocabulary) clamp
 // loads to the last valid row and mask stores.
 //
-// k_skinny: 8 < M <= 64 rows, 16-column tiles, K split over 16 wavefronts.
-// Products over M <= 8 rows (decode, the last-position pass) are k_dgemv in
-// decode.hip.
+// k_stream: M <= 64 rows, weights streamed once, input rows through LDS,
+// K split over workgroups when the column tiles are few. Products over
+// M <= 2 rows (single-sequence decode) are k_dgemv in decode.hip.
+#include <algorithm>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -162,114 +164,171 @@ __global__ void __launch_bounds__(NTHREADS, OCC) k_gemm(GemmArgs a, int tiles_m,
 
 // ---------------------------------------------------------------- skinny
 
-// k_skinny: 8 < M <= 64 rows (batched decode, last-position passes of
-// larger batches, short prefills). Weight-bandwidth bound, and near the
-// fp32 ridge at M = 32 (2 * 32 FLOP per 4-byte weight = 16 FLOP/B against
-// 157.3 / 8 = 19.7). Each workgroup owns 16 output columns and streams those
-// 16 weight rows once; its SK_NW wavefronts split K, and each double-buffers
-// D k-steps of 16 (one 16-byte weight load and MB 16-byte input loads per
-// lane per step): the loads of the next D steps are in flight while the
-// current ones are multiplied with v_mfma_f32_16x16x4f32 (16 rows x 16
-// columns x 4 k). Inside a step lane l feeds column / row l%16 and
-// k = 4*(l/16)..+3, one k per instruction. The wavefronts' partial tiles are
-// summed in LDS in a fixed order, then the epilogue of k_gemm applies.
-constexpr int SK_NW = 16;
+// k_stream: M <= 64 rows (batched decode, last-position passes of larger
+// batches, short prefills). Weight-bandwidth bound: every weight is used by
+// M rows only (at M = 32, 2 * 32 FLOP per 4-byte weight = 16 FLOP/B, near
+// the fp32 ridge of 157.3 / 8 = 19.7), so each weight is read once and the
+// input rows are shared out of LDS. A workgroup of ST_NW wavefronts owns
+// ST_NT = 16 * ST_NW output columns over a K range [kb, ke): each wavefront
+// streams its 16 weight rows with ST_PF 16-byte loads in flight per lane
+// (k-steps of 16: lane l holds column l%16, k = 4*(l/16)..+3), while the
+// input rows of the range pass through LDS in chunks of ST_KC k, the next
+// chunk loaded into registers during the current one. Products are
+// v_mfma_f32_16x16x4f32 (16 rows x 16 columns x 4 k), MB row blocks of 16.
+// When the column tiles alone would leave CUs idle, K is split over KS
+// workgroups that write partial tiles; k_stream_reduce then sums them in
+// order and applies the epilogue (no atomics: the result is reproducible).
+constexpr int ST_NW = 4;
+constexpr int ST_NT = 16 * ST_NW;
+constexpr int ST_KC = 128;
+constexpr int ST_PF = ST_KC / 16;   // weight steps in flight = steps per chunk
+constexpr int ST_XP = ST_KC + 4;    // padded LDS row (floats)
+
+template <int EPI>
+__device__ __forceinline__ void store_out(const GemmArgs& a, long roff, int row, int col, float v) {
+    long orow = a.seg ? (long)(row / a.seg) * a.seg_stride + row % a.seg : row;
+    orow += roff;
+    float* y = a.Y + orow * a.ldy + col;
+    *y = apply_epi<EPI>(v, a.bias, col, y);
+}
 
 template <int EPI, int MB>
-__global__ void __launch_bounds__(SK_NW * 64) k_skinny(GemmArgs a) {
-    constexpr int D = MB <= 2 ? 4 : 2;
-    __shared__ float part[SK_NW][MB][4][64];
+__global__ void __launch_bounds__(ST_NW * 64) k_stream(GemmArgs a, int tiles_n, int KR, int KS) {
+    constexpr int R = 16 * MB;                                  // rows held (M <= R)
+    constexpr int XF4 = R * ST_KC / 4;                          // float4 per X chunk
+    constexpr int XPT = (XF4 + ST_NW * 64 - 1) / (ST_NW * 64);  // per thread
+    __shared__ float xs[2][R * ST_XP];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int lc = lane & 15, lk = (lane >> 4) * 4;
-    const int n0 = blockIdx.x * 16;
-    const int K = a.K;
-    const int nsteps = (K + 15) / 16;
-    const int per = (nsteps + SK_NW - 1) / SK_NW;
-    const int s0 = min(nsteps, wave * per), s1 = min(nsteps, s0 + per);
-    const float* wrow = a.W + (long)min(n0 + lc, a.N - 1) * K;
-    const float* xrow[MB];
+    const int lc = lane & 15, g4 = (lane >> 4) * 4;
+    const int tn = blockIdx.x % tiles_n, ks = blockIdx.x / tiles_n;
+    const int K = a.K, M = a.M, N = a.N;
+    const int kb = ks * KR, ke = min(K, kb + KR);
+    const int nchunks = (ke - kb + ST_KC - 1) / ST_KC;
+    const int nsteps = nchunks * ST_PF;
+    const int col = tn * ST_NT + 16 * wave + lc;
+    const float* wrow = a.W + (long)min(col, N - 1) * K;
+
+    // input chunk c -> registers (zero past M or ke); clamped addresses
+    auto xload = [&](f32x4 (&xr)[XPT], int c) {
 #pragma unroll
-    for (int mb = 0; mb < MB; mb++) xrow[mb] = a.X + (long)min(mb * 16 + lc, a.M - 1) * K;
+        for (int i = 0; i < XPT; i++) {
+            const int f = tid + i * ST_NW * 64;
+            const int row = f / (ST_KC / 4), k = kb + c * ST_KC + (f % (ST_KC / 4)) * 4;
+            const bool ok = f < XF4 && row < M && k < ke;
+            const f32x4 v = *(const f32x4*)(a.X + (long)min(row, M - 1) * K + min(k, K - 4));
+            xr[i] = ok ? v : f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+    };
+    auto xstore = [&](const f32x4 (&xr)[XPT], int buf) {
+#pragma unroll
+        for (int i = 0; i < XPT; i++) {
+            const int f = tid + i * ST_NW * 64;
+            if (f < XF4) {
+                const int row = f / (ST_KC / 4), k4 = f % (ST_KC / 4);
+                *(f32x4*)&xs[buf][row * ST_XP + k4 * 4] = xr[i];
+            }
+        }
+    };
+    // weight step s: this lane's column at k = kb + 16 s + g4 .. +3 (steps
+    // past the range re-read the last one; their product is masked)
+    auto wload = [&](int s) {
+        const int k = kb + 16 * min(s, nsteps - 1) + g4;
+        return *(const f32x4*)(wrow + min(k, K - 4));
+    };
 
     f32x4 acc[MB];
 #pragma unroll
     for (int mb = 0; mb < MB; mb++) acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
-    f32x4 wa[D], xa[D][MB], wb[D], xb[D][MB];
-    bool oa[D], ob[D];
-    // No branches around the loads (a branch per guarded load makes the
-    // compiler wait for every outstanding load at its join, which defeats
-    // the double buffer): a step past this wavefront's range re-reads its
-    // last step (cached) and a k past K re-reads the row's last 4 floats,
-    // and the weight value is zeroed at its use so the product vanishes (a
-    // select in the load phase would wait for the load there).
-    const int slast = max(s0, s1 - 1);
-    auto load = [&](f32x4* w, f32x4 (*x)[MB], bool* ok, int s) {
+    f32x4 wr[ST_PF];
 #pragma unroll
-        for (int d = 0; d < D; d++) {
-            const int k = min(s + d, slast) * 16 + lk;
-            ok[d] = s + d < s1 && k < K;
-            const int kk = min(k, K - 4);
-            w[d] = *(const f32x4*)(wrow + kk);
+    for (int j = 0; j < ST_PF; j++) wr[j] = wload(j);
+    f32x4 xr[XPT];
+    xload(xr, 0);
+    xstore(xr, 0);
+    __syncthreads();
+    for (int c = 0; c < nchunks; c++) {
+        if (c + 1 < nchunks) xload(xr, c + 1);
+        const float* xb = xs[c & 1];
 #pragma unroll
-            for (int mb = 0; mb < MB; mb++) x[d][mb] = *(const f32x4*)(xrow[mb] + kk);
-        }
-    };
-    auto mul = [&](const f32x4* w, f32x4 (*x)[MB], const bool* ok) {
+        for (int j = 0; j < ST_PF; j++) {
+            const int s = c * ST_PF + j;
+            const bool kok = kb + 16 * s + g4 < ke;
+            f32x4 xf[MB];
 #pragma unroll
-        for (int d = 0; d < D; d++)
+            for (int mb = 0; mb < MB; mb++)
+                xf[mb] = *(const f32x4*)&xb[(16 * mb + lc) * ST_XP + 16 * j + g4];
+            const f32x4 w = wr[j];
+            wr[j] = wload(s + ST_PF);
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                const float we = ok[d] ? w[d][e] : 0.f;
+                const float we = kok ? w[e] : 0.f;
 #pragma unroll
                 for (int mb = 0; mb < MB; mb++)
-                    acc[mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[d][mb][e], we, acc[mb], 0, 0,
-                                                                    0);
+                    acc[mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(xf[mb][e], we, acc[mb], 0, 0, 0);
             }
-    };
-    // sched_barrier keeps the scheduler from sinking each load next to its
-    // first use, which would undo the double buffer.
-    if (s0 < s1) {
-        load(wa, xa, oa, s0);
-        for (int s = s0; s < s1; s += 2 * D) {
-            load(wb, xb, ob, s + D);
-            __builtin_amdgcn_sched_barrier(0);
-            mul(wa, xa, oa);
-            __builtin_amdgcn_sched_barrier(0);
-            load(wa, xa, oa, s + 2 * D);
-            __builtin_amdgcn_sched_barrier(0);
-            mul(wb, xb, ob);
-            __builtin_amdgcn_sched_barrier(0);
         }
+        // the other buffer was last read in chunk c - 1, before the barrier
+        if (c + 1 < nchunks) xstore(xr, (c + 1) & 1);
+        __syncthreads();
     }
-    // acc[mb][r]: row mb*16 + 4*(lane/16) + r, column n0 + lane%16.
+
+    // acc[mb][r]: row 16 mb + 4 (lane / 16) + r, column col
+    if (col >= N) return;
+    if (KS == 1) {
+        const long roff = a.row_off + (a.row_off_dev ? *a.row_off_dev : 0);
+#pragma unroll
+        for (int mb = 0; mb < MB; mb++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int row = 16 * mb + g4 + r;
+                if (row < M) store_out<EPI>(a, roff, row, col, acc[mb][r]);
+            }
+        return;
+    }
 #pragma unroll
     for (int mb = 0; mb < MB; mb++)
 #pragma unroll
-        for (int r = 0; r < 4; r++) part[wave][mb][r][lane] = acc[mb][r];
-    __syncthreads();
+        for (int r = 0; r < 4; r++) {
+            const int row = 16 * mb + g4 + r;
+            if (row < M) a.part[((long)ks * M + row) * N + col] = acc[mb][r];
+        }
+}
+
+// Y = epi(sum over the KS partial tiles, in order); one thread per output.
+template <int EPI>
+__global__ void __launch_bounds__(256) k_stream_reduce(GemmArgs a, int KS) {
+    const long i = (long)blockIdx.x * 256 + threadIdx.x;
+    const long MN = (long)a.M * a.N;
+    if (i >= MN) return;
+    float v = 0.f;
+    for (int q = 0; q < KS; q++) v += a.part[q * MN + i];
     const long roff = a.row_off + (a.row_off_dev ? *a.row_off_dev : 0);
-    for (int idx = tid; idx < MB * 4 * 64; idx += SK_NW * 64) {
-        const int mb = idx / 256, r = (idx / 64) & 3, l = idx & 63;
-        float v = 0.f;
-#pragma unroll
-        for (int w = 0; w < SK_NW; w++) v += part[w][mb][r][l];
-        const int row = mb * 16 + 4 * (l >> 4) + r, col = n0 + (l & 15);
-        if (row >= a.M || col >= a.N) continue;
-        long orow = a.seg ? (long)(row / a.seg) * a.seg_stride + row % a.seg : row;
-        orow += roff;
-        float* y = a.Y + orow * a.ldy + col;
-        *y = apply_epi<EPI>(v, a.bias, col, y);
-    }
+    store_out<EPI>(a, roff, (int)(i / a.N), (int)(i % a.N), v);
+}
+
+// Split K until the column tiles times the splits reach two workgroups per
+// CU (the partials must fit a.part_cap floats; ranges are whole chunks).
+template <int EPI, int MB>
+hipError_t stream_mb(const GemmArgs& a, hipStream_t s) {
+    const int tiles_n = (a.N + ST_NT - 1) / ST_NT;
+    const int kchunks = (a.K + ST_KC - 1) / ST_KC;
+    int KS = a.part ? std::max(1, std::min((512 + tiles_n - 1) / tiles_n, kchunks)) : 1;
+    while (KS > 1 && (long)KS * a.M * a.N > a.part_cap) KS--;
+    const int KR = ((kchunks + KS - 1) / KS) * ST_KC;
+    KS = (a.K + KR - 1) / KR;
+    k_stream<EPI, MB><<<tiles_n * KS, ST_NW * 64, 0, s>>>(a, tiles_n, KR, KS);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || KS == 1) return e;
+    k_stream_reduce<EPI><<<(unsigned)(((long)a.M * a.N + 255) / 256), 256, 0, s>>>(a, KS);
+    return hipGetLastError();
 }
 
 template <int EPI>
 hipError_t skinny_epi(const GemmArgs& a, hipStream_t s) {
-    const int grid = (a.N + 15) / 16;
-    if (a.M <= 16) k_skinny<EPI, 1><<<grid, SK_NW * 64, 0, s>>>(a);
-    else if (a.M <= 32) k_skinny<EPI, 2><<<grid, SK_NW * 64, 0, s>>>(a);
-    else if (a.M <= 48) k_skinny<EPI, 3><<<grid, SK_NW * 64, 0, s>>>(a);
-    else k_skinny<EPI, 4><<<grid, SK_NW * 64, 0, s>>>(a);
-    return hipGetLastError();
+    if (a.M <= 16) return stream_mb<EPI, 1>(a, s);
+    if (a.M <= 32) return stream_mb<EPI, 2>(a, s);
+    if (a.M <= 48) return stream_mb<EPI, 3>(a, s);
+    return stream_mb<EPI, 4>(a, s);
 }
 
 // Share of the tile slots the last round of a launch fills when `res`

@@ -28,8 +28,10 @@ struct GemmArgs {
     int row_off;               // added to every output row index
     const int* row_off_dev;    // if set, *row_off_dev is added too (decode position)
     int epi;                   // EpiMode
+    float* part;               // split-K partials of M <= SKINNY_MAX_M (NULL: no split)
+    long part_cap;             // floats available at part
 };
-// M <= SKINNY_MAX_M rows take the weight-streaming k_skinny, larger M the
+// M <= SKINNY_MAX_M rows take the weight-streaming k_stream, larger M the
 // 128 x 128 MFMA tiles.
 constexpr int SKINNY_MAX_M = 64;
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t s);
