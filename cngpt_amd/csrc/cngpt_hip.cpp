@@ -607,7 +607,12 @@ int persist_refused(cngpt_hip_ctx* h) {
 }
 
 // n greedy decode steps of the single cached sequence as one launch.
-int run_persist(cngpt_hip_ctx* h, int n) {
+// n persistent steps; with top_k > 0 each step samples its token with
+// draws[step] inside the launch. *done (when set) receives the steps that
+// ran: a sampling step whose candidates overflowed ends the launch early,
+// its logits in place and its token left to the host.
+int run_persist(cngpt_hip_ctx* h, int n, float temp = 0.f, int top_k = 0,
+                const float* draws = nullptr, int* done = nullptr) {
     const cngpt_hip_config& c = h->cfg;
     const double C = c.n_embd, L = c.n_layer, V = c.vocab_size;
     PersistArgs a{};
@@ -618,6 +623,8 @@ int run_persist(cngpt_hip_ctx* h, int n) {
     a.logits = h->logits; a.hist = h->hist;
     a.pos = h->pos; a.tok = h->next_tok; a.err = h->dev_err;
     a.n_steps = n;
+    a.temp = temp; a.top_k = top_k; a.draws = draws;
+    a.steps_done = done ? h->dev_err + 2 : nullptr;
     // tags only grow; before they would wrap, clear the words and restart
     const unsigned need = persist_tags(c.n_layer, n);
     if (h->ptag_next > 0xF0000000u - need) {
@@ -638,6 +645,13 @@ int run_persist(cngpt_hip_ctx* h, int n) {
     {
         Timed tm(h, CNGPT_K_STEP, flops, bytes);
         HIP_TRY(launch_decode_persist(a, h->persist_G, h->stream));
+    }
+    if (done) {
+        HIP_TRY(hipMemcpyAsync(done, h->dev_err + 2, sizeof(int), hipMemcpyDeviceToHost,
+                               h->stream));
+        HIP_TRY(hipStreamSynchronize(h->stream));
+        if (*done < 1 || *done > n) return fail("persistent decode ran %d of %d steps", *done, n);
+        n = *done;
     }
     h->kvLen += n;
     h->curB = 1; h->curT = 1; h->curMode = CNGPT_LAST;
@@ -1198,6 +1212,22 @@ int cngpt_hip_generate(cngpt_hip_ctx* h, int n_new, float temperature, int top_k
     if (persist && !draws) {
         // greedy: every step in one launch, the argmax fed back on the device
         if (n_new > 1 && run_persist(h, n_new - 1)) return -1;
+    } else if (persist && persist_sampling_supported(h->cfg.vocab_size, h->persist_G, top_k)) {
+        // sampled inside the launch: step i draws token i with draws[i];
+        // a step whose candidates overflow ends the launch, and its token
+        // is drawn here before the next launch continues
+        for (int i = 1; i < n_new;) {
+            int done = 0;
+            if (run_persist(h, n_new - i, temperature, top_k, h->draws + (size_t)i * B, &done))
+                return -1;
+            i += done;
+            int next = 0;
+            HIP_TRY(hipMemcpyAsync(&next, h->next_tok, sizeof(int), hipMemcpyDeviceToHost,
+                                   h->stream));
+            HIP_TRY(hipStreamSynchronize(h->stream));
+            if (next < 0 && run_sample(h, h->draws + (size_t)(i - 1) * B, temperature, top_k))
+                return -1;
+        }
     } else if (persist) {
         // sampled: one persistent step per launch, then the sampler replaces
         // the step's argmax by the sampled token the next launch embeds

@@ -160,6 +160,12 @@ struct PersistArgs {
     int* err;
     int n_steps;
     float scale;            // 1 / sqrt(head size)
+    // sampling (top_k > 0): sample_top_k with draws[step]; 0: greedy
+    float temp;
+    int top_k;
+    const float* draws;
+    int* steps_done;        // steps completed (a sampling step whose
+                            // candidates overflow ends the launch early)
 };
 // Workgroups of the launch (one per CU), 0 if the device has no
 // cooperative launch.
@@ -170,6 +176,9 @@ bool persist_supported(int C, int H, int V, int cap, int G);
 // matches a tag this launch waits for.
 long persist_tagged_words(int C, int H);
 unsigned persist_tags(int L, int n_steps);
+// Whether a launch of G workgroups can draw top-k samples itself (else the
+// host samples between one-step launches).
+bool persist_sampling_supported(int V, int G, int top_k);
 hipError_t launch_decode_persist(const PersistArgs& a, int G, hipStream_t s);
 
 // attention.hip

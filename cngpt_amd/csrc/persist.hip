@@ -67,6 +67,14 @@ constexpr long SPIN_LIMIT = 1L << 20;  // polls of one value before giving up
 // for two phases (2 * UPW * U float4, U = ceil(C / 256)) then fit in
 // registers beside the rest; wider models take the kernel-per-stage decode.
 constexpr int PMAXU = 3;
+// Sampling inside the launch (top_k <= SK_MAX): each workgroup keeps the
+// logits of its lm_head columns (at most SK_RMAX per compute wavefront) and
+// publishes at most SK_CMAX candidates.
+constexpr int SK_MAX = 64;
+constexpr int SK_RMAX = 32;
+constexpr int SK_CMAX = 4;
+constexpr int SK_SLOT = 1 + 2 * SK_CMAX;  // count, then (value, index) pairs
+constexpr int SK_CAND = 256 * SK_CMAX;    // candidates gathered (G <= 256)
 
 __device__ __forceinline__ void st_sc(float* p, float v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -173,6 +181,15 @@ struct Smem {
     float bestv[PW + 1];
     int besti[PW + 1];
     int abort;
+    // sampling
+    float sx[PW * SK_RMAX];       // scaled logits of this workgroup's columns
+    float cx[SK_CAND];            // candidates of every workgroup: value
+    int ci[SK_CAND];              //   and index; then the survivors in index order
+    float so[SK_CAND];
+    int soi[SK_CAND];
+    float raw[256 * SK_SLOT];     // the candidate words as fetched
+    int n_c, n_sv, over, stok;
+    float sL, sc, sns;
 };
 
 // Exchange words (offsets in u64 units).
@@ -182,12 +199,13 @@ struct Smem {
 // reads on the few memory channels that hold it.
 constexpr int REPL = 8;
 struct TagLayout {
-    int xs, hs, ps, as;  // copy strides
-    int x, q, hid, part, am, abortw;
+    int xs, hs, ps, as, cs;  // copy strides
+    int x, q, hid, part, am, cand, abortw;
     __host__ __device__ TagLayout(int C, int H)
         : xs(C + 512), hs(4 * C + 512), ps(H * PMAXS * 68 + 512), as(2 * PT + 512),
-          x(0), q(REPL * xs), hid(q + 3 * C + 512), part(hid + REPL * hs),
-          am(part + REPL * ps), abortw(am + REPL * as) {}
+          cs(SK_SLOT * PT + 512), x(0), q(REPL * xs), hid(q + 3 * C + 512),
+          part(hid + REPL * hs), am(part + REPL * ps), cand(am + REPL * as),
+          abortw(cand + REPL * cs) {}
     __host__ __device__ long words() const { return abortw + 32; }
 };
 __device__ __forceinline__ void put_all(u64* p, int stride, float v, unsigned tag) {
@@ -205,6 +223,18 @@ __device__ __forceinline__ float block_sum(float v, float* wred, int wave, int l
     for (int i = 0; i < PW + 1; i++) s += wred[i];
     __syncthreads();
     return s;
+}
+
+// Max over the workgroup, same value in every thread.
+__device__ __forceinline__ float block_max(float v, float* wred, int wave, int lane) {
+    v = wave_max_dpp(v);
+    if (lane == 0) wred[wave] = v;
+    __syncthreads();
+    float m = wred[0];
+#pragma unroll
+    for (int i = 1; i < PW + 1; i++) m = fmaxf(m, wred[i]);
+    __syncthreads();
+    return m;
 }
 
 // LayerNorm (reference ops.c:191-248) of v (element tid + PT * i) into act.
@@ -314,14 +344,16 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
     u64* const tq = a.tagged + tl.q;      // q, k, v of row t (one copy)
     u64* const th = a.tagged + tl.hid;    // GELU(fc)
     u64* const tp = a.tagged + tl.part;   // attention partials [H][PMAXS][68]
-    u64* const tam = a.tagged + tl.am;    // argmax partials [G][2]
+    u64* const tam = a.tagged + tl.am;    // argmax partials [G][2] (sampling: max, sum)
+    u64* const tcd = a.tagged + tl.cand;  // sampling candidates [G][SK_SLOT]
     const u64* const rx = tx + rep * tl.xs;
     const u64* const rh = th + rep * tl.hs;
     const u64* const rp = tp + rep * tl.ps;
     const u64* const ram = tam + rep * tl.as;
+    const u64* const rcd = tcd + rep * tl.cs;
     u64* const abortw = a.tagged + tl.abortw;
     const u64 amark = (u64)a.tag0 + 1;  // the abort word's value for this launch
-    const unsigned per_step = PHASES * L + 1;
+    const unsigned per_step = PHASES * L + 2;  // + the sampling candidates
 
     if (tid == 0) sm.abort = 0;
     __syncthreads();
@@ -340,6 +372,8 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
 
     int t = *a.pos;
     int tok = *a.tok;
+    const bool samp = a.top_k > 0;
+    const float tdiv = a.temp > 0.0f ? a.temp : 1.0f;
     // Two weight buffers: the weights of the next phase that has any are
     // loaded at the start of the current one (as soon as its input has
     // arrived), so they are in registers before the workgroup reads the
@@ -747,6 +781,7 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
                         }
                         s = wave_sum_dpp(s);
                         if (ln == 0 && a.logits) a.logits[col] = s;
+                        if (samp && ln == 0) sm.sx[wave * SK_RMAX + r] = s / tdiv;
                         if (better(s, col, best, bi)) {
                             best = s;
                             bi = col;
@@ -761,7 +796,26 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
         }
         __syncthreads();
         bo = slot_bias(layers[0].attn_b, C3);
-        if (ctrl && lane1 == 0) {
+        // sampling: the workgroup's scaled logits (wavefront w holds the
+        // first rounds_w of sx[w][.]), their max m_g and sum of expf(x - m_g)
+        auto own_logit = [&](bool& have, int& col) -> float {
+            const int tt = opaque_v(tid);
+            const int w = tt / SK_RMAX, r = tt - w * SK_RMAX;
+            col = blockIdx.x * PW + w + CW * r;
+            have = w < PW && col < V;
+            return have ? sm.sx[min(tt, PW * SK_RMAX - 1)] : -INFINITY;
+        };
+        if (samp) {
+            bool shave;
+            int scol;
+            const float sxv = own_logit(shave, scol);
+            const float mg = block_max(sxv, sm.wred, wave, lane1);
+            const float sg = block_sum(shave ? expf(sxv - mg) : 0.f, sm.wred, wave, lane1);
+            if (ctrl && lane1 == 0) {
+                put_all(tam + 2 * blockIdx.x, tl.as, mg, TF);
+                put_all(tam + 2 * blockIdx.x + 1, tl.as, sg, TF);
+            }
+        } else if (ctrl && lane1 == 0) {
             float b = sm.bestv[0];
             int bi = sm.besti[0];
             for (int v = 1; v < PW; v++)
@@ -778,7 +832,162 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
         }
 
         // ---------------- phase G: every workgroup reduces the argmax partials
-        {
+        if (samp) {
+            // G1: M and S over the workgroups' (m_g, s_g); the lower bound L
+            // of the top_k-th largest scaled logit: the top_k-th largest m_g
+            // (top_k workgroups hold a value >= it; top_k <= G)
+            const int tt = opaque_v(tid);
+            const int g = min(tt, G - 1);
+            int idx[2] = {2 * g, 2 * g + 1};
+            bool need[2] = {tt < G, tt < G};
+            float pv[2];
+            if (!settle(fetch<2>(ram, idx, need, TF, pv, abortw, amark))) return;
+            const float mg = tt < G ? pv[0] : -INFINITY;
+            if (tt < G) sm.ml[0][tt] = mg;
+            const float M = block_max(mg, sm.wred, wave, lane1);
+            const float S = block_sum(tt < G ? pv[1] * expf(mg - M) : 0.f, sm.wred, wave, lane1);
+            if (tt < G) {
+                int gt = 0, ge = 0;
+                for (int u = 0; u < G; u++) {
+                    const float o = sm.ml[0][u];
+                    gt += o > mg;
+                    ge += o >= mg;
+                }
+                if (gt < a.top_k && a.top_k <= ge) sm.sL = mg;
+            }
+            if (tid == 0) sm.n_c = 0;
+            __syncthreads();
+            const float pL = expf(sm.sL - M) / S;
+            // candidates of this workgroup: p >= p(L), which holds every
+            // value with p >= t, t = p(top_k-th largest) >= p(L)
+            bool shave;
+            int scol;
+            const float sxv = own_logit(shave, scol);
+            if (shave && expf(sxv - M) / S >= pL) {
+                const int q = atomicAdd(&sm.n_c, 1);
+                if (q < SK_CMAX) {
+                    sm.cx[q] = sxv;
+                    sm.ci[q] = scol;
+                }
+            }
+            __syncthreads();
+            const unsigned TG = TF + 1;
+            if (tid < SK_SLOT) {
+                // (opaque indices: hoisted out of the step loop, these
+                // addresses would take registers for the whole launch)
+                const int tq = opaque_v(tid);
+                const int m = max((tq - 1) >> 1, 0);
+                const int nq = min(sm.n_c, SK_CMAX);
+                float v = 0.f;
+                if (tq == 0) v = __int_as_float(sm.n_c);
+                else if (m < nq) v = (tq & 1) ? sm.cx[m] : __int_as_float(sm.ci[m]);
+                put_all(tcd + opaque_v(blockIdx.x * SK_SLOT + tq), tl.cs, v, TG);
+            }
+            // G2: every workgroup gathers every candidate and draws the same
+            // token (sample_top_k's arithmetic on the survivors, in index order)
+            constexpr int NF = (256 * SK_SLOT + PT - 1) / PT;
+            const int nw = G * SK_SLOT;
+            int cidx[NF];
+            bool cneed[NF];
+            float cv[NF];
+#pragma unroll
+            for (int i = 0; i < NF; i++) {
+                cidx[i] = min(tt + PT * i, nw - 1);
+                cneed[i] = tt + PT * i < nw;
+            }
+            if (!settle(fetch<NF>(rcd, cidx, cneed, TG, cv, abortw, amark))) return;
+            if (tid == 0) { sm.n_c = 0; sm.over = 0; sm.n_sv = 0; }
+            // counts first (slot 0 of each workgroup), into ml[1]
+#pragma unroll
+            for (int i = 0; i < NF; i++) {
+                const int e = tt + PT * i;
+                if (cneed[i] && e % SK_SLOT == 0) sm.ml[1][e / SK_SLOT] = cv[i];
+            }
+            __syncthreads();
+#pragma unroll
+            for (int i = 0; i < NF; i++) {
+                const int e = tt + PT * i, gg = e / SK_SLOT, j = e - gg * SK_SLOT;
+                if (!cneed[i]) continue;
+                const int cnt = __float_as_int(sm.ml[1][gg]);
+                if (j == 0 && cnt > SK_CMAX) sm.over = 1;
+                // a pair's two words are fetched by different threads:
+                // they meet in LDS
+                if (j > 0 && ((j - 1) >> 1) < min(cnt, SK_CMAX)) sm.raw[gg * SK_SLOT + j] = cv[i];
+            }
+            __syncthreads();
+            if (sm.over) {
+                // more candidates than a workgroup publishes: the host draws
+                // this step's token and continues with a new launch
+                if (blockIdx.x == 0 && tid == 0) {
+                    *a.tok = -1;
+                    *a.pos = t + 1;
+                    if (a.steps_done) *a.steps_done = step + 1;
+                }
+                return;
+            }
+            for (int q = tt; q < G * SK_CMAX; q += PT) {
+                const int gg = q / SK_CMAX, m = q - gg * SK_CMAX;
+                if (m < __float_as_int(sm.ml[1][gg])) {
+                    const int d = atomicAdd(&sm.n_c, 1);
+                    sm.cx[d] = sm.raw[gg * SK_SLOT + 1 + 2 * m];
+                    sm.ci[d] = __float_as_int(sm.raw[gg * SK_SLOT + 2 + 2 * m]);
+                }
+            }
+            __syncthreads();
+            const int nc = sm.n_c;
+            // c = the top_k-th largest candidate (equal values give equal c)
+            for (int q = tt; q < nc; q += PT) {
+                const float v = sm.cx[q];
+                int gt = 0, ge = 0;
+                for (int u = 0; u < nc; u++) {
+                    const float o = sm.cx[u];
+                    gt += o > v;
+                    ge += o >= v;
+                }
+                if (gt < a.top_k && a.top_k <= ge) sm.sc = v;
+            }
+            __syncthreads();
+            const float thr = expf(sm.sc - M) / S;
+            for (int q = tt; q < nc; q += PT) {
+                const float p = expf(sm.cx[q] - M) / S;
+                if (p >= thr) {
+                    const int d = atomicAdd(&sm.n_sv, 1);
+                    sm.so[d] = p;
+                    sm.soi[d] = sm.ci[q];
+                }
+            }
+            __syncthreads();
+            const int nsv = sm.n_sv;
+            for (int q = tt; q < nsv; q += PT) {
+                const int iq = sm.soi[q];
+                int rank = 0;
+                for (int u = 0; u < nsv; u++) rank += sm.soi[u] < iq;
+                sm.cx[rank] = sm.so[q];
+                sm.ci[rank] = iq;
+            }
+            __syncthreads();
+            if (tid == 0) {
+                float ns = 0.f;
+                for (int q = 0; q < nsv; q++) ns += sm.cx[q];
+                sm.sns = ns;
+            }
+            __syncthreads();
+            for (int q = tt; q < nsv; q += PT) sm.cx[q] = sm.sns > 0.0f ? sm.cx[q] / sm.sns : sm.cx[q];
+            __syncthreads();
+            if (tid == 0) {
+                const float r = a.draws[step];
+                int tk = V - 1;
+                float cdf = 0.f;
+                for (int q = 0; q < nsv; q++) {
+                    cdf += sm.cx[q];
+                    if (r < cdf) { tk = sm.ci[q]; break; }
+                }
+                sm.stok = tk;
+            }
+            __syncthreads();
+            tok = sm.stok;
+            __syncthreads();
+        } else {
             const int tt = opaque_v(tid);
             const int g = min(tt, G - 1);
             int idx[2] = {2 * g, 2 * g + 1};
@@ -818,6 +1027,7 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
     if (blockIdx.x == 0 && tid == 0) {
         *a.tok = tok;
         *a.pos = t;
+        if (a.steps_done) *a.steps_done = a.n_steps;
     }
 }
 
@@ -842,7 +1052,7 @@ int persist_workgroups(int device) {
 
 long persist_tagged_words(int C, int H) { return TagLayout(C, H).words(); }
 
-unsigned persist_tags(int L, int n_steps) { return (unsigned)n_steps * (PHASES * L + 1) + 1; }
+unsigned persist_tags(int L, int n_steps) { return (unsigned)n_steps * (PHASES * L + 2) + 1; }
 
 bool persist_supported(int C, int H, int V, int cap, int G) {
     if (G < 1 || G > PT || C % 64 || C != 64 * H || C > 256 * PMAXU || H > 32 || C > LNE * PT)
@@ -854,6 +1064,12 @@ bool persist_supported(int C, int H, int V, int cap, int G) {
     const int ns = std::min(G / H, PMAXS);
     if (ns < 1 || (long)ns * PW * KPW < cap) return false;
     return true;
+}
+
+bool persist_sampling_supported(int V, int G, int top_k) {
+    const long CW = (long)PW * G;
+    return top_k > 0 && top_k <= SK_MAX && top_k <= G && top_k < V && G <= 256 &&
+           (V + CW - 1) / CW <= SK_RMAX;
 }
 
 hipError_t launch_decode_persist(const PersistArgs& a, int G, hipStream_t s) {

@@ -120,6 +120,46 @@ def test_persistent_sampled_generate():
             break
 
 
+def test_persistent_in_launch_sampling_designed_rows():
+    """Sampling inside the persistent launch on logits rows set exactly (the
+    final LayerNorm outputs e_0, so every step's logits are wte[:, 0]):
+    random values, 50 ties at the cut spread over the vocabulary, and a
+    3000-way tie at the top, which overflows the workgroups' candidate
+    slots so that each step ends the launch and the host draws its token.
+    Every token is sample_top_k of the row with its draw, up to the
+    rounding of the CDF's fp32 running sums."""
+    from test_decode_gpu import consistent, designed_logits_model, survivors
+    V = 50257
+    cfg, params, w = designed_logits_model(V)
+    rng = np.random.default_rng(31)
+    base = (rng.standard_normal(V) * 3).astype(np.float32)
+    rows = {"random": base}
+    r = base.copy()
+    r[rng.choice(V, 30, replace=False)] = 30 + rng.random(30).astype(np.float32)
+    r[np.arange(50) * 1000 + 7] = np.float32(25.0)
+    rows["tie_spread"] = r
+    r = base.copy()
+    r[5000:8000] = np.float32(12.5)
+    rows["wide_tie"] = r
+    n = 24
+    prompt = oracle.lcg_tokens(8, V, seed=4).reshape(1, 8)
+    with cngpt_amd.Model(cfg, params) as m:
+        for name, row in rows.items():
+            w["wte"][:, 0] = row
+            m.load_params(params)
+            for temp, k in ((1.0, 40), (0.7, 1), (1.2, 64)):
+                draws = rng.random(n).astype(np.float32)
+                say(f"in-launch sampling: {name}, temp {temp}, top-k {k}")
+                m.decode_begin(prompt, capacity=8 + n)
+                got = m.generate(n, temp, k, draws)[0]
+                assert m.decode_path() == cngpt_amd.DECODE_PERSISTENT
+                tol = 1e-5 + 2 * survivors(row, temp, k) * 2.0**-24
+                for i in range(n):
+                    ref = oracle.sample_top_k(row, temp, k, float(draws[i]))
+                    assert got[i] == ref or consistent(row, temp, k, float(draws[i]), got[i],
+                                                       tol), (name, temp, k, i, got[i], ref)
+
+
 def test_persistent_gpt2_small_long_context():
     """GPT-2 small at full depth, the last 24 positions of the 1024-token
     window (keys up to 1023)."""
