@@ -56,10 +56,10 @@ enum {
 /* How decode steps run. KERNELS: one replayed graph of per-stage kernels
  * per step (any batch). PERSISTENT: the steps of one sequence as a
  * cooperative launch whose workgroups exchange each stage's outputs
- * through tagged words (B = 1, head size 64, n_embd <= 768): all greedy
- * steps of a generate call in one launch, sampled steps one launch each
- * followed by the sampler. AUTO: PERSISTENT where it applies, else
- * KERNELS. */
+ * through tagged words (B = 1, head size 64, n_embd <= 768): all steps of
+ * a generate call in one launch, greedy or sampled (top_k <= 64; other
+ * sampling runs one launch per step followed by the sampler). AUTO:
+ * PERSISTENT where it applies, else KERNELS. */
 enum { CNGPT_DECODE_AUTO = 0, CNGPT_DECODE_KERNELS = 1, CNGPT_DECODE_PERSISTENT = 2 };
 
 /* Last error message of the calling thread ("" if none). */
