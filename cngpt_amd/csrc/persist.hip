@@ -320,7 +320,7 @@ __device__ __forceinline__ int slot_col(int slot, int N, int CW, int& j, int& q)
     return c < N ? c : -1;
 }
 
-template <int U>
+template <int U, bool SAMP>
 __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
     constexpr int NW = UPW * U;  // weight registers (float4) per lane
     __shared__ Smem<U> sm;
@@ -372,7 +372,7 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
 
     int t = *a.pos;
     int tok = *a.tok;
-    const bool samp = a.top_k > 0;
+    constexpr bool samp = SAMP;  // the greedy instantiation carries no sampling code
     const float tdiv = a.temp > 0.0f ? a.temp : 1.0f;
     // Two weight buffers: the weights of the next phase that has any are
     // loaded at the start of the current one (as soon as its input has
@@ -843,15 +843,17 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
             float pv[2];
             if (!settle(fetch<2>(ram, idx, need, TF, pv, abortw, amark))) return;
             const float mg = tt < G ? pv[0] : -INFINITY;
-            if (tt < G) sm.ml[0][tt] = mg;
+            if (tt < G + 4) sm.ml[0][tt] = mg;
             const float M = block_max(mg, sm.wred, wave, lane1);
             const float S = block_sum(tt < G ? pv[1] * expf(mg - M) : 0.f, sm.wred, wave, lane1);
             if (tt < G) {
+                // (entries G .. G+3 hold -inf: the float4 reads stay in range)
                 int gt = 0, ge = 0;
-                for (int u = 0; u < G; u++) {
-                    const float o = sm.ml[0][u];
-                    gt += o > mg;
-                    ge += o >= mg;
+                const f32x4* m4 = (const f32x4*)sm.ml[0];
+                for (int u = 0; u < (G + 3) / 4; u++) {
+                    const f32x4 o = m4[u];
+                    gt += (o.x > mg) + (o.y > mg) + (o.z > mg) + (o.w > mg);
+                    ge += (o.x >= mg) + (o.y >= mg) + (o.z >= mg) + (o.w >= mg);
                 }
                 if (gt < a.top_k && a.top_k <= ge) sm.sL = mg;
             }
@@ -966,23 +968,32 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
                 sm.ci[rank] = iq;
             }
             __syncthreads();
-            if (tid == 0) {
-                float ns = 0.f;
-                for (int q = 0; q < nsv; q++) ns += sm.cx[q];
-                sm.sns = ns;
-            }
-            __syncthreads();
-            for (int q = tt; q < nsv; q += PT) sm.cx[q] = sm.sns > 0.0f ? sm.cx[q] / sm.sns : sm.cx[q];
-            __syncthreads();
-            if (tid == 0) {
+            // wavefront 0: the renormalising sum and the running sum, each in
+            // index order, 64 survivors per round read from the lanes
+            if (wave == 0) {
                 const float r = a.draws[step];
+                float ns = 0.f;
+                for (int q0 = 0; q0 < nsv; q0 += 64) {
+                    const float pv = sm.cx[min(q0 + lane1, nsv - 1)];
+                    const int m = min(64, nsv - q0);
+                    for (int u = 0; u < m; u++) ns += lane_f(pv, u);
+                }
                 int tk = V - 1;
                 float cdf = 0.f;
-                for (int q = 0; q < nsv; q++) {
-                    cdf += sm.cx[q];
-                    if (r < cdf) { tk = sm.ci[q]; break; }
+                for (int q0 = 0; q0 < nsv && tk == V - 1; q0 += 64) {
+                    const float pv = sm.cx[min(q0 + lane1, nsv - 1)];
+                    const float qv = ns > 0.0f ? pv / ns : pv;
+                    const int iv = sm.ci[min(q0 + lane1, nsv - 1)];
+                    const int m = min(64, nsv - q0);
+                    for (int u = 0; u < m; u++) {
+                        cdf += lane_f(qv, u);
+                        if (r < cdf) {
+                            tk = __builtin_amdgcn_readlane(iv, u);
+                            break;
+                        }
+                    }
                 }
-                sm.stok = tk;
+                if (lane1 == 0) sm.stok = tk;
             }
             __syncthreads();
             tok = sm.stok;
@@ -1034,7 +1045,9 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
 template <int U>
 hipError_t launch_u(const PersistArgs& a, int G, hipStream_t s) {
     void* args[] = {(void*)&a};
-    return hipLaunchCooperativeKernel((const void*)k_decode_persist<U>, dim3(G), dim3(PT), args, 0,
+    const void* k = a.top_k > 0 ? (const void*)k_decode_persist<U, true>
+                                : (const void*)k_decode_persist<U, false>;
+    return hipLaunchCooperativeKernel(k, dim3(G), dim3(PT), args, 0,
                                       s);
 }
 
