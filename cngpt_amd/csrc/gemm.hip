@@ -12,10 +12,9 @@
 // the step's k and lanes 32-63 the second half, so each lane reads 4
 // contiguous floats per row per LDS read. Short K steps keep the LDS small
 // enough for 3-4 workgroups per CU, whose wavefronts hide each other's
-// barrier and load stalls: BK = 8 with 4 workgroups per CU is the fastest
-// variant on most GPT-2 shapes (122-135 TFLOP/s measured, against 93-121
-// for BK = 32 with 2); gemm_epi picks among BK = 8, 16 and 32 by how full
-// the last round of tiles is. The epilogue adds bias / GELU / residual and
+// barrier and load stalls; gemm_epi picks among three variants (BK = 16 at
+// 4 or 3 workgroups per CU, BK = 32 at 2) by how full the last round of
+// tiles is. The epilogue adds bias / GELU / residual and
 // stores straight from the accumulators (one 128-byte row segment per half
 // wavefront). Ragged M and N edges (e.g. the 50257-wide vocabulary) clamp
 // loads to the last valid row and mask stores.
@@ -338,18 +337,20 @@ double round_fill(int tiles, int res) {
     return rounds <= 1 ? 1.0 : (double)tiles / ((double)rounds * res);
 }
 
-// Variant choice, from a sweep of the three over the GPT-2 small / medium /
-// XL prefill products (M = 16384 / 8192 / 4096 rows): BK = 8 with 4
-// workgroups per CU is fastest whenever its tiles fit one round or fill its
-// last round; else BK = 16 with 3 per CU when that fills its last round
-// (e.g. 1536 or 2304 tiles); else BK = 32 with 2 per CU, whose longer K
-// steps hold up best when a round is left part-empty (e.g. 1216 tiles).
+// Variant choice, from sweeps over the GPT-2 small / medium / XL prefill
+// products (M = 16384 / 8192 / 4096 rows): BK = 16 with rows padded by 4
+// floats (40 KB of LDS, so 4 workgroups per CU still fit in 160 KB) is
+// fastest whenever its tiles fit one round or fill its last round (2-5 %
+// above BK = 8 at 4 per CU on GPT-2 small's c_proj, fc, proj and lm_head);
+// else BK = 16 with 3 per CU when that fills its last round (e.g. 1536 or
+// 2304 tiles); else BK = 32 with 2 per CU, whose longer K steps hold up
+// best when a round is left part-empty (e.g. 1216 tiles).
 template <int EPI>
 hipError_t gemm_epi(const GemmArgs& a, hipStream_t s) {
     const int tiles_m = (a.M + BM - 1) / BM, tiles_n = (a.N + BN - 1) / BN;
     const int tiles = tiles_m * tiles_n, cus = 256;
     if (tiles <= 4 * cus || round_fill(tiles, 4 * cus) >= 0.9)
-        k_gemm<EPI, 8, 4, 4><<<tiles, NTHREADS, 0, s>>>(a, tiles_m, tiles_n);
+        k_gemm<EPI, 16, 4, 4><<<tiles, NTHREADS, 0, s>>>(a, tiles_m, tiles_n);
     else if (round_fill(tiles, 3 * cus) >= 0.9)
         k_gemm<EPI, 16, 8, 3><<<tiles, NTHREADS, 0, s>>>(a, tiles_m, tiles_n);
     else
