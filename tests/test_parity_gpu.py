@@ -1,6 +1,6 @@
 """HIP forward pass vs the CPU oracle on the same seeded weights and tokens.
 
-Bar (north star): logits max|diff| <= 1e-3 and max|diff| / max|ref| <= 1e-4,
+Bar: logits max|diff| <= 1e-3 and max|diff| / max|ref| <= 1e-4,
 argmax identical. The tiny shapes of the reference's tests/check_fast.c use
 that test's own tighter bound, max|diff| < 1e-4 (check_fast.c:62).
 """
