@@ -62,11 +62,15 @@ __device__ __forceinline__ float wave_max_dpp(float v) {
 
 // GELU, tanh form (the formula of the reference's ops.h:56-58), with the
 // device library's tanhf.
+// 0.5 x (1 + tanh(u)), u = sqrt(2/pi) (x + 0.044715 x^3), evaluated as
+// x / (1 + exp(-2u)) (1 + tanh(u) = 2 / (1 + exp(-2u))): one hardware exp
+// and one reciprocal instead of a library tanh, a few ulp from it. Large
+// negative x give exp(-2u) = inf and the limit -0.
 __device__ __forceinline__ float gelu_tanh(float x) {
     const float k0 = 0.7978845608028654f;  // sqrt(2/pi)
     const float k1 = 0.044715f;
-    float x3 = x * x * x;
-    return 0.5f * x * (1.0f + tanhf(k0 * (x + k1 * x3)));
+    const float u = k0 * (x + k1 * (x * x * x));
+    return x * __builtin_amdgcn_rcpf(1.0f + __expf(-2.0f * u));
 }
 
 // Epilogues shared by the GEMM and GEMV kernels.

@@ -5,19 +5,28 @@
 // (fast.c:175-205). Both operands are K-contiguous, so both tiles are staged
 // in LDS the same way and read back with 16-byte LDS reads.
 //
-// k_gemm: 128x128 output tile per 256-thread workgroup, K in steps of BK,
-// double-buffered LDS (global loads for step k+1 are in flight while step k
-// is multiplied). Each wavefront owns a 64x64 sub-tile = 2x2 blocks of
+// k_gemm_dl / k_gemm: 128x128 output tile per 256-thread workgroup, K in
+// steps of BK. Each wavefront owns a 64x64 sub-tile = 2x2 blocks of
 // v_mfma_f32_32x32x2f32. Inside a K step, lanes 0-31 feed the first half of
 // the step's k and lanes 32-63 the second half, so each lane reads 4
-// contiguous floats per row per LDS read. Short K steps keep the LDS small
-// enough for 3-4 workgroups per CU, whose wavefronts hide each other's
-// barrier and load stalls; gemm_epi picks among three variants (BK = 16 at
-// 4 or 3 workgroups per CU, BK = 32 at 2) by how full the last round of
-// tiles is. The epilogue adds bias / GELU / residual and
-// stores straight from the accumulators (one 128-byte row segment per half
-// wavefront). Ragged M and N edges (e.g. the 50257-wide vocabulary) clamp
-// loads to the last valid row and mask stores.
+// contiguous floats per row per LDS read. The epilogue adds bias / GELU /
+// residual and stores straight from the accumulators (one 128-byte row
+// segment per half wavefront). Ragged M and N edges (e.g. the 50257-wide
+// vocabulary) clamp loads to the last valid row and mask stores.
+//
+// k_gemm_dl (K a multiple of BK): tiles go from global memory straight into
+// LDS (global_load_lds_dwordx4, no registers on the way) through a ring of
+// S stages, so the loads of S - 1 steps are in flight while one step is
+// multiplied, and each step costs one wait and one barrier. A wavefront's
+// load instruction fills 64 consecutive 16-byte granules, so the granule
+// order within a row is XOR-swizzled by the row (rows that share LDS banks
+// get different k quads at a given address) instead of padded: the 16
+// lanes of a quarter-wavefront reading 16 rows at one k quad hit 16
+// different granules of a 256-byte bank line.
+//
+// k_gemm (any K that is a multiple of 4): global loads into registers for
+// step k+1 while step k is multiplied, then into a padded LDS double buffer;
+// the last step zero-fills past K.
 //
 // k_stream: M <= 64 rows, weights streamed once, input rows through LDS,
 // K split over workgroups when the column tiles are few. Products over
@@ -48,6 +57,131 @@ __device__ __forceinline__ void tile_coords(int pid, int tiles_m, int tiles_n, i
     const int in_group = p % (GM * tiles_n);
     tm = first_m + in_group % gsize;
     tn = in_group / gsize;
+}
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// s_waitcnt vmcnt(N), expcnt and lgkmcnt left alone.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (7 << 4) | (0xF << 8));
+}
+
+// Stage layout: operand tile of BM rows x BK floats, granule (16 bytes) g
+// at row g / GPR, slot g % GPR, where slot s of row r holds k quad
+// s ^ ((r / RSW) % GPR) (RSW = rows per 256 bytes). The MFMA order over k
+// is that of k_gemm with the same BK, so both give the same bits.
+template <int EPI, int BK, int S, int OCC>
+__global__ void __launch_bounds__(NTHREADS, OCC) k_gemm_dl(GemmArgs a, int tiles_m, int tiles_n) {
+    constexpr int GPR = BK / 4;      // granules per row
+    constexpr int RSW = 16 / GPR;    // rows per 256 bytes
+    constexpr int NI = GPR / 2;      // load instructions per operand per stage per wavefront
+    constexpr int NG = BK / 8;       // MFMA groups per step
+    constexpr int TILE = BM * BK;    // floats per operand per stage
+    static_assert(BM == BN && BM * GPR == NI * 4 * 64, "one granule per lane per instruction");
+    __shared__ __attribute__((aligned(1024))) float sm[S * 2 * TILE];
+
+    int tm, tn;
+    tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int K = a.K;
+
+    // granule (i * 4 + wave) * 64 + lane of each operand, every stage
+    const float* xp[NI];
+    const float* wp[NI];
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        const int g = (i * 4 + wave) * 64 + lane;
+        const int row = g / GPR, kq = (g % GPR) ^ ((row / RSW) % GPR);
+        xp[i] = a.X + (long)min(m0 + row, a.M - 1) * K + 4 * kq;
+        wp[i] = a.W + (long)min(n0 + row, a.N - 1) * K + 4 * kq;
+    }
+    auto issue = [&](int kt, int st) {
+        float* base = sm + st * 2 * TILE;
+#pragma unroll
+        for (int i = 0; i < NI; i++) {
+            float* la = base + (i * 4 + wave) * 64 * 4;
+            __builtin_amdgcn_global_load_lds((const void*)(xp[i] + kt * BK), (lds_void*)la, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((const void*)(wp[i] + kt * BK), (lds_void*)(la + TILE), 16,
+                                             0, 0);
+        }
+    };
+
+    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+    const int lr = lane & 31, lh = lane >> 5;
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
+    // LDS offsets (floats) of this lane's reads: group g, k quad lh * NG + g
+    int ao[2][NG], bo[2][NG];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int g = 0; g < NG; g++) {
+            const int ra = wm + i * 32 + lr, rb = wn + i * 32 + lr, kq = lh * NG + g;
+            ao[i][g] = ra * BK + 4 * (kq ^ ((ra / RSW) % GPR));
+            bo[i][g] = TILE + rb * BK + 4 * (kq ^ ((rb / RSW) % GPR));
+        }
+
+    const int nk = K / BK;
+#pragma unroll
+    for (int st = 0; st < S - 1; st++)
+        if (st < nk) issue(st, st);
+    for (int kt = 0; kt < nk; kt++) {
+        // this step's granules are in LDS once at most the later steps'
+        // loads (2 * NI instructions each) are outstanding
+        if (kt + S - 2 < nk) wait_vmcnt<2 * NI * (S - 2)>();
+        else wait_vmcnt<0>();
+        // every wavefront's granules of this step have landed, and every
+        // wavefront is done with the stage the next issue overwrites. A
+        // bare barrier: __syncthreads' fence would also wait for the later
+        // steps' loads.
+        asm volatile("s_barrier" ::: "memory");
+        if (kt + S - 1 < nk) issue(kt + S - 1, (kt + S - 1) % S);
+        const float* base = sm + (kt % S) * 2 * TILE;
+#pragma unroll
+        for (int g = 0; g < NG; g++) {
+            f32x4 av[2], bv[2];
+#pragma unroll
+            for (int i = 0; i < 2; i++) av[i] = *(const f32x4*)&base[ao[i][g]];
+#pragma unroll
+            for (int j = 0; j < 2; j++) bv[j] = *(const f32x4*)&base[bo[j][g]];
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+#pragma unroll
+                for (int i = 0; i < 2; i++)
+#pragma unroll
+                    for (int j = 0; j < 2; j++)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][e], bv[j][e],
+                                                                          acc[i][j], 0, 0, 0);
+        }
+    }
+
+    const long roff = a.row_off + (a.row_off_dev ? *a.row_off_dev : 0);
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int col = n0 + wn + j * 32 + lr;
+        if (col >= a.N) continue;
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                if (row >= a.M) continue;
+                long orow = a.seg ? (long)(row / a.seg) * a.seg_stride + row % a.seg : row;
+                orow += roff;
+                float* y = a.Y + orow * a.ldy + col;
+                *y = apply_epi<EPI>(acc[i][j][r], a.bias, col, y);
+            }
+        }
+    }
 }
 
 template <int EPI, int BK, int PAD, int OCC>
@@ -338,18 +472,23 @@ double round_fill(int tiles, int res) {
 }
 
 // Variant choice, from sweeps over the GPT-2 small / medium / XL prefill
-// products (M = 16384 / 8192 / 4096 rows): BK = 16 with rows padded by 4
-// floats (40 KB of LDS, so 4 workgroups per CU still fit in 160 KB) is
-// fastest whenever its tiles fit one round or fill its last round (2-5 %
-// above BK = 8 at 4 per CU on GPT-2 small's c_proj, fc, proj and lm_head);
-// else BK = 16 with 3 per CU when that fills its last round (e.g. 1536 or
-// 2304 tiles); else BK = 32 with 2 per CU, whose longer K steps hold up
-// best when a round is left part-empty (e.g. 1216 tiles).
+// products (M = 16384 / 8192 / 4096 rows). K a multiple of 32 (every GPT-2
+// width): k_gemm_dl with BK = 32, two stages (64 KB, 2 workgroups per CU),
+// within 1 % of the best direct-load variant on 13 of the 15 products and
+// 1-15 % above k_gemm; a multiple of 16: BK = 16, three stages (48 KB, 3
+// per CU). Otherwise k_gemm: BK = 16 with rows padded by 4 floats (40 KB, 4
+// per CU) when its tiles fit one round or fill its last round; else BK = 16
+// at 3 per CU when that fills its last round; else BK = 32 at 2 per CU,
+// whose longer K steps hold up best when a round is left part-empty.
 template <int EPI>
 hipError_t gemm_epi(const GemmArgs& a, hipStream_t s) {
     const int tiles_m = (a.M + BM - 1) / BM, tiles_n = (a.N + BN - 1) / BN;
     const int tiles = tiles_m * tiles_n, cus = 256;
-    if (tiles <= 4 * cus || round_fill(tiles, 4 * cus) >= 0.9)
+    if (a.K % 32 == 0)
+        k_gemm_dl<EPI, 32, 2, 2><<<tiles, NTHREADS, 0, s>>>(a, tiles_m, tiles_n);
+    else if (a.K % 16 == 0)
+        k_gemm_dl<EPI, 16, 3, 3><<<tiles, NTHREADS, 0, s>>>(a, tiles_m, tiles_n);
+    else if (tiles <= 4 * cus || round_fill(tiles, 4 * cus) >= 0.9)
         k_gemm<EPI, 16, 4, 4><<<tiles, NTHREADS, 0, s>>>(a, tiles_m, tiles_n);
     else if (round_fill(tiles, 3 * cus) >= 0.9)
         k_gemm<EPI, 16, 8, 3><<<tiles, NTHREADS, 0, s>>>(a, tiles_m, tiles_n);

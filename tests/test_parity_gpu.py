@@ -81,6 +81,10 @@ HS_CASES = {
     "hs32": (cngpt_amd.Config(2, 4, 128, 333, 96), [(1, 5), (2, 33), (1, 96)]),
     "hs16": (cngpt_amd.Config(1, 8, 128, 257, 70), [(2, 70)]),
     "hs128": (cngpt_amd.Config(1, 2, 256, 500, 160), [(2, 130), (1, 160)]),
+    # widths that are not multiples of 32 (GEMM K steps of 16) or of 16
+    # (register-staged tiles, zero-filled past K), more than 64 rows each
+    "hs16_c48": (cngpt_amd.Config(1, 3, 48, 257, 40), [(2, 40), (3, 33)]),
+    "hs8_c40": (cngpt_amd.Config(1, 5, 40, 101, 24), [(3, 24), (4, 19)]),
 }
 
 
