@@ -471,20 +471,26 @@ double round_fill(int tiles, int res) {
     return rounds <= 1 ? 1.0 : (double)tiles / ((double)rounds * res);
 }
 
-// Variant choice, from sweeps over the GPT-2 small / medium / XL prefill
-// products (M = 16384 / 8192 / 4096 rows). K a multiple of 32 (every GPT-2
+// Variant choice, from kernel traces of the GPT-2 small / medium / XL
+// forwards (M = 16384 / 8192 / 4096 rows). K a multiple of 32 (every GPT-2
 // width): k_gemm_dl with BK = 32, two stages (64 KB, 2 workgroups per CU),
-// within 1 % of the best direct-load variant on 13 of the 15 products and
-// 1-15 % above k_gemm; a multiple of 16: BK = 16, three stages (48 KB, 3
-// per CU). Otherwise k_gemm: BK = 16 with rows padded by 4 floats (40 KB, 4
-// per CU) when its tiles fit one round or fill its last round; else BK = 16
-// at 3 per CU when that fills its last round; else BK = 32 at 2 per CU,
-// whose longer K steps hold up best when a round is left part-empty.
+// the fastest direct-load variant on every product but one and 1-15 %
+// above k_gemm; the exception is a second round of tiles left part-empty
+// when one round at 4 per CU would hold them all (GPT-2 small's c_proj and
+// proj, 768 tiles: 187 / 611 us with BK = 16 in two 32 KB stages at 4 per
+// CU against 209 / 620 us). K a multiple of 16: BK = 16, three stages (48
+// KB, 3 per CU). Otherwise k_gemm: BK = 16 with rows padded by 4 floats (40
+// KB, 4 per CU) when its tiles fit one round or fill its last round; else
+// BK = 16 at 3 per CU when that fills its last round; else BK = 32 at 2
+// per CU, whose longer K steps hold up best when a round is left
+// part-empty.
 template <int EPI>
 hipError_t gemm_epi(const GemmArgs& a, hipStream_t s) {
     const int tiles_m = (a.M + BM - 1) / BM, tiles_n = (a.N + BN - 1) / BN;
     const int tiles = tiles_m * tiles_n, cus = 256;
-    if (a.K % 32 == 0)
+    if (a.K % 32 == 0 && tiles > 2 * cus && tiles <= 4 * cus && round_fill(tiles, 2 * cus) < 0.9)
+        k_gemm_dl<EPI, 16, 2, 4><<<tiles, NTHREADS, 0, s>>>(a, tiles_m, tiles_n);
+    else if (a.K % 32 == 0)
         k_gemm_dl<EPI, 32, 2, 2><<<tiles, NTHREADS, 0, s>>>(a, tiles_m, tiles_n);
     else if (a.K % 16 == 0)
         k_gemm_dl<EPI, 16, 3, 3><<<tiles, NTHREADS, 0, s>>>(a, tiles_m, tiles_n);

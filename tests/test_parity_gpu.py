@@ -85,6 +85,9 @@ HS_CASES = {
     # (register-staged tiles, zero-filled past K), more than 64 rows each
     "hs16_c48": (cngpt_amd.Config(1, 3, 48, 257, 40), [(2, 40), (3, 33)]),
     "hs8_c40": (cngpt_amd.Config(1, 5, 40, 101, 24), [(3, 24), (4, 19)]),
+    # an all-position lm_head of 2 x 297 tiles: more than one round at 2
+    # workgroups per CU, all in one at 4 (GEMM K steps of 16, two stages)
+    "v38000": (cngpt_amd.Config(1, 4, 256, 38000, 64), [(4, 64)]),
 }
 
 
