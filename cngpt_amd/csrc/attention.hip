@@ -14,7 +14,10 @@
 // row sum need one cross-half shuffle, and the probabilities feed the
 // O^T += V^T P^T product directly from the accumulator registers (the key
 // order of the S^T output layout is used as the k order of that product).
-// The softmax is the online (running max / running sum) form.
+// The softmax is the online (running max / running sum) form, in base 2:
+// Q is pre-multiplied by scale * log2(e), so a probability is one hardware
+// exp2 of (score - running max); the causal mask is applied only on the
+// tiles that cross the diagonal.
 //
 // The one-query form (the last-position pass, fast.c:287-297, and a decode
 // step) is k_attn_dec in decode.hip.
@@ -55,10 +58,11 @@ __global__ void __launch_bounds__(256, 2)
     float qreg[HALF];
     {
         const float* qp = base + (long)min(qi, T - 1) * C3 + h * HS + lh * HALF;
+        const float qs = scale * 1.4426950408889634f;  // scores in units of log2
 #pragma unroll
         for (int s = 0; s < HALF; s += 4) {
             f32x4 v = *(const f32x4*)(qp + s);
-            qreg[s] = v.x; qreg[s + 1] = v.y; qreg[s + 2] = v.z; qreg[s + 3] = v.w;
+            qreg[s] = v.x * qs; qreg[s + 1] = v.y * qs; qreg[s + 2] = v.z * qs; qreg[s + 3] = v.w * qs;
         }
     }
 
@@ -118,27 +122,32 @@ __global__ void __launch_bounds__(256, 2)
                     s[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.w, qreg[d + 3], s[kb], 0, 0, 0);
                 }
             }
-            // s[kb][r] = score of key kt*64 + 32kb + 8(r/4) + 4lh + r%4 for query qi.
+            // s[kb][r] = score (log2 units) of key kt*64 + 32kb + 8(r/4) +
+            // 4lh + r%4 for query qi; keys after qi exist only in a tile that
+            // reaches past this wavefront's first query
+            if (kt * KT + KT - 1 > q0) {
+#pragma unroll
+                for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const int key = kt * KT + kb * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                        s[kb][r] = (key > qi) ? -INFINITY : s[kb][r];
+                    }
+            }
             float mt = -INFINITY;
 #pragma unroll
             for (int kb = 0; kb < 2; kb++)
 #pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    int key = kt * KT + kb * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-                    float v = s[kb][r] * scale;
-                    v = (key > qi) ? -INFINITY : v;
-                    s[kb][r] = v;
-                    mt = fmaxf(mt, v);
-                }
+                for (int r = 0; r < 16; r++) mt = fmaxf(mt, s[kb][r]);
             mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
             const float m_new = fmaxf(m_run, mt);
-            const float alpha = expf(m_run - m_new);
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
             float ps = 0.f;
 #pragma unroll
             for (int kb = 0; kb < 2; kb++)
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
-                    float p = expf(s[kb][r] - m_new);
+                    float p = __builtin_amdgcn_exp2f(s[kb][r] - m_new);
                     s[kb][r] = p;
                     ps += p;
                 }
