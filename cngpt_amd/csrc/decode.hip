@@ -51,16 +51,29 @@ __device__ void merge_rows(const MergeArgs& g, int M, f32x4* xs) {
         const float* pb = g.part + (long)(r * g.H + h) * g.stride * rs;
         float mx = -INFINITY, L = 0.f;
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        // splits in batches of MB, each batch's loads in flight together
+        // (clamped indices; a load under the s < ns branch would be waited
+        // for inside it), merged in split order
+        constexpr int MB = 4;
+        for (int s0 = 0; s0 < ns; s0 += MB) {
+            float ms[MB], ls[MB];
+            f32x4 os[MB];
 #pragma unroll
-        for (int s = 0; s < MAXS; s++) {
-            if (s < ns) {
-                const float ms = pb[s * rs], ls = pb[s * rs + 1];
-                const f32x4 os = *(const f32x4*)(pb + s * rs + 4 + 4 * d4);
-                const float mn = fmaxf(mx, ms);
-                const float a = expf(mx - mn), b = expf(ms - mn);
-                acc = acc * a + os * b;
-                L = L * a + ls * b;
-                mx = mn;
+            for (int j = 0; j < MB; j++) {
+                const float* ps = pb + min(s0 + j, ns - 1) * rs;
+                ms[j] = ps[0];
+                ls[j] = ps[1];
+                os[j] = *(const f32x4*)(ps + 4 + 4 * d4);
+            }
+#pragma unroll
+            for (int j = 0; j < MB; j++) {
+                if (s0 + j < ns) {
+                    const float mn = fmaxf(mx, ms[j]);
+                    const float a = expf(mx - mn), b = expf(ms[j] - mn);
+                    acc = acc * a + os[j] * b;
+                    L = L * a + ls[j] * b;
+                    mx = mn;
+                }
             }
         }
         xs[e] = acc * (1.0f / L);

@@ -433,8 +433,16 @@ __global__ void __launch_bounds__(256) k_stream_reduce(GemmArgs a, int KS) {
     const long i = (long)blockIdx.x * 256 + threadIdx.x;
     const long MN = (long)a.M * a.N;
     if (i >= MN) return;
+    // partials in batches of 8 loads in flight, summed in split order
     float v = 0.f;
-    for (int q = 0; q < KS; q++) v += a.part[q * MN + i];
+    for (int q0 = 0; q0 < KS; q0 += 8) {
+        float p[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) p[j] = a.part[min(q0 + j, KS - 1) * MN + i];
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            if (q0 + j < KS) v += p[j];
+    }
     const long roff = a.row_off + (a.row_off_dev ? *a.row_off_dev : 0);
     store_out<EPI>(a, roff, (int)(i / a.N), (int)(i % a.N), v);
 }
