@@ -39,7 +39,9 @@ __device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
 // view), C = H * hs. Split s of (row r, head h) holds m_s, l_s and the
 // unnormalised o_s[hs] at part + ((r*H + h) * stride + s) * (hs + 4):
 //   M = max m_s,  L = sum exp(m_s - M) l_s,  out = sum exp(m_s - M) o_s / L,
-// accumulated online so every split's loads are issued together.
+// accumulated online, the splits read in batches of MB whose loads are in
+// flight together.
+template <int MB>
 __device__ void merge_rows(const MergeArgs& g, int M, f32x4* xs) {
     const int t = g.pos_dev ? *g.pos_dev : g.q_pos;
     const int ns = (t + g.kps) / g.kps;  // splits over keys 0..t
@@ -51,10 +53,8 @@ __device__ void merge_rows(const MergeArgs& g, int M, f32x4* xs) {
         const float* pb = g.part + (long)(r * g.H + h) * g.stride * rs;
         float mx = -INFINITY, L = 0.f;
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        // splits in batches of MB, each batch's loads in flight together
-        // (clamped indices; a load under the s < ns branch would be waited
-        // for inside it), merged in split order
-        constexpr int MB = 4;
+        // clamped indices: a load under the s < ns branch would be waited
+        // for inside it; merged in split order
         for (int s0 = 0; s0 < ns; s0 += MB) {
             float ms[MB], ls[MB];
             f32x4 os[MB];
@@ -198,7 +198,7 @@ __global__ void __launch_bounds__(256) k_dgemv(DecGemvArgs a) {
         }
         __syncthreads();
     } else if (SRC == SRC_MERGE) {
-        merge_rows(a.merge, M, xs);
+        merge_rows<4>(a.merge, M, xs);
     }
 
     // 3. Dot products over this wavefront's K range.
@@ -376,7 +376,7 @@ __global__ void __launch_bounds__(256) k_attn_merge(MergeArgs g, float* __restri
     // one row per workgroup: offset the partials to row blockIdx.x
     MergeArgs gr = g;
     gr.part = g.part + (long)blockIdx.x * g.H * g.stride * (g.hs + 4);
-    merge_rows(gr, 1, xs);
+    merge_rows<MAXS>(gr, 1, xs);
     const int C4 = g.H * g.hs / 4;
     f32x4* o = (f32x4*)(out + (long)blockIdx.x * ldo);
     for (int c = threadIdx.x; c < C4; c += blockDim.x) o[c] = xs[c];
