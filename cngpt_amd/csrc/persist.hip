@@ -188,6 +188,8 @@ struct Smem {
     float so[SK_CAND];
     int soi[SK_CAND];
     float raw[256 * SK_SLOT];     // the candidate words as fetched
+    float kv[PW][32][64];         // the next layer's cached keys of each compute
+                                  // wavefront (its kq, then vr), staged in E
     int n_c, n_sv, over, stok;
     float sL, sc, sns;
 };
@@ -470,22 +472,44 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
             ns = min(ns, min(G / H, PMAXS));
             const int kps = (nk + ns - 1) / ns;
             const int kpw = (kps + PW - 1) / PW;
-            const bool has_item = blockIdx.x < H * ns;
-            const int ih = blockIdx.x / ns, isp = blockIdx.x - (blockIdx.x / ns) * ns;
+            // The (head, split) items go to the workgroups after the c_proj /
+            // proj column owners when they fit there ("early"): those
+            // workgroups have no column work in C and E, so in E they load
+            // the next layer's cached keys and park them in LDS, and their
+            // QKV publish in A is not held up behind those loads.
+            const int owners = (C + PW - 1) / PW;
+            const bool early = owners + H * ns <= G;
+            const int item = (int)blockIdx.x - (early ? owners : 0);
+            const bool has_item = item >= 0 && item < H * ns;
+            const int ih = max(item, 0) / ns, isp = max(item, 0) - ih * ns;
             const int k0 = isp * kps, k1 = min(k0 + kps, nk);
             const int kw0 = k0 + wave * kpw, kw1 = min(kw0 + kpw, k1);
-            // next weights (c_proj) and this workgroup's cached keys (< t)
-            load_cols<UPW, U>(wb, P.proj_w, C, C, cw, CW, lane);
-            if (!ctrl && has_item) {
+            // this workgroup's cached keys (< t) of layer `ll`, loaded by its
+            // compute wavefronts
+            auto load_keys = [&](int ll) {
+                const float* kv = a.cache + (long)ll * a.cap * C3;
                 const int kk = kw0 + (lane >> 2), dq = lane & 3;
                 const int kc = min(kk, max(t - 1, 0));
-                const float* kr = kvl + (long)kc * C3 + C + ih * 64 + dq * 16;
+                const float* kr = kv + (long)kc * C3 + C + ih * 64 + dq * 16;
 #pragma unroll
                 for (int i = 0; i < 4; i++) kq[i] = ldg4(kr + 4 * i);
 #pragma unroll
                 for (int jj = 0; jj < KPW; jj++) {
                     const int kj = min(kw0 + jj, max(t - 1, 0));
-                    vr[jj] = ldg(kvl + (long)kj * C3 + 2 * C + ih * 64 + lane);
+                    vr[jj] = ldg(kv + (long)kj * C3 + 2 * C + ih * 64 + lane);
+                }
+            };
+            if (!ctrl && has_item) {
+                if (early && l > 0) {
+                    // staged in the previous layer's E by this wavefront
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+#pragma unroll
+                        for (int c = 0; c < 4; c++) kq[i][c] = sm.kv[wave][4 * i + c][lane];
+#pragma unroll
+                    for (int jj = 0; jj < KPW; jj++) vr[jj] = sm.kv[wave][16 + jj][lane];
+                } else {
+                    load_keys(l);
                 }
             } else {
 #pragma unroll
@@ -493,6 +517,9 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
 #pragma unroll
                 for (int jj = 0; jj < KPW; jj++) vr[jj] = 0.f;
             }
+            // next weights (c_proj), behind the keys: loads return in order,
+            // and the attention needs only the keys
+            load_cols<UPW, U>(wb, P.proj_w, C, C, cw, CW, lane);
             ln_to_act(xv, lw, lb, C, actf, sm.wred, tid, wave, lane);
             if (!ctrl) {
                 float acc[UPW];
@@ -740,6 +767,15 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
             } else if (l + 1 < L) {
                 load_cols<UPW, U>(wa, PN.attn_w, C3, C, cw, CW, lane);
                 ln_params(PN.ln1_w, PN.ln1_b);
+                if (early && has_item && !ctrl) {
+                    load_keys(l + 1);
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+#pragma unroll
+                        for (int c = 0; c < 4; c++) sm.kv[wave][4 * i + c][lane] = kq[i][c];
+#pragma unroll
+                    for (int jj = 0; jj < KPW; jj++) sm.kv[wave][16 + jj][lane] = vr[jj];
+                }
             } else {
                 load_cols<UPW, U>(wa, a.wte, V, C, cw, CW, lane);
                 ln_params(a.lnf_w, a.lnf_b);
