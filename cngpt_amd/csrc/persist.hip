@@ -172,6 +172,7 @@ __device__ __forceinline__ unsigned slots_below(int n, int tt) {
 template <int U>
 struct Smem {
     f32x4 act[256 * U];           // activation vector (up to 1024 * U floats)
+    float xraw[256 * U];          // x as fetched by the control wavefront
     float red[UPW][PW];           // per-wavefront column sums
     float wred[PW + 1];           // block reductions
     float attn[PW][68];           // per-wavefront attention partials: m, l, -, -, o[64]
@@ -401,17 +402,33 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
             lb[i] = ldg(gb + e);
         }
     };
-    // xv = x (tag `tag`), element tid + PT * i
+    // xv = x (tag `tag`), element tid + PT * i. The control wavefront polls
+    // (it has no weight loads in flight for the polls to queue behind) and
+    // passes x on through LDS; false (in every thread) when a wait gave up.
     auto fetch_x = [&](unsigned tag) -> bool {
-        const int tt = opaque_v(tid);
-        int idx[LNE];
-        bool need[LNE];
+        bool ok = true;
+        if (ctrl) {
+            constexpr int NX = 4 * U;  // C <= 256 * U words, 64 per round
+            const int ln = opaque_v(lane);
+            int idx[NX];
+            bool need[NX];
+            float v[NX];
 #pragma unroll
-        for (int i = 0; i < LNE; i++) {
-            idx[i] = min(tt + PT * i, C - 1);
-            need[i] = tt + PT * i < C;
+            for (int k = 0; k < NX; k++) {
+                idx[k] = min(ln + 64 * k, C - 1);
+                need[k] = ln + 64 * k < C;
+            }
+            const unsigned en = (1u << ((C + 63) / 64)) - 1u;
+            ok = fetch<NX>(rx, idx, need, tag, v, abortw, amark, en);
+#pragma unroll
+            for (int k = 0; k < NX; k++)
+                if (need[k]) sm.xraw[ln + 64 * k] = v[k];
         }
-        return fetch<LNE>(rx, idx, need, tag, xv, abortw, amark, slots_below(C, tt));
+        if (!settle(ok)) return false;
+        const int tt = opaque_v(tid);
+#pragma unroll
+        for (int i = 0; i < LNE; i++) xv[i] = sm.xraw[min(tt + PT * i, C - 1)];
+        return true;
     };
     // Bias of this lane's output column in the next phase (control lanes;
     // the others load b[0]). Issued before the current epilogue's stores.
@@ -423,6 +440,7 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
     const LayerW* layers = a.layers;
     load_cols<UPW, U>(wa, layers[0].attn_w, C3, C, cw0, CW, lane);
     ln_params(layers[0].ln1_w, layers[0].ln1_b);
+    load_cols<UPW, U>(wb, layers[0].proj_w, C, C, cw0, CW, lane);
     bo = slot_bias(layers[0].attn_b, C3);
 
     for (int step = 0; step < a.n_steps; step++, t++) {
@@ -463,7 +481,7 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
                            TE = TA + 4, TXIN = TA - 1;
 
             // ---------------- phase A: LayerNorm 1 + QKV into row t
-            if (l > 0 && !settle(fetch_x(TXIN))) return;
+            if (l > 0 && !fetch_x(TXIN)) return;
             // attention split layout for keys 0..t
             const int nk = t + 1;
             // as few splits as the workgroup's PW * KPW keys allow (fewer
@@ -517,9 +535,6 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
 #pragma unroll
                 for (int jj = 0; jj < KPW; jj++) vr[jj] = 0.f;
             }
-            // next weights (c_proj), behind the keys: loads return in order,
-            // and the attention needs only the keys
-            load_cols<UPW, U>(wb, P.proj_w, C, C, cw, CW, lane);
             ln_to_act(xv, lw, lb, C, actf, sm.wred, tid, wave, lane);
             if (!ctrl) {
                 float acc[UPW];
@@ -542,6 +557,14 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
                 }
                 bo = bn;
             }
+            // Weight loads are issued after the phase's publish (the barrier
+            // puts them behind its stores) into the buffer the phase has just
+            // freed: queued ahead of the stores they delayed the publish, and
+            // a wait the compiler places for them inside the phase delayed
+            // its products. wa: fc (D), with LayerNorm 2's gains.
+            __syncthreads();
+            load_cols<UPW, U>(wa, P.fc_w, C4, C, cw, CW, lane);
+            ln_params(P.ln2_w, P.ln2_b);
 
             // ---------------- phase B: attention, one (head, key split) per workgroup
             if (has_item) {
@@ -665,8 +688,6 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
                     }
                 }
                 if (!settle(ok)) return;
-                load_cols<UPW, U>(wa, P.fc_w, C4, C, cw, CW, lane);
-                ln_params(P.ln2_w, P.ln2_b);
                 for (int e = tid; e < C; e += PT) {
                     const int h = e >> 6;
                     float mx = -INFINITY, Ls = 0.f, acc = 0.f;
@@ -690,16 +711,14 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
                 }
                 __syncthreads();
                 if (ctrl && c >= 0) put_all(tx + c, tl.xs, (xo + sm.red[j][q]) + bo, TC);
-            } else {
-                load_cols<UPW, U>(wa, P.fc_w, C4, C, cw, CW, lane);
-                ln_params(P.ln2_w, P.ln2_b);
+                __syncthreads();
             }
+            // wb: proj (E), one column of depth 4C per wavefront
+            load_cols<1, 4 * U>(wb, P.mlp_w, C, C4, cw, CW, lane);
             bo = slot_bias(P.fc_b, C4);
 
             // ---------------- phase D: LayerNorm 2, fc + b, GELU into hid
-            if (!settle(fetch_x(TC))) return;
-            // proj: one column of depth 4C per wavefront
-            load_cols<1, 4 * U>(wb, P.mlp_w, C, C4, cw, CW, lane);
+            if (!fetch_x(TC)) return;
             ln_to_act(xv, lw, lb, C, actf, sm.wred, tid, wave, lane);
             if (!ctrl) {
                 float acc[UPW];
@@ -717,6 +736,17 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
                     if (c >= 0) put_all(th + c, tl.hs, gelu_tanh(sm.red[j][q] + bo), TD);
                 }
                 bo = bn;
+            }
+            // wa: the next layer's QKV with LayerNorm 1's gains, or the
+            // first UPW rounds of lm_head columns (tied wte) with the final
+            // LayerNorm's
+            __syncthreads();
+            if (l + 1 < L) {
+                load_cols<UPW, U>(wa, PN.attn_w, C3, C, cw, CW, lane);
+                ln_params(PN.ln1_w, PN.ln1_b);
+            } else {
+                load_cols<UPW, U>(wa, a.wte, V, C, cw, CW, lane);
+                ln_params(a.lnf_w, a.lnf_b);
             }
 
             // ---------------- phase E: proj, x += . + b (column owners only)
@@ -748,13 +778,6 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
                     if (ctrl) xo = hv[NH];
                 }
                 if (!settle(ok)) return;
-                if (l + 1 < L) {
-                    load_cols<UPW, U>(wa, PN.attn_w, C3, C, cw, CW, lane);
-                    ln_params(PN.ln1_w, PN.ln1_b);
-                } else {  // the first UPW rounds of lm_head columns (tied wte)
-                    load_cols<UPW, U>(wa, a.wte, V, C, cw, CW, lane);
-                    ln_params(a.lnf_w, a.lnf_b);
-                }
                 if (!ctrl) {
                     float acc[UPW];
                     col_dots<1, 4 * U>(acc, wb, sm.act, C, C4, cw, CW, lane);
@@ -764,9 +787,8 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
                 }
                 __syncthreads();
                 if (ctrl && c >= 0) put_all(tx + c, tl.xs, (xo + sm.red[j][q]) + bo, TE);
+                __syncthreads();
             } else if (l + 1 < L) {
-                load_cols<UPW, U>(wa, PN.attn_w, C3, C, cw, CW, lane);
-                ln_params(PN.ln1_w, PN.ln1_b);
                 if (early && has_item && !ctrl) {
                     load_keys(l + 1);
 #pragma unroll
@@ -776,16 +798,15 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
 #pragma unroll
                     for (int jj = 0; jj < KPW; jj++) sm.kv[wave][16 + jj][lane] = vr[jj];
                 }
-            } else {
-                load_cols<UPW, U>(wa, a.wte, V, C, cw, CW, lane);
-                ln_params(a.lnf_w, a.lnf_b);
             }
+            // wb: the next c_proj (layer 0's for the next step after the last)
+            load_cols<UPW, U>(wb, layers[l + 1 < L ? l + 1 : 0].proj_w, C, C, cw, CW, lane);
             bo = slot_bias(PN.attn_b, C3);
         }
 
         // ---------------- phase F: final LayerNorm, lm_head (tied wte), argmax partials
         const unsigned TF = sbase + PHASES * L + 1;
-        if (!settle(fetch_x(TF - 1))) return;
+        if (!fetch_x(TF - 1)) return;
         ln_to_act(xv, lw, lb, C, actf, sm.wred, tid, wave, lane1);
         if (!ctrl) {
             const int ln = opaque_v(lane1);
