@@ -58,7 +58,8 @@ namespace {
 constexpr int PW = 7;                  // compute wavefronts per workgroup
 constexpr int PT = (PW + 1) * 64;      // + the control wavefront: 2 per SIMD
 constexpr int PHASES = 5;              // phases per layer
-constexpr int UPW = 4;                 // output columns per wavefront per phase
+constexpr int UPW = 4;                 // lm_head columns per wavefront in flight
+constexpr int NJQ = 2;                 // QKV / fc columns per wavefront (4C <= NJQ * 7G)
 constexpr int KPW = 16;                // attention keys per wavefront
 constexpr int LNE = 4;                 // LayerNorm elements per thread (C <= 4 * PT)
 constexpr int PMAXS = 16;              // attention splits per head
@@ -267,11 +268,11 @@ __device__ __forceinline__ void ln_to_act(const float (&v)[LNE], const float (&l
 
 // Columns of a product Y[N] = W[N, K] . act: column cw + CW * j (j < NJ)
 // belongs to compute wavefront cw; its lane l holds float4 i * 64 + l
-// (i < NI) of the column's weight row in w[j * NI + i].
-template <int NJ, int NI, int NW>
+// (i < NI) of the column's weight row in w[OFF + j * NI + i].
+template <int NJ, int NI, int OFF = 0, int NW>
 __device__ __forceinline__ void load_cols(f32x4 (&w)[NW], const float* __restrict__ W, int N,
                                           int K, int cw, int CW, int lane) {
-    static_assert(NJ * NI <= NW, "register budget");
+    static_assert(OFF + NJ * NI <= NW, "register budget");
     cw = opaque_s(cw);
     lane = opaque_v(lane);
     const int K4 = K >> 2;
@@ -281,11 +282,12 @@ __device__ __forceinline__ void load_cols(f32x4 (&w)[NW], const float* __restric
         if (c < N) {
             const float* row = W + (long)c * K;
 #pragma unroll
-            for (int i = 0; i < NI; i++) w[j * NI + i] = ldg4(row + 4 * min(i * 64 + lane, K4 - 1));
+            for (int i = 0; i < NI; i++)
+                w[OFF + j * NI + i] = ldg4(row + 4 * min(i * 64 + lane, K4 - 1));
         } else {
             // written on every path, so the previous phase's values are dead
 #pragma unroll
-            for (int i = 0; i < NI; i++) w[j * NI + i] = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int i = 0; i < NI; i++) w[OFF + j * NI + i] = f32x4{0.f, 0.f, 0.f, 0.f};
         }
     }
 }
@@ -377,12 +379,16 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
     int tok = *a.tok;
     constexpr bool samp = SAMP;  // the greedy instantiation carries no sampling code
     const float tdiv = a.temp > 0.0f ? a.temp : 1.0f;
-    // Two weight buffers: the weights of the next phase that has any are
-    // loaded at the start of the current one (as soon as its input has
-    // arrived), so they are in registers before the workgroup reads the
-    // next input; loads return in order, and a read queued behind a
-    // phase's worth of weight loads would wait for all of them.
-    // A and D use wa, C and E use wb, the lm_head streams through wa.
+    // Two weight buffers of UPW * U float4 per lane, NJQ * U of them the
+    // QKV or fc columns, U the c_proj column, 4U the proj column:
+    //   wa[0, 2U): QKV (A), then fc (D)      wa[2U, 4U): proj, first half (E)
+    //   wb[0, U):  c_proj (C)                wb[U, 3U):  proj, second half (E)
+    // Loads are issued after a phase's publish into the slots it freed:
+    // after A fc and all of proj (the c_proj / proj column owners have no
+    // work in B, which leaves the longest time for their largest loads),
+    // after D the next QKV (the lm_head's first two rounds after the last
+    // layer), after E the next c_proj (and the lm_head's rounds 2 and 3).
+    // The lm_head streams UPW rounds through all of wa.
     f32x4 wa[NW], wb[NW];
     f32x4 kq[4];             // attention prefetch: K, 16 dims of one key
     float vr[KPW];           // V of 16 keys, one dim
@@ -438,9 +444,9 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
     };
 
     const LayerW* layers = a.layers;
-    load_cols<UPW, U>(wa, layers[0].attn_w, C3, C, cw0, CW, lane);
+    load_cols<NJQ, U>(wa, layers[0].attn_w, C3, C, cw0, CW, lane);
     ln_params(layers[0].ln1_w, layers[0].ln1_b);
-    load_cols<UPW, U>(wb, layers[0].proj_w, C, C, cw0, CW, lane);
+    load_cols<1, U>(wb, layers[0].proj_w, C, C, cw0, CW, lane);
     bo = slot_bias(layers[0].attn_b, C3);
 
     for (int step = 0; step < a.n_steps; step++, t++) {
@@ -538,7 +544,7 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
             ln_to_act(xv, lw, lb, C, actf, sm.wred, tid, wave, lane);
             if (!ctrl) {
                 float acc[UPW];
-                col_dots<UPW, U>(acc, wa, sm.act, C3, C, cw, CW, lane);
+                col_dots<NJQ, U>(acc, wa, sm.act, C3, C, cw, CW, lane);
                 if (lane == 0)
 #pragma unroll
                     for (int j = 0; j < UPW; j++) sm.red[j][wave] = acc[j];
@@ -558,13 +564,25 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
                 bo = bn;
             }
             // Weight loads are issued after the phase's publish (the barrier
-            // puts them behind its stores) into the buffer the phase has just
-            // freed: queued ahead of the stores they delayed the publish, and
-            // a wait the compiler places for them inside the phase delayed
-            // its products. wa: fc (D), with LayerNorm 2's gains.
+            // puts them behind its stores): queued ahead of the stores they
+            // delayed the publish, and a wait the compiler places for them
+            // inside the phase delayed its products. fc with LayerNorm 2's
+            // gains, and this wavefront's proj column (depth 4C) in wa[2U,
+            // 4U) and wb[U, 3U).
             __syncthreads();
-            load_cols<UPW, U>(wa, P.fc_w, C4, C, cw, CW, lane);
+            load_cols<NJQ, U>(wa, P.fc_w, C4, C, cw, CW, lane);
             ln_params(P.ln2_w, P.ln2_b);
+            {
+                const int c = opaque_s(cw), ln = opaque_v(lane);
+                const float* row = P.mlp_w + (long)min(c, C - 1) * C4;
+#pragma unroll
+                for (int i = 0; i < 4 * U; i++) {
+                    const f32x4 v = c < C ? ldg4(row + 4 * min(i * 64 + ln, C - 1))
+                                          : f32x4{0.f, 0.f, 0.f, 0.f};
+                    if (i < 2 * U) wa[2 * U + i] = v;
+                    else wb[i - U] = v;
+                }
+            }
 
             // ---------------- phase B: attention, one (head, key split) per workgroup
             if (has_item) {
@@ -704,17 +722,14 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
                 __syncthreads();
                 if (!ctrl) {
                     float acc[UPW];
-                    col_dots<UPW, U>(acc, wb, sm.act, C, C, cw, CW, lane);
+                    col_dots<1, U>(acc, wb, sm.act, C, C, cw, CW, lane);
                     if (lane == 0)
 #pragma unroll
                         for (int jj = 0; jj < UPW; jj++) sm.red[jj][wave] = acc[jj];
                 }
                 __syncthreads();
                 if (ctrl && c >= 0) put_all(tx + c, tl.xs, (xo + sm.red[j][q]) + bo, TC);
-                __syncthreads();
             }
-            // wb: proj (E), one column of depth 4C per wavefront
-            load_cols<1, 4 * U>(wb, P.mlp_w, C, C4, cw, CW, lane);
             bo = slot_bias(P.fc_b, C4);
 
             // ---------------- phase D: LayerNorm 2, fc + b, GELU into hid
@@ -722,7 +737,7 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
             ln_to_act(xv, lw, lb, C, actf, sm.wred, tid, wave, lane);
             if (!ctrl) {
                 float acc[UPW];
-                col_dots<UPW, U>(acc, wa, sm.act, C4, C, cw, CW, lane);
+                col_dots<NJQ, U>(acc, wa, sm.act, C4, C, cw, CW, lane);
                 if (lane == 0)
 #pragma unroll
                     for (int j = 0; j < UPW; j++) sm.red[j][wave] = acc[j];
@@ -737,15 +752,15 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
                 }
                 bo = bn;
             }
-            // wa: the next layer's QKV with LayerNorm 1's gains, or the
-            // first UPW rounds of lm_head columns (tied wte) with the final
-            // LayerNorm's
+            // wa[0, 2U): the next layer's QKV with LayerNorm 1's gains, or
+            // the first two rounds of lm_head columns (tied wte) with the
+            // final LayerNorm's
             __syncthreads();
             if (l + 1 < L) {
-                load_cols<UPW, U>(wa, PN.attn_w, C3, C, cw, CW, lane);
+                load_cols<NJQ, U>(wa, PN.attn_w, C3, C, cw, CW, lane);
                 ln_params(PN.ln1_w, PN.ln1_b);
             } else {
-                load_cols<UPW, U>(wa, a.wte, V, C, cw, CW, lane);
+                load_cols<2, U>(wa, a.wte, V, C, cw, CW, lane);
                 ln_params(a.lnf_w, a.lnf_b);
             }
 
@@ -779,8 +794,18 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
                 }
                 if (!settle(ok)) return;
                 if (!ctrl) {
-                    float acc[UPW];
-                    col_dots<1, 4 * U>(acc, wb, sm.act, C, C4, cw, CW, lane);
+                    // proj: float4 i * 64 + lane of the column, i < 2U in
+                    // wa[2U + i], then i < 4U in wb[U + i - 2U]
+                    const int ln = opaque_v(lane);
+                    float acc[UPW] = {0.f, 0.f, 0.f, 0.f};
+                    if (cw < C) {
+#pragma unroll
+                        for (int i = 0; i < 4 * U; i++) {
+                            const int f = i * 64 + ln;
+                            if (f < C) acc[0] += dot4(i < 2 * U ? wa[2 * U + i] : wb[i - U], sm.act[f]);
+                        }
+                    }
+                    acc[0] = wave_sum_dpp(acc[0]);
                     if (lane == 0)
 #pragma unroll
                         for (int jj = 0; jj < UPW; jj++) sm.red[jj][wave] = acc[jj];
@@ -799,8 +824,10 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
                     for (int jj = 0; jj < KPW; jj++) sm.kv[wave][16 + jj][lane] = vr[jj];
                 }
             }
-            // wb: the next c_proj (layer 0's for the next step after the last)
-            load_cols<UPW, U>(wb, layers[l + 1 < L ? l + 1 : 0].proj_w, C, C, cw, CW, lane);
+            // wb[0, U): the next c_proj (layer 0's for the next step after
+            // the last layer, then also the lm_head's rounds 2 and 3)
+            load_cols<1, U>(wb, layers[l + 1 < L ? l + 1 : 0].proj_w, C, C, cw, CW, lane);
+            if (l + 1 == L) load_cols<2, U, 2 * U>(wa, a.wte, V, C, cw + 2 * CW, CW, lane);
             bo = slot_bias(PN.attn_b, C3);
         }
 
@@ -884,7 +911,7 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
             put_all(tam + 2 * blockIdx.x + 1, tl.as, __int_as_float(bi), TF);
         }
         if (step + 1 < a.n_steps) {
-            load_cols<UPW, U>(wa, layers[0].attn_w, C3, C, cw, CW, lane1);
+            load_cols<NJQ, U>(wa, layers[0].attn_w, C3, C, cw, CW, lane1);
             ln_params(layers[0].ln1_w, layers[0].ln1_b);
         }
 
@@ -1128,8 +1155,8 @@ bool persist_supported(int C, int H, int V, int cap, int G) {
     if (G < 1 || G > PT || C % 64 || C != 64 * H || C > 256 * PMAXU || H > 32 || C > LNE * PT)
         return false;
     const long CW = (long)PW * G;
-    // columns per wavefront: QKV and fc at most UPW, proj one
-    if (4L * C > UPW * CW || C > CW || V < 1) return false;
+    // columns per wavefront: QKV and fc at most NJQ, c_proj and proj one
+    if (4L * C > NJQ * CW || C > CW || V < 1) return false;
     // attention: H * splits workgroups, at most PW * KPW keys per split
     const int ns = std::min(G / H, PMAXS);
     if (ns < 1 || (long)ns * PW * KPW < cap) return false;
