@@ -60,8 +60,7 @@ __device__ __forceinline__ float wave_max_dpp(float v) {
     return fmaxf(fmaxf(lane_f(v, 0), lane_f(v, 16)), fmaxf(lane_f(v, 32), lane_f(v, 48)));
 }
 
-// GELU, tanh form (the formula of the reference's ops.h:56-58), with the
-// device library's tanhf.
+// GELU, tanh form (the formula of the reference's ops.h:56-58):
 // 0.5 x (1 + tanh(u)), u = sqrt(2/pi) (x + 0.044715 x^3), evaluated as
 // x / (1 + exp(-2u)) (1 + tanh(u) = 2 / (1 + exp(-2u))): one hardware exp
 // and one reciprocal instead of a library tanh, a few ulp from it. Large

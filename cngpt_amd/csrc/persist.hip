@@ -61,7 +61,6 @@ constexpr int PHASES = 5;              // phases per layer
 constexpr int UPW = 4;                 // lm_head columns per wavefront in flight
 constexpr int NJQ = 2;                 // QKV / fc columns per wavefront (4C <= NJQ * 7G)
 constexpr int KPW = 16;                // attention keys per wavefront
-constexpr int LNE = 4;                 // LayerNorm elements per thread (C <= 4 * PT)
 constexpr int PMAXS = 16;              // attention splits per head
 constexpr long SPIN_LIMIT = 1L << 20;  // polls of one value before giving up
 // Widths up to 256 * PMAXU channels (GPT-2 small): the weights a lane holds
@@ -173,7 +172,7 @@ __device__ __forceinline__ unsigned slots_below(int n, int tt) {
 template <int U>
 struct Smem {
     f32x4 act[256 * U];           // activation vector (up to 1024 * U floats)
-    float xraw[256 * U];          // x as fetched by the control wavefront
+    float lnw[256 * U], lnb[256 * U];  // gains and biases of the next LayerNorm
     float red[UPW][PW];           // per-wavefront column sums
     float wred[PW + 1];           // block reductions
     float attn[PW][68];           // per-wavefront attention partials: m, l, -, -, o[64]
@@ -241,29 +240,32 @@ __device__ __forceinline__ float block_max(float v, float* wred, int wave, int l
     return m;
 }
 
-// LayerNorm (reference ops.c:191-248) of v (element tid + PT * i) into act.
-__device__ __forceinline__ void ln_to_act(const float (&v)[LNE], const float (&lw)[LNE],
-                                          const float (&lb)[LNE], int C, float* act, float* wred,
-                                          int tid, int wave, int lane) {
+typedef __attribute__((address_space(3))) void lds_void;
+
+// LayerNorm (reference ops.c:191-248) by one wavefront: x[lane + 64 k] in
+// v[k], gains and biases from LDS, result into act. Two passes (mean, then
+// the mean square deviation), each one wavefront reduction.
+template <int NX>
+__device__ __forceinline__ void ln_wave(const float (&v)[NX], int C, int ln, const float* gw,
+                                        const float* gb, float* act) {
     float s = 0.f;
 #pragma unroll
-    for (int i = 0; i < LNE; i++)
-        if (tid + PT * i < C) s += v[i];
-    const float mean = block_sum(s, wred, wave, lane) / (float)C;
+    for (int k = 0; k < NX; k++)
+        if (ln + 64 * k < C) s += v[k];
+    const float mean = wave_sum_dpp(s) / (float)C;
     float q = 0.f;
 #pragma unroll
-    for (int i = 0; i < LNE; i++)
-        if (tid + PT * i < C) {
-            const float d = v[i] - mean;
+    for (int k = 0; k < NX; k++)
+        if (ln + 64 * k < C) {
+            const float d = v[k] - mean;
             q += d * d;
         }
-    const float rstd = 1.0f / sqrtf(block_sum(q, wred, wave, lane) / (float)C + 1e-5f);
+    const float rstd = 1.0f / sqrtf(wave_sum_dpp(q) / (float)C + 1e-5f);
 #pragma unroll
-    for (int i = 0; i < LNE; i++) {
-        const int e = tid + PT * i;
-        if (e < C) act[e] = (v[i] - mean) * rstd * lw[i] + lb[i];
+    for (int k = 0; k < NX; k++) {
+        const int e = ln + 64 * k;
+        if (e < C) act[e] = (v[k] - mean) * rstd * gw[e] + gb[e];
     }
-    __syncthreads();
 }
 
 // Columns of a product Y[N] = W[N, K] . act: column cw + CW * j (j < NJ)
@@ -392,49 +394,68 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
     f32x4 wa[NW], wb[NW];
     f32x4 kq[4];             // attention prefetch: K, 16 dims of one key
     float vr[KPW];           // V of 16 keys, one dim
-    float xv[LNE];           // LayerNorm input
-    float lw[LNE], lb[LNE];  // gains and biases of the next LayerNorm
     float bo = 0.f;          // control lanes: bias of the next output column
 
     // Loads below are unconditional with clamped indices: a load under a
     // divergent branch makes the compiler wait for it inside the branch,
     // which serialises the loads of a phase.
+    // Gains and biases of the next LayerNorm, loaded by the control
+    // wavefront straight into LDS (no registers held across the phases in
+    // between); its next poll waits for them, as loads return in order.
+    // Source indices are clamped to the C floats of each array.
     auto ln_params = [&](const float* gw, const float* gb) {
-        const int tt = opaque_v(tid);
+        if (ctrl) {
+            const int ln = opaque_v(lane);
 #pragma unroll
-        for (int i = 0; i < LNE; i++) {
-            const int e = min(tt + PT * i, C - 1);
-            lw[i] = ldg(gw + e);
-            lb[i] = ldg(gb + e);
+            for (int k = 0; k < U; k++) {
+                const int f4 = min(k * 64 + ln, C / 4 - 1);
+                __builtin_amdgcn_global_load_lds((const void*)(gw + 4 * f4),
+                                                 (lds_void*)(sm.lnw + 256 * k), 16, 0, 0);
+                __builtin_amdgcn_global_load_lds((const void*)(gb + 4 * f4),
+                                                 (lds_void*)(sm.lnb + 256 * k), 16, 0, 0);
+            }
         }
     };
-    // xv = x (tag `tag`), element tid + PT * i. The control wavefront polls
-    // (it has no weight loads in flight for the polls to queue behind) and
-    // passes x on through LDS; false (in every thread) when a wait gave up.
-    auto fetch_x = [&](unsigned tag) -> bool {
+    // LayerNorm of x into act (reference ops.c:191-248) by the control
+    // wavefront, which holds no weight loads for its polls to queue behind:
+    // x is polled (tag `tag`), or for layer 0 formed from the embedding
+    // wte[tok] + wpe[t] (reference fast.c:245-254). One barrier then hands
+    // act to the compute wavefronts; false (in every thread) when a wait
+    // gave up.
+    auto fetch_ln = [&](unsigned tag, bool embed, int tk, int tpos) -> bool {
         bool ok = true;
         if (ctrl) {
             constexpr int NX = 4 * U;  // C <= 256 * U words, 64 per round
             const int ln = opaque_v(lane);
-            int idx[NX];
-            bool need[NX];
             float v[NX];
+            if (embed) {
+                const float* er = a.wte + (long)tk * C;
+                const float* pr = a.wpe + (long)tpos * C;
+                float ev[NX], pv[NX];
 #pragma unroll
-            for (int k = 0; k < NX; k++) {
-                idx[k] = min(ln + 64 * k, C - 1);
-                need[k] = ln + 64 * k < C;
+                for (int k = 0; k < NX; k++) {
+                    const int e = min(ln + 64 * k, C - 1);
+                    ev[k] = ldg(er + e);
+                    pv[k] = ldg(pr + e);
+                }
+#pragma unroll
+                for (int k = 0; k < NX; k++) v[k] = ev[k] + pv[k];
+            } else {
+                int idx[NX];
+                bool need[NX];
+#pragma unroll
+                for (int k = 0; k < NX; k++) {
+                    idx[k] = min(ln + 64 * k, C - 1);
+                    need[k] = ln + 64 * k < C;
+                }
+                const unsigned en = (1u << ((C + 63) / 64)) - 1u;
+                ok = fetch<NX>(rx, idx, need, tag, v, abortw, amark, en);
             }
-            const unsigned en = (1u << ((C + 63) / 64)) - 1u;
-            ok = fetch<NX>(rx, idx, need, tag, v, abortw, amark, en);
-#pragma unroll
-            for (int k = 0; k < NX; k++)
-                if (need[k]) sm.xraw[ln + 64 * k] = v[k];
+            // the gains' loads into LDS have landed once nothing is pending
+            __builtin_amdgcn_s_waitcnt(0x0F70);
+            if (ok) ln_wave<NX>(v, C, ln, sm.lnw, sm.lnb, actf);
         }
-        if (!settle(ok)) return false;
-        const int tt = opaque_v(tid);
-#pragma unroll
-        for (int i = 0; i < LNE; i++) xv[i] = sm.xraw[min(tt + PT * i, C - 1)];
-        return true;
+        return settle(ok);
     };
     // Bias of this lane's output column in the next phase (control lanes;
     // the others load b[0]). Issued before the current epilogue's stores.
@@ -459,20 +480,7 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
             if (tid == 0 && a.err) atomicOr(a.err, 1);
             tok = tok < 0 ? 0 : V - 1;
         }
-        {
-            const float* er = a.wte + (long)tok * C;
-            const float* pr = a.wpe + (long)t * C;
-            float ev[LNE], pv[LNE];
-#pragma unroll
-            for (int i = 0; i < LNE; i++) {
-                const int e = min(tid + PT * i, C - 1);
-                ev[i] = ldg(er + e);
-                pv[i] = ldg(pr + e);
-            }
-#pragma unroll
-            for (int i = 0; i < LNE; i++) xv[i] = ev[i] + pv[i];
-            if (blockIdx.x == 0 && tid == 0) a.hist[t] = tok;
-        }
+        if (blockIdx.x == 0 && tid == 0) a.hist[t] = tok;
 
         for (int l = 0; l < L; l++) {
             const int lane = opaque_v(lane1), cw = opaque_s(cw1);
@@ -487,7 +495,7 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
                            TE = TA + 4, TXIN = TA - 1;
 
             // ---------------- phase A: LayerNorm 1 + QKV into row t
-            if (l > 0 && !fetch_x(TXIN)) return;
+            if (!fetch_ln(TXIN, l == 0, tok, t)) return;
             // attention split layout for keys 0..t
             const int nk = t + 1;
             // as few splits as the workgroup's PW * KPW keys allow (fewer
@@ -541,7 +549,6 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
 #pragma unroll
                 for (int jj = 0; jj < KPW; jj++) vr[jj] = 0.f;
             }
-            ln_to_act(xv, lw, lb, C, actf, sm.wred, tid, wave, lane);
             if (!ctrl) {
                 float acc[UPW];
                 col_dots<NJQ, U>(acc, wa, sm.act, C3, C, cw, CW, lane);
@@ -733,8 +740,7 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
             bo = slot_bias(P.fc_b, C4);
 
             // ---------------- phase D: LayerNorm 2, fc + b, GELU into hid
-            if (!fetch_x(TC)) return;
-            ln_to_act(xv, lw, lb, C, actf, sm.wred, tid, wave, lane);
+            if (!fetch_ln(TC, false, 0, 0)) return;
             if (!ctrl) {
                 float acc[UPW];
                 col_dots<NJQ, U>(acc, wa, sm.act, C4, C, cw, CW, lane);
@@ -833,8 +839,7 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
 
         // ---------------- phase F: final LayerNorm, lm_head (tied wte), argmax partials
         const unsigned TF = sbase + PHASES * L + 1;
-        if (!fetch_x(TF - 1)) return;
-        ln_to_act(xv, lw, lb, C, actf, sm.wred, tid, wave, lane1);
+        if (!fetch_ln(TF - 1, false, 0, 0)) return;
         if (!ctrl) {
             const int ln = opaque_v(lane1);
             const int K4 = C >> 2;
@@ -1152,7 +1157,7 @@ long persist_tagged_words(int C, int H) { return TagLayout(C, H).words(); }
 unsigned persist_tags(int L, int n_steps) { return (unsigned)n_steps * (PHASES * L + 2) + 1; }
 
 bool persist_supported(int C, int H, int V, int cap, int G) {
-    if (G < 1 || G > PT || C % 64 || C != 64 * H || C > 256 * PMAXU || H > 32 || C > LNE * PT)
+    if (G < 1 || G > PT || C % 64 || C != 64 * H || C > 256 * PMAXU || H > 32)
         return false;
     const long CW = (long)PW * G;
     // columns per wavefront: QKV and fc at most NJQ, c_proj and proj one
