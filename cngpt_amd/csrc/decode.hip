@@ -376,7 +376,11 @@ __global__ void __launch_bounds__(256) k_attn_merge(MergeArgs g, float* __restri
     // one row per workgroup: offset the partials to row blockIdx.x
     MergeArgs gr = g;
     gr.part = g.part + (long)blockIdx.x * g.H * g.stride * (g.hs + 4);
-    merge_rows<MAXS>(gr, 1, xs);
+    // every split of a row in one batch, or batches of 4 while the splits
+    // are few (a batch past the last split re-reads it)
+    const int t = g.pos_dev ? *g.pos_dev : g.q_pos;
+    if ((t + g.kps) / g.kps > 4) merge_rows<MAXS>(gr, 1, xs);
+    else merge_rows<4>(gr, 1, xs);
     const int C4 = g.H * g.hs / 4;
     f32x4* o = (f32x4*)(out + (long)blockIdx.x * ldo);
     for (int c = threadIdx.x; c < C4; c += blockDim.x) o[c] = xs[c];
