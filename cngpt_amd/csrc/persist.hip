@@ -7,15 +7,19 @@
 // as separate kernels, every stage pays a kernel boundary plus the HBM
 // latency of its weights. Here the stages are phases of one cooperative
 // launch (one workgroup per CU), and since no weight depends on the data,
-// each workgroup loads the next phase's weights into registers as soon as
-// the current phase's products are done, so that traffic overlaps the wait
-// for the next phase's input. One launch runs any number of greedy steps
-// (the argmax of step s feeds step s+1 without leaving the GPU).
+// each workgroup loads weights into registers phases before they are
+// used, right after the publish of the phase that freed their slots, so
+// that traffic overlaps the waits for later inputs. One launch runs any
+// number of steps (the token of step s feeds step s+1 without leaving the
+// GPU; sampled tokens are drawn inside the launch too).
 //
 // Workgroup: PW compute wavefronts + 1 control wavefront. The compute
-// wavefronts hold weights and form dot products; the control wavefront
-// sums their per-column results in a fixed order, applies the epilogue and
-// publishes the outputs.
+// wavefronts hold weights and form dot products; the control wavefront,
+// which holds no weight loads for its polls to queue behind, polls x and
+// forms both LayerNorms, collects the per-column results, applies the
+// epilogue and publishes the outputs. The (head, key split) attention items
+// run on the workgroups that own no c_proj / proj column when they fit
+// there; those load the next layer's cached keys during E.
 //
 // Exchange between workgroups: every value a phase publishes is one 64-bit
 // word, the float in the low half and the tag of the phase that made it in
