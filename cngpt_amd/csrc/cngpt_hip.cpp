@@ -603,7 +603,8 @@ bool persist_usable(cngpt_hip_ctx* h) {
 
 int persist_refused(cngpt_hip_ctx* h) {
     return fail("persistent decode needs one cached sequence (B=%d), head size 64, n_embd <= "
-                "768 and a device with cooperative launch", h->kvB);
+                "768, a device with cooperative launch and enough CUs for the widths and the "
+                "cache capacity", h->kvB);
 }
 
 // n greedy decode steps of the single cached sequence as one launch.

@@ -502,20 +502,19 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
             if (!fetch_ln(TXIN, l == 0, tok, t)) return;
             // attention split layout for keys 0..t
             const int nk = t + 1;
-            // as few splits as the workgroup's PW * KPW keys allow (fewer
-            // partials to exchange)
+            // The (head, split) items go to the workgroups after the c_proj /
+            // proj column owners (persist_supported checks that they fit
+            // there): those workgroups have no column work in C and E, so in
+            // E they load the next layer's cached keys and park them in LDS,
+            // and their QKV publish in A is not held up behind those loads.
+            // As few splits as the workgroup's PW * KPW keys allow (fewer
+            // partials to exchange).
+            const int owners = (C + PW - 1) / PW;
             int ns = (nk + PW * KPW - 1) / (PW * KPW);
-            ns = min(ns, min(G / H, PMAXS));
+            ns = min(ns, min((G - owners) / H, PMAXS));
             const int kps = (nk + ns - 1) / ns;
             const int kpw = (kps + PW - 1) / PW;
-            // The (head, split) items go to the workgroups after the c_proj /
-            // proj column owners when they fit there ("early"): those
-            // workgroups have no column work in C and E, so in E they load
-            // the next layer's cached keys and park them in LDS, and their
-            // QKV publish in A is not held up behind those loads.
-            const int owners = (C + PW - 1) / PW;
-            const bool early = owners + H * ns <= G;
-            const int item = (int)blockIdx.x - (early ? owners : 0);
+            const int item = (int)blockIdx.x - owners;
             const bool has_item = item >= 0 && item < H * ns;
             const int ih = max(item, 0) / ns, isp = max(item, 0) - ih * ns;
             const int k0 = isp * kps, k1 = min(k0 + kps, nk);
@@ -536,7 +535,7 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
                 }
             };
             if (!ctrl && has_item) {
-                if (early && l > 0) {
+                if (l > 0) {
                     // staged in the previous layer's E by this wavefront
 #pragma unroll
                     for (int i = 0; i < 4; i++)
@@ -824,7 +823,7 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
                 if (ctrl && c >= 0) put_all(tx + c, tl.xs, (xo + sm.red[j][q]) + bo, TE);
                 __syncthreads();
             } else if (l + 1 < L) {
-                if (early && has_item && !ctrl) {
+                if (has_item && !ctrl) {
                     load_keys(l + 1);
 #pragma unroll
                     for (int i = 0; i < 4; i++)
@@ -1166,8 +1165,10 @@ bool persist_supported(int C, int H, int V, int cap, int G) {
     const long CW = (long)PW * G;
     // columns per wavefront: QKV and fc at most NJQ, c_proj and proj one
     if (4L * C > NJQ * CW || C > CW || V < 1) return false;
-    // attention: H * splits workgroups, at most PW * KPW keys per split
-    const int ns = std::min(G / H, PMAXS);
+    // attention: H * splits workgroups after the c_proj / proj column
+    // owners, at most PW * KPW keys per split
+    const int owners = (C + PW - 1) / PW;
+    const int ns = std::min((G - owners) / H, PMAXS);
     if (ns < 1 || (long)ns * PW * KPW < cap) return false;
     return true;
 }
