@@ -177,9 +177,15 @@ struct Timed {
 // rows wins (measured on GPT-2 medium, 8 sequences: 1.72 vs 1.88 ms a step).
 constexpr int SKINNY = 2;
 
+int run_ln(cngpt_hip_ctx* h, const float* x, long in_stride, const float* w, const float* b,
+           float* out, int rows);
+
+// With lnw / lnb / lnout set, also LayerNorm(Y rows) into lnout (the next
+// product's input); over more than SKINNY rows the split-K sum forms it.
 int run_gemm(cngpt_hip_ctx* h, const float* X, const float* W, const float* bias, float* Y, int M,
              int N, int K, int epi, int seg = 0, long seg_stride = 0, long ldy = -1,
-             int row_off = 0, const int* row_off_dev = nullptr) {
+             int row_off = 0, const int* row_off_dev = nullptr, const float* lnw = nullptr,
+             const float* lnb = nullptr, float* lnout = nullptr) {
     const double flops = 2.0 * M * N * K;
     const double bytes =
         4.0 * ((double)M * K + (double)N * K + (double)M * N * (epi == EPI_RESID ? 2 : 1));
@@ -191,9 +197,11 @@ int run_gemm(cngpt_hip_ctx* h, const float* X, const float* W, const float* bias
         d.seg = seg; d.seg_stride = seg_stride;
         d.row_off = row_off; d.row_off_dev = row_off_dev;
         d.epi = epi;
-        Timed t(h, CNGPT_K_GEMV, flops, bytes);
-        HIP_TRY(launch_dgemv(d, h->stream));
-        return 0;
+        {
+            Timed t(h, CNGPT_K_GEMV, flops, bytes);
+            HIP_TRY(launch_dgemv(d, h->stream));
+        }
+        return lnout ? run_ln(h, Y, d.ldy, lnw, lnb, lnout, M) : 0;
     }
     GemmArgs a{};
     a.X = X; a.W = W; a.bias = bias; a.Y = Y;
@@ -203,6 +211,7 @@ int run_gemm(cngpt_hip_ctx* h, const float* X, const float* W, const float* bias
     a.row_off = row_off; a.row_off_dev = row_off_dev;
     a.epi = epi;
     a.part = h->gemm_part; a.part_cap = GEMM_PART_FLOATS;
+    a.ln_w = lnw; a.ln_b = lnb; a.ln_out = lnout;
     Timed t(h, CNGPT_K_GEMM, flops, bytes);
     HIP_TRY(launch_gemm(a, h->stream));
     return 0;
@@ -243,7 +252,8 @@ int run_ln_gemm(cngpt_hip_ctx* h, const float* x, const float* lw, const float* 
 // Final LayerNorm and lm_head over M rows of x -> logits [M, V]; with
 // want_tok the greedy token of each row goes to next_tok, and pos_inc (if
 // set) is advanced once everything else of the step has run.
-int run_lm_head(cngpt_hip_ctx* h, const float* x, int M, bool want_tok, int* pos_inc) {
+int run_lm_head(cngpt_hip_ctx* h, const float* x, int M, bool want_tok, int* pos_inc,
+                bool ln_done = false) {
     const int C = h->cfg.n_embd, V = h->cfg.vocab_size;
     if (M <= SKINNY) {
         // The final LayerNorm runs once on its own: recomputing it in each of
@@ -272,7 +282,8 @@ int run_lm_head(cngpt_hip_ctx* h, const float* x, int M, bool want_tok, int* pos
                                        h->stream));
         }
     } else {
-        if (run_ln(h, x, C, h->lnf_w, h->lnf_b, h->lnc, M)) return -1;
+        // (ln_done: the final LayerNorm is already in lnc)
+        if (!ln_done && run_ln(h, x, C, h->lnf_w, h->lnf_b, h->lnc, M)) return -1;
         if (run_gemm(h, h->lnc, h->wte, nullptr, h->logits, M, V, C, EPI_STORE)) return -1;
         if (want_tok) {
             Timed t(h, CNGPT_K_ARGMAX, 0.0, 4.0 * M * V);
@@ -288,7 +299,9 @@ int run_lm_head(cngpt_hip_ctx* h, const float* x, int M, bool want_tok, int* pos
 // + bias. For B <= 8 the c_proj product merges the attention splits itself;
 // otherwise the merged rows go through aoutc.
 int run_attn_row_proj(cngpt_hip_ctx* h, const float* qkv, long seq_stride, int B, int q_pos,
-                      const int* pos_dev, int max_keys, const LayerW& w, float* xres) {
+                      const int* pos_dev, int max_keys, const LayerW& w, float* xres,
+                      const float* lnw = nullptr, const float* lnb = nullptr,
+                      float* lnout = nullptr) {
     const cngpt_hip_config& c = h->cfg;
     const int C = c.n_embd, hs = C / c.n_head;
     AttnDecArgs a{};
@@ -317,15 +330,18 @@ int run_attn_row_proj(cngpt_hip_ctx* h, const float* qkv, long seq_stride, int B
         d.W = w.proj_w; d.bias = w.proj_b; d.Y = xres; d.ldy = C;
         d.M = B; d.N = C; d.K = C;
         d.epi = EPI_RESID;
-        Timed t(h, CNGPT_K_GEMV, 2.0 * B * C * C, 4.0 * ((double)C * C + 2.0 * B * C));
-        HIP_TRY(launch_dgemv(d, h->stream));
-        return 0;
+        {
+            Timed t(h, CNGPT_K_GEMV, 2.0 * B * C * C, 4.0 * ((double)C * C + 2.0 * B * C));
+            HIP_TRY(launch_dgemv(d, h->stream));
+        }
+        return lnout ? run_ln(h, xres, C, lnw, lnb, lnout, B) : 0;
     }
     {
         Timed t(h, CNGPT_K_ATTN_ROW, 0.0, 4.0 * B * C);
         HIP_TRY(launch_attention_merge(g, B, h->aoutc, C, h->stream));
     }
-    return run_gemm(h, h->aoutc, w.proj_w, w.proj_b, xres, B, C, C, EPI_RESID);
+    return run_gemm(h, h->aoutc, w.proj_w, w.proj_b, xres, B, C, C, EPI_RESID, 0, 0, -1, 0,
+                    nullptr, lnw, lnb, lnout);
 }
 
 void drop_graph(cngpt_hip_ctx* h) {
@@ -516,6 +532,9 @@ int enqueue_decode_step(cngpt_hip_ctx* h) {
     const int B = h->kvB;
     const long cap = h->capKV;
     const bool fused_embed = B <= SKINNY;
+    // over more than SKINNY rows, every LayerNorm after the first is formed
+    // by the residual product before it (in its split-K sum)
+    const bool fuse_ln = B > SKINNY;
     if (!fused_embed) {
         Timed t(h, CNGPT_K_EMBED, 0.0, 12.0 * C * B);
         HIP_TRY(launch_embed(h->next_tok, h->wte, h->wpe, h->xc, B, 1, C, c.vocab_size, 0, h->pos,
@@ -538,9 +557,28 @@ int enqueue_decode_step(cngpt_hip_ctx* h) {
             Timed t(h, CNGPT_K_GEMV, 2.0 * B * 3 * C * C,
                     4.0 * (3.0 * C * C + 3.0 * B * C + 2.0 * B * C));
             HIP_TRY(launch_dgemv(d, h->stream));
+        } else if (fuse_ln && l > 0) {
+            // LayerNorm 1 was formed with the previous layer's residual
+            if (run_gemm(h, h->lnc, w.attn_w, w.attn_b, kvl, B, 3 * C, C, EPI_BIAS, 1, cap, 3L * C,
+                         0, h->pos))
+                return -1;
         } else if (run_ln_gemm(h, h->xc, w.ln1_w, w.ln1_b, h->lnc, w.attn_w, w.attn_b, kvl, B,
                                3 * C, EPI_BIAS, 1, cap, 3L * C, h->pos)) {
             return -1;
+        }
+        if (fuse_ln) {
+            // the residual products also form the next LayerNorm (2, then 1
+            // of the next layer or the final one) while summing their splits
+            const bool last = l + 1 == L;
+            const LayerW& wn = h->layers[last ? l : l + 1];
+            if (run_attn_row_proj(h, kvl, cap, B, 0, h->pos, (int)cap, w, h->xc, w.ln2_w,
+                                  w.ln2_b, h->lnc) ||
+                run_gemm(h, h->lnc, w.fc_w, w.fc_b, h->hidc, B, 4 * C, C, EPI_BIAS_GELU) ||
+                run_gemm(h, h->hidc, w.mlp_w, w.mlp_b, h->xc, B, C, 4 * C, EPI_RESID, 0, 0, -1, 0,
+                         nullptr, last ? h->lnf_w : wn.ln1_w, last ? h->lnf_b : wn.ln1_b,
+                         h->lnc))
+                return -1;
+            continue;
         }
         if (run_attn_row_proj(h, kvl, cap, B, 0, h->pos, (int)cap, w, h->xc)) return -1;
         if (run_ln_gemm(h, h->xc, w.ln2_w, w.ln2_b, h->lnc, w.fc_w, w.fc_b, h->hidc, B, 4 * C,
@@ -548,7 +586,7 @@ int enqueue_decode_step(cngpt_hip_ctx* h) {
             return -1;
         if (run_gemm(h, h->hidc, w.mlp_w, w.mlp_b, h->xc, B, C, 4 * C, EPI_RESID)) return -1;
     }
-    if (run_lm_head(h, h->xc, B, true, h->pos)) return -1;
+    if (run_lm_head(h, h->xc, B, true, h->pos, fuse_ln)) return -1;
     h->curB = B; h->curT = 1; h->curMode = CNGPT_LAST;
     return 0;
 }

@@ -447,6 +447,64 @@ __global__ void __launch_bounds__(256) k_stream_reduce(GemmArgs a, int KS) {
     store_out<EPI>(a, roff, (int)(i / a.N), (int)(i % a.N), v);
 }
 
+// The same sum for one row per workgroup (float4 columns tid + 256 i),
+// then the LayerNorm (reference ops.c:191-248) of the finished row into
+// a.ln_out: the residual stream and the next product's input in one pass.
+template <int EPI, int NCH>
+__global__ void __launch_bounds__(256) k_stream_reduce_ln(GemmArgs a, int KS) {
+    __shared__ float red[4];
+    const int r = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int N4 = a.N >> 2;
+    const long MN4 = (long)a.M * N4;
+    const f32x4* p = (const f32x4*)(a.part + (long)r * a.N);
+    float* yrow = a.Y + (long)r * a.ldy;
+    f32x4 y[NCH];
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < NCH; i++) {
+        const int c4 = tid + 256 * i, cc = min(c4, N4 - 1);
+        f32x4 v = {0.f, 0.f, 0.f, 0.f};
+        for (int q0 = 0; q0 < KS; q0 += 8) {
+            f32x4 t[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) t[j] = p[(long)min(q0 + j, KS - 1) * MN4 + cc];
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                if (q0 + j < KS) v += t[j];
+        }
+#pragma unroll
+        for (int k = 0; k < 4; k++) y[i][k] = apply_epi<EPI>(v[k], a.bias, 4 * cc + k, yrow + 4 * cc + k);
+        if (c4 < N4) {
+            *(f32x4*)(yrow + 4 * c4) = y[i];
+            s += (y[i].x + y[i].y) + (y[i].z + y[i].w);
+        }
+    }
+    auto block_sum = [&](float v) {
+        v = wave_sum(v);
+        __syncthreads();
+        if (lane == 0) red[wave] = v;
+        __syncthreads();
+        return (red[0] + red[1]) + (red[2] + red[3]);
+    };
+    const float mean = block_sum(s) / (float)a.N;
+    float q = 0.f;
+#pragma unroll
+    for (int i = 0; i < NCH; i++)
+        if (tid + 256 * i < N4) {
+            const f32x4 d = y[i] - mean;
+            q += (d.x * d.x + d.y * d.y) + (d.z * d.z + d.w * d.w);
+        }
+    const float rstd = 1.0f / sqrtf(block_sum(q) / (float)a.N + 1e-5f);
+    float* orow = a.ln_out + (long)r * a.N;
+#pragma unroll
+    for (int i = 0; i < NCH; i++) {
+        const int c4 = tid + 256 * i;
+        if (c4 < N4)
+            *(f32x4*)(orow + 4 * c4) = (y[i] - mean) * rstd * *(const f32x4*)(a.ln_w + 4 * c4) +
+                                       *(const f32x4*)(a.ln_b + 4 * c4);
+    }
+}
+
 // Split K until the column tiles times the splits reach two workgroups per
 // CU (the partials must fit a.part_cap floats; ranges are whole chunks).
 template <int EPI, int MB>
@@ -459,7 +517,18 @@ hipError_t stream_mb(const GemmArgs& a, hipStream_t s) {
     KS = (a.K + KR - 1) / KR;
     k_stream<EPI, MB><<<tiles_n * KS, ST_NW * 64, 0, s>>>(a, tiles_n, KR, KS);
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || KS == 1) return e;
+    if (e != hipSuccess) return e;
+    if (KS == 1) {
+        if (!a.ln_out) return e;
+        return launch_layernorm(a.Y, a.ldy, a.ln_w, a.ln_b, a.ln_out, a.N, a.M, a.N, s);
+    }
+    if (a.ln_out) {
+        const int n4 = a.N / 4;
+        if (n4 <= 256) k_stream_reduce_ln<EPI, 1><<<a.M, 256, 0, s>>>(a, KS);
+        else if (n4 <= 512) k_stream_reduce_ln<EPI, 2><<<a.M, 256, 0, s>>>(a, KS);
+        else k_stream_reduce_ln<EPI, 4><<<a.M, 256, 0, s>>>(a, KS);
+        return hipGetLastError();
+    }
     k_stream_reduce<EPI><<<(unsigned)(((long)a.M * a.N + 255) / 256), 256, 0, s>>>(a, KS);
     return hipGetLastError();
 }
@@ -516,6 +585,9 @@ hipError_t gemm_epi(const GemmArgs& a, hipStream_t s) {
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
     if (a.M <= 0 || a.N <= 0) return hipSuccess;
     if (a.K <= 0 || (a.K & 3)) return hipErrorInvalidValue;
+    if (a.ln_out && (a.seg || a.row_off || a.row_off_dev || (a.N & 3) || a.N > 4096 || !a.ln_w ||
+                     !a.ln_b))
+        return hipErrorInvalidValue;
     if (a.M <= SKINNY_MAX_M) {
         switch (a.epi) {
             case EPI_STORE: return skinny_epi<EPI_STORE>(a, s);
@@ -525,11 +597,13 @@ hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
         }
         return hipErrorInvalidValue;
     }
+    hipError_t e = hipErrorInvalidValue;
     switch (a.epi) {
-        case EPI_STORE: return gemm_epi<EPI_STORE>(a, s);
-        case EPI_BIAS: return gemm_epi<EPI_BIAS>(a, s);
-        case EPI_BIAS_GELU: return gemm_epi<EPI_BIAS_GELU>(a, s);
-        case EPI_RESID: return gemm_epi<EPI_RESID>(a, s);
+        case EPI_STORE: e = gemm_epi<EPI_STORE>(a, s); break;
+        case EPI_BIAS: e = gemm_epi<EPI_BIAS>(a, s); break;
+        case EPI_BIAS_GELU: e = gemm_epi<EPI_BIAS_GELU>(a, s); break;
+        case EPI_RESID: e = gemm_epi<EPI_RESID>(a, s); break;
     }
-    return hipErrorInvalidValue;
+    if (e != hipSuccess || !a.ln_out) return e;
+    return launch_layernorm(a.Y, a.ldy, a.ln_w, a.ln_b, a.ln_out, a.N, a.M, a.N, s);
 }

@@ -30,6 +30,12 @@ struct GemmArgs {
     int epi;                   // EpiMode
     float* part;               // split-K partials of M <= SKINNY_MAX_M (NULL: no split)
     long part_cap;             // floats available at part
+    // Optional (seg = 0, no row offsets): also the LayerNorm of every output
+    // row with gains ln_w and biases ln_b into ln_out (rows of N floats),
+    // formed while the split-K partials are summed when K is split.
+    const float* ln_w;
+    const float* ln_b;
+    float* ln_out;
 };
 // M <= SKINNY_MAX_M rows take the weight-streaming k_stream, larger M the
 // 128 x 128 MFMA tiles.
