@@ -137,6 +137,27 @@ def test_decode_more_than_eight_sequences():
     compare(np.stack(logits, 1), ref, what="B=12 decode")
 
 
+@pytest.mark.parametrize("C,H,B", [(128, 2, 5), (128, 4, 70)])
+def test_decode_layernorm_formed_by_the_residual_products(C, H, B):
+    """Over more than two sequences each residual product (c_proj, proj)
+    also writes the next LayerNorm: in its split-K sum, or, where K is not
+    split (width 128: one chunk) or the rows take MFMA tiles (70 > 64), by
+    a LayerNorm launch right after it."""
+    cfg = cngpt_amd.Config(2, H, C, 500, 64)
+    params = randomize(cfg, cngpt_amd.init_weights(cfg, 21), 22)
+    prompt = np.random.default_rng(13).integers(0, cfg.vocab_size, size=(B, 7), dtype=np.int32)
+    with cngpt_amd.Model(cfg, params) as m:
+        logits = [m.decode_begin(prompt, capacity=24)]
+        toks = [logits[0].argmax(-1).astype(np.int32)]
+        for _ in range(12):
+            logits.append(m.decode_step(toks[-1]))
+            toks.append(logits[-1].argmax(-1).astype(np.int32))
+    seq = np.concatenate([prompt, np.stack(toks[:-1], 1)], axis=1)
+    ref = oracle.forward(ocfg(cfg), params, seq, oracle.ALL)[:, 6:]
+    say(f"decode C={C} B={B}")
+    compare(np.stack(logits, 1), ref, what=f"C={C} B={B} decode")
+
+
 SAMPLE_CASES = [(0.8, 40), (1.0, 40), (0.0, 40), (1.0, 1), (1.3, 0), (0.7, 50257),
                 (1.0, 5000)]
 
