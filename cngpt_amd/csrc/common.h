@@ -45,6 +45,17 @@ __device__ __forceinline__ float row_sum16(float v) {
     v += CNGPT_DPP(v, 0x140);  // row_mirror
     return v;
 }
+// LDS pointer type of the direct global -> LDS loads (global_load_lds).
+typedef __attribute__((address_space(3))) void lds_void;
+
+// s_waitcnt vmcnt(N), expcnt and lgkmcnt left alone (GFX9 encoding: vmcnt
+// in bits 3:0 and 15:14).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (7 << 4) | (0xF << 8));
+}
+
 __device__ __forceinline__ float lane_f(float v, int l) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
 }

@@ -59,15 +59,6 @@ __device__ __forceinline__ void tile_coords(int pid, int tiles_m, int tiles_n, i
     tn = in_group / gsize;
 }
 
-typedef __attribute__((address_space(3))) void lds_void;
-
-// s_waitcnt vmcnt(N), expcnt and lgkmcnt left alone.
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (7 << 4) | (0xF << 8));
-}
-
 // Stage layout: operand tile of BM rows x BK floats, granule (16 bytes) g
 // at row g / GPR, slot g % GPR, where slot s of row r holds k quad
 // s ^ ((r / RSW) % GPR) (RSW = rows per 256 bytes). The MFMA order over k

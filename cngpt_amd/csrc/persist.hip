@@ -244,8 +244,6 @@ __device__ __forceinline__ float block_max(float v, float* wred, int wave, int l
     return m;
 }
 
-typedef __attribute__((address_space(3))) void lds_void;
-
 // LayerNorm (reference ops.c:191-248) by one wavefront: x[lane + 64 k] in
 // v[k], gains and biases from LDS, result into act. Two passes (mean, then
 // the mean square deviation), each one wavefront reduction.
@@ -456,7 +454,7 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
                 ok = fetch<NX>(rx, idx, need, tag, v, abortw, amark, en);
             }
             // the gains' loads into LDS have landed once nothing is pending
-            __builtin_amdgcn_s_waitcnt(0x0F70);
+            wait_vmcnt<0>();
             if (ok) ln_wave<NX>(v, C, ln, sm.lnw, sm.lnb, actf);
         }
         return settle(ok);
