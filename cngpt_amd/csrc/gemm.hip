@@ -449,22 +449,30 @@ __global__ void __launch_bounds__(256) k_stream_reduce_ln(GemmArgs a, int KS) {
     const long MN4 = (long)a.M * N4;
     const f32x4* p = (const f32x4*)(a.part + (long)r * a.N);
     float* yrow = a.Y + (long)r * a.ldy;
-    f32x4 y[NCH];
+    f32x4 y[NCH], v[NCH];
+#pragma unroll
+    for (int i = 0; i < NCH; i++) v[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // batches of 8 partials of every column of this thread in flight together
+    for (int q0 = 0; q0 < KS; q0 += 8) {
+        f32x4 t[NCH][8];
+#pragma unroll
+        for (int i = 0; i < NCH; i++) {
+            const int cc = min(tid + 256 * i, N4 - 1);
+#pragma unroll
+            for (int j = 0; j < 8; j++) t[i][j] = p[(long)min(q0 + j, KS - 1) * MN4 + cc];
+        }
+#pragma unroll
+        for (int i = 0; i < NCH; i++)
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                if (q0 + j < KS) v[i] += t[i][j];
+    }
     float s = 0.f;
 #pragma unroll
     for (int i = 0; i < NCH; i++) {
         const int c4 = tid + 256 * i, cc = min(c4, N4 - 1);
-        f32x4 v = {0.f, 0.f, 0.f, 0.f};
-        for (int q0 = 0; q0 < KS; q0 += 8) {
-            f32x4 t[8];
 #pragma unroll
-            for (int j = 0; j < 8; j++) t[j] = p[(long)min(q0 + j, KS - 1) * MN4 + cc];
-#pragma unroll
-            for (int j = 0; j < 8; j++)
-                if (q0 + j < KS) v += t[j];
-        }
-#pragma unroll
-        for (int k = 0; k < 4; k++) y[i][k] = apply_epi<EPI>(v[k], a.bias, 4 * cc + k, yrow + 4 * cc + k);
+        for (int k = 0; k < 4; k++) y[i][k] = apply_epi<EPI>(v[i][k], a.bias, 4 * cc + k, yrow + 4 * cc + k);
         if (c4 < N4) {
             *(f32x4*)(yrow + 4 * c4) = y[i];
             s += (y[i].x + y[i].y) + (y[i].z + y[i].w);
