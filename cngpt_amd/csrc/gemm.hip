@@ -59,6 +59,89 @@ __device__ __forceinline__ void tile_coords(int pid, int tiles_m, int tiles_n, i
     tn = in_group / gsize;
 }
 
+// Epilogue of one wavefront's 64 x 64 block at (r0, c0): acc[i][j][r] is
+// row r0 + 32 i + 8 (r / 4) + 4 (lane / 32) + r % 4, column c0 + 32 j +
+// lane % 32. The bias is read once per column, and with the residual the
+// old values of a block are all loaded before its first store: the
+// compiler cannot tell that a store leaves the later loads' addresses
+// alone, and element by element would wait for each load in turn. A block
+// wholly inside a plain row-major output takes one base address and
+// constant row steps; edge blocks and segmented rows map each row, load
+// from clamped rows and columns (inside the output) and mask the stores.
+// Same arithmetic as apply_epi.
+template <int EPI>
+__device__ __forceinline__ float epi_value(float v, float b, float old) {
+    if (EPI == EPI_STORE) return v;
+    if (EPI == EPI_BIAS) return v + b;
+    if (EPI == EPI_BIAS_GELU) return gelu_tanh(v + b);
+    return (old + v) + b;
+}
+
+template <int EPI>
+__device__ __forceinline__ void tile_store(const GemmArgs& a, const f32x16 (&acc)[2][2], int r0,
+                                           int c0, int lane) {
+    const int lr = lane & 31, lh = lane >> 5;
+    const long roff = a.row_off + (a.row_off_dev ? *a.row_off_dev : 0);
+    const long ldy = a.ldy;
+    float bj[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) bj[j] = EPI == EPI_STORE ? 0.f : a.bias[min(c0 + 32 * j + lr, a.N - 1)];
+    if (!a.seg && r0 + 64 <= a.M && c0 + 64 <= a.N && ldy <= (1L << 28)) {
+        // The row pointer of each 4-row group is uniform over the wavefront
+        // (scalar registers); a lane adds one unsigned 32-bit byte offset
+        // (4 rows of at most 2^28 floats), the same for every element.
+        const unsigned lob = 4u * (unsigned)(4 * lh * ldy + lr);
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                auto at = [&](int r) {
+                    const float* rowp = a.Y + (r0 + 32 * i + 8 * (r >> 2) + (r & 3) + roff) * ldy + c0 + 32 * j;
+                    return (float*)((char*)rowp + lob);
+                };
+                float old[16];
+                if (EPI == EPI_RESID) {
+#pragma unroll
+                    for (int r = 0; r < 16; r++) old[r] = *at(r);
+                }
+#pragma unroll
+                for (int r = 0; r < 16; r++)
+                    *at(r) = epi_value<EPI>(acc[i][j][r], bj[j], EPI == EPI_RESID ? old[r] : 0.f);
+            }
+        return;
+    }
+    // edge blocks: the bias and each group's values are pinned (an empty
+    // asm that takes and returns them) before the group's masked stores;
+    // formed inside the masked blocks, each would wait for every store
+    // issued before it (the wait counter counts stores too)
+    asm volatile("" : "+v"(bj[0]), "+v"(bj[1]));
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int col = c0 + 32 * j + lr, cc = min(col, a.N - 1);
+#pragma unroll
+            for (int r4 = 0; r4 < 4; r4++) {
+                long ro[4];
+                float y[4];
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int row = min(r0 + 32 * i + 8 * r4 + 4 * lh + r, a.M - 1);
+                    const long orow = a.seg ? (long)(row / a.seg) * a.seg_stride + row % a.seg : row;
+                    ro[r] = (orow + roff) * ldy;
+                    y[r] = EPI == EPI_RESID ? a.Y[ro[r] + cc] : 0.f;
+                }
+#pragma unroll
+                for (int r = 0; r < 4; r++) y[r] = epi_value<EPI>(acc[i][j][4 * r4 + r], bj[j], y[r]);
+                asm volatile("" : "+v"(y[0]), "+v"(y[1]), "+v"(y[2]), "+v"(y[3]));
+                if (col >= a.N) continue;
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    if (r0 + 32 * i + 8 * r4 + 4 * lh + r < a.M) a.Y[ro[r] + col] = y[r];
+            }
+        }
+}
+
 // Stage layout: operand tile of BM rows x BK floats, granule (16 bytes) g
 // at row g / GPR, slot g % GPR, where slot s of row r holds k quad
 // s ^ ((r / RSW) % GPR) (RSW = rows per 256 bytes). The MFMA order over k
@@ -155,24 +238,7 @@ __global__ void __launch_bounds__(NTHREADS, OCC) k_gemm_dl(GemmArgs a, int tiles
         }
     }
 
-    const long roff = a.row_off + (a.row_off_dev ? *a.row_off_dev : 0);
-#pragma unroll
-    for (int j = 0; j < 2; j++) {
-        const int col = n0 + wn + j * 32 + lr;
-        if (col >= a.N) continue;
-#pragma unroll
-        for (int i = 0; i < 2; i++) {
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-                if (row >= a.M) continue;
-                long orow = a.seg ? (long)(row / a.seg) * a.seg_stride + row % a.seg : row;
-                orow += roff;
-                float* y = a.Y + orow * a.ldy + col;
-                *y = apply_epi<EPI>(acc[i][j][r], a.bias, col, y);
-            }
-        }
-    }
+    tile_store<EPI>(a, acc, m0 + wm, n0 + wn, lane);
 }
 
 template <int EPI, int BK, int PAD, int OCC>
@@ -264,26 +330,7 @@ __global__ void __launch_bounds__(NTHREADS, OCC) k_gemm(GemmArgs a, int tiles_m,
         __syncthreads();
     }
 
-    // Epilogue. acc[i][j][r] holds row wm + 32i + 8(r/4) + 4*lh + r%4,
-    // column wn + 32j + lr of the tile.
-    const long roff = a.row_off + (a.row_off_dev ? *a.row_off_dev : 0);
-#pragma unroll
-    for (int j = 0; j < 2; j++) {
-        const int col = n0 + wn + j * 32 + lr;
-        if (col >= a.N) continue;
-#pragma unroll
-        for (int i = 0; i < 2; i++) {
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-                if (row >= a.M) continue;
-                long orow = a.seg ? (long)(row / a.seg) * a.seg_stride + row % a.seg : row;
-                orow += roff;
-                float* y = a.Y + orow * a.ldy + col;
-                *y = apply_epi<EPI>(acc[i][j][r], a.bias, col, y);
-            }
-        }
-    }
+    tile_store<EPI>(a, acc, m0 + wm, n0 + wn, lane);
 }
 
 // ---------------------------------------------------------------- skinny
