@@ -86,10 +86,11 @@ __device__ __forceinline__ void tile_store(const GemmArgs& a, const f32x16 (&acc
     float bj[2];
 #pragma unroll
     for (int j = 0; j < 2; j++) bj[j] = EPI == EPI_STORE ? 0.f : a.bias[min(c0 + 32 * j + lr, a.N - 1)];
-    if (!a.seg && r0 + 64 <= a.M && c0 + 64 <= a.N && ldy <= (1L << 28)) {
+    if (!a.seg && r0 + 64 <= a.M && c0 + 64 <= a.N && ldy <= (1L << 27)) {
         // The row pointer of each 4-row group is uniform over the wavefront
-        // (scalar registers); a lane adds one unsigned 32-bit byte offset
-        // (4 rows of at most 2^28 floats), the same for every element.
+        // (scalar registers); a lane adds one unsigned 32-bit byte offset,
+        // the same for every element: 4 * (4 ldy + 31) < 2^32 for row
+        // strides up to 2^27 floats.
         const unsigned lob = 4u * (unsigned)(4 * lh * ldy + lr);
 #pragma unroll
         for (int i = 0; i < 2; i++)
