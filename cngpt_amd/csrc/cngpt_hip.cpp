@@ -71,7 +71,8 @@ struct cngpt_hip_ctx {
     long n_params = 0;
     const float *wte = nullptr, *wpe = nullptr, *lnf_w = nullptr, *lnf_b = nullptr;
     std::vector<LayerW> layers;
-    LayerW* d_layers = nullptr;  // device copy of layers (persistent decode)
+    LayerW* d_layers = nullptr;  // device copy of layers (persistent decode), at the
+                                 // end of the parameter allocation
 
     // activation arena: one allocation, carved below
     char* d_act = nullptr;
@@ -746,10 +747,9 @@ long params_of(const cngpt_hip_config* c) {
 // Make h->d_params hold the parameters of shape cfg: reuse the allocation
 // when the shape is unchanged, else free it (and the activations, which
 // depend on the shape) and allocate anew.
-int params_prepare(cngpt_hip_ctx* h, const cngpt_hip_config* cfg, bool* same_shape) {
+int params_prepare(cngpt_hip_ctx* h, const cngpt_hip_config* cfg) {
     HIP_TRY(hipSetDevice(h->device));
-    *same_shape = h->d_params && memcmp(&h->cfg, cfg, sizeof(*cfg)) == 0;
-    if (*same_shape) return 0;
+    if (h->d_params && memcmp(&h->cfg, cfg, sizeof(*cfg)) == 0) return 0;
     if (h->d_params) {
         HIP_TRY(hipStreamSynchronize(h->stream));
         HIP_TRY(hipFree(h->d_params));
@@ -763,19 +763,24 @@ int params_prepare(cngpt_hip_ctx* h, const cngpt_hip_config* cfg, bool* same_sha
         h->kvB = h->kvLen = 0;
     }
     h->have_params = false;
+    h->d_layers = nullptr;
+    // one allocation: the parameters, then the table of per-layer pointers
+    // into them that the persistent decode reads
     const long want = params_of(cfg);
-    if (hipMalloc(&h->d_params, (size_t)want * sizeof(float)) != hipSuccess) {
+    const size_t bytes = align_up((size_t)want * sizeof(float)) + (size_t)cfg->n_layer * sizeof(LayerW);
+    if (hipMalloc(&h->d_params, bytes) != hipSuccess) {
         (void)hipGetLastError();
         h->d_params = nullptr;
         return fail("parameter allocation of %ld floats failed", want);
     }
+    h->d_layers = (LayerW*)((char*)h->d_params + align_up((size_t)want * sizeof(float)));
     h->cfg = *cfg;  // the allocation now has this shape
     return 0;
 }
 
 // Views of the uploaded parameters, carved like assign_weights
 // (src/model.c:54-83), and their device table for the persistent decode.
-int params_commit(cngpt_hip_ctx* h, const cngpt_hip_config* cfg, bool same_shape) {
+int params_commit(cngpt_hip_ctx* h, const cngpt_hip_config* cfg) {
     h->cfg = *cfg;
     h->n_params = params_of(cfg);
     const long C = cfg->n_embd, V = cfg->vocab_size, T = cfg->block_size;
@@ -800,17 +805,8 @@ int params_commit(cngpt_hip_ctx* h, const cngpt_hip_config* cfg, bool same_shape
     }
     h->lnf_w = p; p += C;
     h->lnf_b = p;
-    const size_t lbytes = (size_t)cfg->n_layer * sizeof(LayerW);
-    if (!same_shape || !h->d_layers) {
-        if (h->d_layers) HIP_TRY(hipFree(h->d_layers));
-        h->d_layers = nullptr;
-        if (hipMalloc(&h->d_layers, lbytes) != hipSuccess) {
-            (void)hipGetLastError();
-            h->d_layers = nullptr;
-            return fail("layer table allocation failed");
-        }
-    }
-    HIP_TRY(hipMemcpy(h->d_layers, h->layers.data(), lbytes, hipMemcpyHostToDevice));
+    HIP_TRY(hipMemcpy(h->d_layers, h->layers.data(), (size_t)cfg->n_layer * sizeof(LayerW),
+                      hipMemcpyHostToDevice));
     h->have_params = true;
     return 0;
 }
@@ -996,7 +992,6 @@ void cngpt_hip_destroy(cngpt_hip_ctx* h) {
     for (hipEvent_t e : h->pool) (void)hipEventDestroy(e);
     if (h->d_act) (void)hipFree(h->d_act);
     if (h->d_params) (void)hipFree(h->d_params);
-    if (h->d_layers) (void)hipFree(h->d_layers);
     if (h->stream) (void)hipStreamDestroy(h->stream);
     delete h;
 }
@@ -1008,12 +1003,11 @@ int cngpt_hip_load_params(cngpt_hip_ctx* h, const cngpt_hip_config* cfg, const f
     const long want = cngpt_hip_num_params(cfg);
     if (!params || n_params != want)
         return fail("parameter count %ld does not match the shape (%ld)", n_params, want);
-    bool same_shape = false;
-    if (params_prepare(h, cfg, &same_shape)) return -1;
+    if (params_prepare(h, cfg)) return -1;
     HIP_TRY(hipMemcpyAsync(h->d_params, params, (size_t)want * sizeof(float),
                            hipMemcpyHostToDevice, h->stream));
     HIP_TRY(hipStreamSynchronize(h->stream));
-    return params_commit(h, cfg, same_shape);
+    return params_commit(h, cfg);
 }
 
 int cngpt_hip_file_config(const char* path, cngpt_hip_config* cfg, long* n_params) {
@@ -1029,9 +1023,8 @@ int cngpt_hip_load_file(cngpt_hip_ctx* h, const char* path, cngpt_hip_config* cf
     if (!h) return fail("null handle");
     WeightFile wf;
     if (open_weight_file(path, &wf)) return -1;
-    bool same_shape = false;
     int rc = check_shape(&wf.cfg);
-    if (!rc) rc = params_prepare(h, &wf.cfg, &same_shape);
+    if (!rc) rc = params_prepare(h, &wf.cfg);
     if (!rc) rc = stream_to_device(h, wf, path);
     close(wf.fd);
     if (rc) {
@@ -1039,7 +1032,7 @@ int cngpt_hip_load_file(cngpt_hip_ctx* h, const char* path, cngpt_hip_config* cf
         h->have_params = false;
         return -1;
     }
-    if (params_commit(h, &wf.cfg, same_shape)) return -1;
+    if (params_commit(h, &wf.cfg)) return -1;
     if (cfg_out) *cfg_out = wf.cfg;
     return 0;
 }

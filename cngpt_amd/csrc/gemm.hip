@@ -489,8 +489,11 @@ __global__ void __launch_bounds__(256) k_stream_reduce(GemmArgs a, int KS) {
 // The same sum for one row per workgroup (float4 columns tid + 256 i),
 // then the LayerNorm (reference ops.c:191-248) of the finished row into
 // a.ln_out: the residual stream and the next product's input in one pass.
+// Only the residual epilogue forms a LayerNorm (the residual stream feeds the
+// next sub-layer); rows of up to 2048 floats (NCH = 1 or 2 float4 per thread).
 template <int EPI, int NCH>
 __global__ void __launch_bounds__(256) k_stream_reduce_ln(GemmArgs a, int KS) {
+    static_assert(EPI == EPI_RESID && (NCH == 1 || NCH == 2), "residual rows of <= 2048 floats");
     __shared__ float red[4];
     const int r = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int N4 = a.N >> 2;
@@ -569,12 +572,13 @@ hipError_t stream_mb(const GemmArgs& a, hipStream_t s) {
         if (!a.ln_out) return e;
         return launch_layernorm(a.Y, a.ldy, a.ln_w, a.ln_b, a.ln_out, a.N, a.M, a.N, s);
     }
-    if (a.ln_out) {
-        const int n4 = a.N / 4;
-        if (n4 <= 256) k_stream_reduce_ln<EPI, 1><<<a.M, 256, 0, s>>>(a, KS);
-        else if (n4 <= 512) k_stream_reduce_ln<EPI, 2><<<a.M, 256, 0, s>>>(a, KS);
-        else k_stream_reduce_ln<EPI, 4><<<a.M, 256, 0, s>>>(a, KS);
-        return hipGetLastError();
+    if constexpr (EPI == EPI_RESID) {
+        // launch_gemm admits ln_out for the residual epilogue and N <= 2048 only
+        if (a.ln_out) {
+            if (a.N <= 1024) k_stream_reduce_ln<EPI, 1><<<a.M, 256, 0, s>>>(a, KS);
+            else k_stream_reduce_ln<EPI, 2><<<a.M, 256, 0, s>>>(a, KS);
+            return hipGetLastError();
+        }
     }
     k_stream_reduce<EPI><<<(unsigned)(((long)a.M * a.N + 255) / 256), 256, 0, s>>>(a, KS);
     return hipGetLastError();
@@ -632,8 +636,9 @@ hipError_t gemm_epi(const GemmArgs& a, hipStream_t s) {
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
     if (a.M <= 0 || a.N <= 0) return hipSuccess;
     if (a.K <= 0 || (a.K & 3)) return hipErrorInvalidValue;
-    if (a.ln_out && (a.seg || a.row_off || a.row_off_dev || (a.N & 3) || a.N > 4096 || !a.ln_w ||
-                     !a.ln_b))
+    // the LayerNorm rows are written and read with 16-byte accesses
+    if (a.ln_out && (a.epi != EPI_RESID || a.seg || a.row_off || a.row_off_dev || (a.N & 3) ||
+                     (a.ldy & 3) || a.N > 2048 || !a.ln_w || !a.ln_b))
         return hipErrorInvalidValue;
     if (a.M <= SKINNY_MAX_M) {
         switch (a.epi) {

@@ -30,9 +30,10 @@ struct GemmArgs {
     int epi;                   // EpiMode
     float* part;               // split-K partials of M <= SKINNY_MAX_M (NULL: no split)
     long part_cap;             // floats available at part
-    // Optional (seg = 0, no row offsets): also the LayerNorm of every output
-    // row with gains ln_w and biases ln_b into ln_out (rows of N floats),
-    // formed while the split-K partials are summed when K is split.
+    // Optional (EPI_RESID, seg = 0, no row offsets, N <= 2048, N and ldy
+    // multiples of 4): also the LayerNorm of every output row with gains
+    // ln_w and biases ln_b into ln_out (rows of N floats), formed while the
+    // split-K partials are summed when K is split.
     const float* ln_w;
     const float* ln_b;
     float* ln_out;

@@ -11,9 +11,15 @@
  *                              and stays valid until the next call; NULL on
  *                              failure (fast_last_error() says why)
  *
- * FastCtx differs inside (callers never read its fields, src/cngpt.c and
- * tests/check_fast.c only pass it around): it holds the device handle and a
- * pinned host buffer for the returned logits.
+ * FastCtx has the reference's size and alignment (two ints and nine
+ * pointers, 80 bytes on LP64), so a caller compiled against the reference's
+ * src/fast.h - whose quote include finds that header first - hands this
+ * library a struct of the right size. B and T sit where the reference keeps
+ * them and `logits` (the buffer the last call returned) at the offset of the
+ * reference's `logits`; the other slots hold the device handle and the
+ * parameter-upload cache instead of host scratch. Callers never read the
+ * other fields (src/cngpt.c and tests/check_fast.c only pass the struct
+ * around).
  *
  * One deliberate divergence from the reference: the reference reads
  * m->params on every call; this context copies them to the device on the
@@ -31,14 +37,29 @@
 
 typedef struct {
     int    B, T;              /* shape of the last call */
-    float *logits;            /* [B, V] host (pinned), owned by the context */
-    size_t logits_cap;        /* floats the logits buffer holds */
     void  *dev;               /* cngpt_hip_ctx * */
     const float *params_seen; /* parameter upload cache key */
-    int    n_params_seen;
+    size_t logits_cap;        /* floats the logits buffer holds */
     GPTConfig cfg_seen;
+    int    n_params_seen;
     int    params_dirty;
+    void  *reserved;
+    float *logits;            /* [B, V] host (pinned), owned by the context */
 } FastCtx;
+
+/* The reference's layout: int B, T; then x, ln, qkv, scores, aout, hid,
+ * mean, rstd, logits (src/fast.h:35-45). */
+#ifdef __cplusplus
+static_assert(sizeof(FastCtx) == 2 * sizeof(int) + 9 * sizeof(void *), "FastCtx size");
+static_assert(alignof(FastCtx) == alignof(void *), "FastCtx alignment");
+static_assert(offsetof(FastCtx, logits) == 2 * sizeof(int) + 8 * sizeof(void *),
+              "FastCtx logits offset");
+#else
+_Static_assert(sizeof(FastCtx) == 2 * sizeof(int) + 9 * sizeof(void *), "FastCtx size");
+_Static_assert(_Alignof(FastCtx) == _Alignof(void *), "FastCtx alignment");
+_Static_assert(offsetof(FastCtx, logits) == 2 * sizeof(int) + 8 * sizeof(void *),
+               "FastCtx logits offset");
+#endif
 
 #ifdef __cplusplus
 extern "C" {

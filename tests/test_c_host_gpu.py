@@ -7,12 +7,23 @@ import pytest
 
 pytestmark = pytest.mark.gpu
 
-BIN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "c", "check_fast_hip")
+CDIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "c")
 
 
-def test_check_fast_hip_binary():
-    assert os.path.exists(BIN), "tests/c/check_fast_hip not built (run __graft_entry__.build())"
-    r = subprocess.run([BIN], capture_output=True, text=True, timeout=120)
+def _run(name):
+    path = os.path.join(CDIR, name)
+    assert os.path.exists(path), f"tests/c/{name} not built (run __graft_entry__.build())"
+    r = subprocess.run([path], capture_output=True, text=True, timeout=120)
     print(r.stdout, r.stderr, flush=True)
     assert r.returncode == 0, r.stderr
     assert "0 failed" in r.stdout
+
+
+def test_check_fast_hip_binary():
+    _run("check_fast_hip")
+
+
+def test_reference_layout_fastctx():
+    """The library driven through the reference's 80-byte FastCtx
+    (src/fast.h:35-45), guard bytes on both sides."""
+    _run("check_refctx")
