@@ -120,7 +120,7 @@ def gelu_through(kat, x, path):
     return gemm(kat, X, W, np.zeros(1, np.float32), M, 1, 4, 2, path)[:, 0]
 
 
-@pytest.mark.parametrize("path,M", LINEAR_PATHS)
+@pytest.mark.parametrize("path,M", [(1, 4), (0, 4), (0, 130)])
 def test_gelu_known_answer(kat, path, M):
     """check_ops.c:146-157: gelu(0) = 0 (1e-4), gelu(1) = 0.8413,
     gelu(-1) = -0.1587, gelu(2) = 1.9545 (1e-3)."""
@@ -171,9 +171,13 @@ def test_softmax_known_answer(kat, kind):
 # ------------------------------------------------------------------ error bounds
 
 def gelu64(x):
+    """0.5 x (1 + tanh v) in float64 as x expit(2v) (1 + tanh v = 2 expit(2v)
+    exactly; scipy's expit keeps full relative precision where float64's
+    1 + tanh(v) cancels to zero, v < -19)."""
+    from scipy.special import expit
     x = x.astype(np.float64)
     v = np.sqrt(2 / np.pi) * (x + 0.044715 * x ** 3)
-    return 0.5 * x * (1 + np.tanh(v)), v
+    return x * expit(2 * v), v
 
 
 @pytest.mark.parametrize("path", [0, 1])
