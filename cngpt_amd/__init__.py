@@ -76,7 +76,8 @@ EXPORTS = [
     "cngpt_hip_last_error", "cngpt_hip_create", "cngpt_hip_destroy", "cngpt_hip_num_params",
     "cngpt_hip_load_params", "cngpt_hip_file_config", "cngpt_hip_load_file",
     "cngpt_hip_reserve", "cngpt_hip_forward",
-    "cngpt_hip_upload_tokens", "cngpt_hip_forward_resident", "cngpt_hip_synchronize",
+    "cngpt_hip_upload_tokens", "cngpt_hip_forward_resident", "cngpt_hip_forward_noalloc",
+    "cngpt_hip_synchronize",
     "cngpt_hip_read_logits", "cngpt_hip_logits_device", "cngpt_hip_cross_entropy",
     "cngpt_hip_upload_targets", "cngpt_hip_cross_entropy_resident", "cngpt_hip_read_loss",
     "cngpt_hip_decode_begin",
@@ -113,6 +114,8 @@ def lib():
     L.cngpt_hip_forward.argtypes = [_VP, _I, ctypes.c_int, ctypes.c_int, ctypes.c_int, _F]
     L.cngpt_hip_upload_tokens.argtypes = [_VP, _I, ctypes.c_int, ctypes.c_int]
     L.cngpt_hip_forward_resident.argtypes = [_VP, ctypes.c_int, ctypes.c_int, ctypes.c_int]
+    L.cngpt_hip_forward_noalloc.argtypes = [_VP, _VP, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                            _VP, _VP]
     L.cngpt_hip_synchronize.argtypes = [_VP]
     L.cngpt_hip_read_logits.argtypes = [_VP, ctypes.c_size_t, ctypes.c_size_t, _F]
     L.cngpt_hip_logits_device.argtypes = [_VP]
@@ -288,6 +291,13 @@ class Model:
 
     def forward_resident(self, B: int, T: int, mode: int = LAST) -> None:
         _check(lib().cngpt_hip_forward_resident(self._h, B, T, mode), "forward_resident")
+
+    def forward_noalloc(self, tokens_dev: int, B: int, T: int, mode: int, logits_dev: int,
+                        err_dev: int | None = None) -> None:
+        """cngpt_hip_forward_noalloc: device tokens [B, T] -> device logits,
+        activations in the library's scratch (no allocation); enqueued."""
+        _check(lib().cngpt_hip_forward_noalloc(self._h, tokens_dev, B, T, mode, logits_dev,
+                                               err_dev), "forward_noalloc")
 
     def synchronize(self) -> None:
         _check(lib().cngpt_hip_synchronize(self._h), "synchronize")

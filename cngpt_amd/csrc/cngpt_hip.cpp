@@ -21,6 +21,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <thread>
 #include <vector>
 
@@ -58,6 +59,47 @@ constexpr size_t ALIGN = 256;
 // split-K partials of the products over <= 64 rows (16 MB)
 constexpr long GEMM_PART_FLOATS = 1l << 22;
 size_t align_up(size_t n) { return (n + ALIGN - 1) & ~(ALIGN - 1); }
+
+// Scratch of cngpt_hip_forward_noalloc: every activation of one forward
+// (64 MiB: the B*T rows of x, ln, qkv, aout and hid, the B gathered rows,
+// the attention split partials and the split-K partials). Each device the
+// library runs on holds its own copy from the first use until the process
+// ends. Host code never uses the array's name as an address: it is a
+// host-side stand-in; the device address of each device's copy comes from
+// hipGetSymbolAddress, once per device, in cngpt_hip_create.
+constexpr long SCRATCH_FLOATS = 16l << 20;
+__device__ __align__(256) float scratch[SCRATCH_FLOATS];
+
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+float* g_scratch[MAX_DEVICES];  // device address of `scratch`, per device
+
+// With `device` current: look up and keep its address of the scratch array.
+int scratch_setup(int device) {
+    if (device < 0 || device >= MAX_DEVICES) return 0;  // the no-alloc entry refuses such devices
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch[device]) return 0;
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+        (void)hipGetLastError();
+        return fail("scratch address on device %d: %s", device, hipGetErrorString(e));
+    }
+    g_scratch[device] = (float*)p;
+    return 0;
+}
+
+float* scratch_of(int device) {
+    if (device < 0 || device >= MAX_DEVICES) return nullptr;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    return g_scratch[device];
+}
+
+// Zeroes n ints with a kernel (a memset node in a captured graph is avoided).
+__global__ void k_zero_i32(int* p, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0;
+}
 
 }  // namespace
 
@@ -714,6 +756,7 @@ int need_params(const cngpt_hip_ctx* h) {
 }
 
 int check_dev_err(cngpt_hip_ctx* h) {
+    if (!h->dev_err) return 0;  // no activation arena yet: nothing has flagged
     int e = 0;
     HIP_TRY(hipMemcpyAsync(&e, h->dev_err, sizeof(int), hipMemcpyDeviceToHost, h->stream));
     HIP_TRY(hipStreamSynchronize(h->stream));
@@ -950,6 +993,64 @@ int stream_to_device(cngpt_hip_ctx* h, const WeightFile& wf, const char* path) {
     return rc;
 }
 
+// The buffers enqueue_forward reads and writes, so that one forward can run
+// on another set (the no-alloc scratch) and the handle's own come back
+// afterwards, together with the state of its held logits.
+struct FwdBufs {
+    int *tok, *dev_err;
+    float *x, *ln, *qkv, *aout, *hid, *logits, *xc, *lnc, *aoutc, *hidc, *attn_part, *gemm_part;
+    int attn_splits;
+    int curB, curT, curMode;
+    size_t logits_count;
+    bool prof;
+};
+
+FwdBufs fwd_bufs(const cngpt_hip_ctx* h) {
+    return FwdBufs{h->tok, h->dev_err, h->x, h->ln, h->qkv, h->aout, h->hid, h->logits, h->xc,
+                   h->lnc, h->aoutc, h->hidc, h->attn_part, h->gemm_part, h->attn_splits,
+                   h->curB, h->curT, h->curMode, h->logits_count, h->prof};
+}
+
+void set_fwd_bufs(cngpt_hip_ctx* h, const FwdBufs& f) {
+    h->tok = f.tok; h->dev_err = f.dev_err;
+    h->x = f.x; h->ln = f.ln; h->qkv = f.qkv; h->aout = f.aout; h->hid = f.hid;
+    h->logits = f.logits;
+    h->xc = f.xc; h->lnc = f.lnc; h->aoutc = f.aoutc; h->hidc = f.hidc;
+    h->attn_part = f.attn_part; h->gemm_part = f.gemm_part; h->attn_splits = f.attn_splits;
+    h->curB = f.curB; h->curT = f.curT; h->curMode = f.curMode;
+    h->logits_count = f.logits_count;
+    h->prof = f.prof;
+}
+
+// Carve of the scratch for a forward of B x T: floats from `base` (a null
+// base only counts them). Regions start on 256-byte boundaries.
+long carve_scratch(const cngpt_hip_config& c, int B, int T, float* base, FwdBufs* f) {
+    const long C = c.n_embd, H = c.n_head, hs = C / H, rows = (long)B * T;
+    const int kps = attn_dec_keys_per_split((int)hs);
+    const int splits = (T + kps - 1) / kps;
+    long off = 0;
+    auto take = [&](long n) {
+        float* r = base ? base + off : nullptr;
+        off += (n + 63) / 64 * 64;
+        return r;
+    };
+    float* err = take(1);
+    f->x = take(rows * C);
+    f->ln = take(rows * C);
+    f->qkv = take(rows * 3 * C);
+    f->aout = take(rows * C);
+    f->hid = take(rows * 4 * C);
+    f->xc = take(B * C);
+    f->lnc = take(B * C);
+    f->aoutc = take(B * C);
+    f->hidc = take(B * 4 * C);
+    f->attn_part = take((long)B * H * splits * (hs + 4));
+    f->attn_splits = splits;
+    f->gemm_part = take(GEMM_PART_FLOATS);
+    f->dev_err = (int*)err;
+    return off;
+}
+
 }  // namespace
 
 // ==================================================================== C ABI
@@ -970,6 +1071,7 @@ int cngpt_hip_create(int device, cngpt_hip_ctx** out) {
     HIP_TRY(hipGetDeviceCount(&n));
     if (device < 0 || device >= n) return fail("device %d not present (%d devices)", device, n);
     HIP_TRY(hipSetDevice(device));
+    if (scratch_setup(device)) return -1;
     cngpt_hip_ctx* h = new cngpt_hip_ctx();
     h->device = device;
     const char* g = getenv("CNGPT_HIP_GRAPH");
@@ -1066,6 +1168,36 @@ int cngpt_hip_forward_resident(cngpt_hip_ctx* h, int B, int T, int mode) {
     HIP_TRY(hipSetDevice(h->device));
     h->kvB = h->kvLen = 0;
     return enqueue_forward(h, B, T, mode, false, false);
+}
+
+int cngpt_hip_forward_noalloc(cngpt_hip_ctx* h, const int* tokens, int B, int T, int mode,
+                              float* logits, int* err) {
+    if (need_params(h)) return -1;
+    if (mode != CNGPT_LAST && mode != CNGPT_ALL) return fail("bad mode %d", mode);
+    if (!tokens || !logits) return fail("forward_noalloc: null device pointer");
+    if (B <= 0 || T <= 0) return fail("B=%d T=%d must be positive", B, T);
+    if (T > h->cfg.block_size) return fail("T=%d exceeds block_size %d", T, h->cfg.block_size);
+    FwdBufs f{};
+    const long need = carve_scratch(h->cfg, B, T, nullptr, &f);
+    if (need > SCRATCH_FLOATS)
+        return fail("forward_noalloc: B=%d T=%d needs %ld floats of scratch; it holds %ld "
+                    "(%ld MiB)", B, T, need, SCRATCH_FLOATS, SCRATCH_FLOATS * 4 >> 20);
+    float* base = scratch_of(h->device);
+    if (!base) return fail("forward_noalloc: no scratch address for device %d", h->device);
+    HIP_TRY(hipSetDevice(h->device));
+    carve_scratch(h->cfg, B, T, base, &f);
+    f.tok = const_cast<int*>(tokens);  // read only (token ids of the embedding)
+    if (err) f.dev_err = err;
+    f.logits = logits;
+    f.prof = false;  // no timing events: their pool may grow
+    // the token-range flag starts at zero (a kernel: callers may capture this)
+    k_zero_i32<<<1, 64, 0, h->stream>>>(f.dev_err, 1);
+    HIP_TRY(hipGetLastError());
+    const FwdBufs saved = fwd_bufs(h);
+    set_fwd_bufs(h, f);
+    const int rc = enqueue_forward(h, B, T, mode, false, false);
+    set_fwd_bufs(h, saved);
+    return rc;
 }
 
 int cngpt_hip_forward(cngpt_hip_ctx* h, const int* tokens, int B, int T, int mode,

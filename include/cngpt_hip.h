@@ -116,6 +116,23 @@ int  cngpt_hip_forward(cngpt_hip_ctx *h, const int *tokens, int B, int T, int mo
 int  cngpt_hip_upload_tokens(cngpt_hip_ctx *h, const int *tokens, int B, int T);
 int  cngpt_hip_forward_resident(cngpt_hip_ctx *h, int B, int T, int mode);
 int  cngpt_hip_synchronize(cngpt_hip_ctx *h);
+/* Forward pass that allocates nothing: no reference counterpart; for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). Same kernels and
+ * results as cngpt_hip_forward_resident, but tokens [B, T] (device int32,
+ * ids in [0, vocab_size)) and logits (device; [B, V] for CNGPT_LAST,
+ * [B, T, V] for CNGPT_ALL) are the caller's, and every activation lives in a
+ * 64 MiB scratch array of the library that each device holds from its first
+ * use until the process ends (a 1024-token window of GPT-2 small or medium
+ * fits; larger B * T * n_embd is refused with an error). Needs parameters
+ * (cngpt_hip_load_params or _load_file) but no cngpt_hip_reserve. Enqueues
+ * on the handle's stream and returns without waiting. Token ids outside
+ * [0, vocab_size) are clamped and set *err (device int, may be NULL), which
+ * the call zeroes first. All calls on one device share its scratch and it
+ * keeps the last call's contents: calls that overlap on one device (other
+ * handles, other streams) race. */
+int  cngpt_hip_forward_noalloc(cngpt_hip_ctx *h, const int *tokens, int B, int T, int mode,
+                               float *logits, int *err);
 /* Copy count floats of the logits, starting at float offset, to host. */
 int  cngpt_hip_read_logits(cngpt_hip_ctx *h, size_t offset, size_t count, float *dst);
 /* Device address of the logits of the last forward / decode step. */
