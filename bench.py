@@ -195,6 +195,19 @@ def reference_shape(m: cngpt_amd.Model, iters: int = 20):
             "published_cpu": "Ryzen 5 7600, 6 threads, OpenBLAS 0.3.29 (reference README.md:415)"}
 
 
+def dp_share(m: cngpt_amd.Model, cfg, steps: int = 10, warmup: int = 2):
+    """One GPU's share of the B=16 T=1024 workload under 8-way sequence
+    sharding: B=2, T=1024 (M = 2048 rows, where the products have too few
+    128 x 128 tiles to fill the CUs without splitting K)."""
+    dt, prof = prefill(m, cfg, 2, 1024, steps, warmup)
+    g = prof["gemm"]
+    return {"B": 2, "T": 1024, "tok_s": round(2 * 1024 * steps / dt, 1),
+            "ms_per_forward": round(dt * 1e3 / steps, 3),
+            "gemm_tflops": round(g["flops"] / (g["ms"] * 1e-3) / 1e12, 2),
+            "gemm_frac": round(g["flops"] / (g["ms"] * 1e-3) / PEAK_FP32_MFMA, 4),
+            "gemm_ms_per_forward": round(g["ms"] / steps, 3)}
+
+
 def cpu_baseline(name: str, cfg, params, budget_s: float):
     """The oracle (C restatement of the reference's gpt_forward_fast with
     OpenBLAS, one pinned thread per physical core) on a bounded sample of the
@@ -319,6 +332,7 @@ def main():
     draws = np.random.default_rng(7).random((dsteps + 1) * dB).astype(np.float32)
     samp_dt, _ = decode(m, cfg, dB, prompt, dsteps, draws)
     ref_shape = reference_shape(m) if name == "small" else None
+    share = dp_share(m, cfg) if name == "small" else None
     load = load_leg(m, cfg, params)
     m.close()
 
@@ -378,6 +392,8 @@ def main():
     }
     if ref_shape:
         line["reference_shape"] = ref_shape
+    if share:
+        line["dp_share"] = share
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(name, cfg, params, args.cpu_budget)
     if args.copy_calibration:

@@ -56,18 +56,19 @@ struct ProfRec {
 };
 
 constexpr size_t ALIGN = 256;
-// split-K partials of the products over <= 64 rows (16 MB)
-constexpr long GEMM_PART_FLOATS = 1l << 22;
+// split-K partials of the few-row products and of the tile launches too
+// small to fill the CUs (32 MB)
+constexpr long GEMM_PART_FLOATS = 1l << 23;
 size_t align_up(size_t n) { return (n + ALIGN - 1) & ~(ALIGN - 1); }
 
 // Scratch of cngpt_hip_forward_noalloc: every activation of one forward
-// (64 MiB: the B*T rows of x, ln, qkv, aout and hid, the B gathered rows,
+// (96 MiB: the B*T rows of x, ln, qkv, aout and hid, the B gathered rows,
 // the attention split partials and the split-K partials). Each device the
 // library runs on holds its own copy from the first use until the process
 // ends. Host code never uses the array's name as an address: it is a
 // host-side stand-in; the device address of each device's copy comes from
 // hipGetSymbolAddress, once per device, in cngpt_hip_create.
-constexpr long SCRATCH_FLOATS = 16l << 20;
+constexpr long SCRATCH_FLOATS = 24l << 20;
 __device__ __align__(256) float scratch[SCRATCH_FLOATS];
 
 constexpr int MAX_DEVICES = 64;
@@ -254,10 +255,17 @@ int run_gemm(cngpt_hip_ctx* h, const float* X, const float* W, const float* bias
     a.row_off = row_off; a.row_off_dev = row_off_dev;
     a.epi = epi;
     a.part = h->gemm_part; a.part_cap = GEMM_PART_FLOATS;
-    a.ln_w = lnw; a.ln_b = lnb; a.ln_out = lnout;
-    Timed t(h, CNGPT_K_GEMM, flops, bytes);
-    HIP_TRY(launch_gemm(a, h->stream));
-    return 0;
+    // a split product forms the LayerNorm while it sums its partials;
+    // otherwise the LayerNorm is a launch (and a timing class) of its own
+    const bool ln_in_sum = lnout && launch_gemm_splits(a) > 1;
+    if (ln_in_sum) {
+        a.ln_w = lnw; a.ln_b = lnb; a.ln_out = lnout;
+    }
+    {
+        Timed t(h, CNGPT_K_GEMM, flops, bytes);
+        HIP_TRY(launch_gemm(a, h->stream));
+    }
+    return lnout && !ln_in_sum ? run_ln(h, Y, a.ldy, lnw, lnb, lnout, M) : 0;
 }
 
 int run_ln(cngpt_hip_ctx* h, const float* x, long in_stride, const float* w, const float* b,
@@ -518,12 +526,16 @@ int enqueue_forward(cngpt_hip_ctx* h, int B, int T, int mode, bool kv, bool want
         HIP_TRY(launch_embed(h->tok, h->wte, h->wpe, h->x, rows, T, C, c.vocab_size, 0, nullptr,
                              h->dev_err, nullptr, 0, h->stream));
     }
+    // LayerNorm 1 of layer 0; every later LayerNorm over all rows is formed
+    // by the residual product before it (while it sums its K splits, or in a
+    // launch right after it), into ln
+    if (run_ln(h, h->x, C, h->layers[0].ln1_w, h->layers[0].ln1_b, h->ln, (int)rows)) return -1;
     for (int l = 0; l < L; l++) {
         const LayerW& w = h->layers[l];
         const bool last = (mode == CNGPT_LAST) && (l == L - 1);
         float* qkv = kv ? h->qkv + (size_t)l * B * h->capKV * 3 * C : h->qkv;
-        if (run_ln_gemm(h, h->x, w.ln1_w, w.ln1_b, h->ln, w.attn_w, w.attn_b, qkv, (int)rows,
-                        3 * C, EPI_BIAS, kv ? T : 0, seq_stride, 3L * C))
+        if (run_gemm(h, h->ln, w.attn_w, w.attn_b, qkv, (int)rows, 3 * C, C, EPI_BIAS,
+                     kv ? T : 0, seq_stride, 3L * C))
             return -1;
         if (!last) {
             {
@@ -532,11 +544,16 @@ int enqueue_forward(cngpt_hip_ctx* h, int B, int T, int mode, bool kv, bool want
                 Timed t(h, CNGPT_K_ATTN, fl, by);
                 HIP_TRY(launch_attention_causal(qkv, seq_stride, h->aout, B, T, C, H, h->stream));
             }
-            if (run_gemm(h, h->aout, w.proj_w, w.proj_b, h->x, (int)rows, C, C, EPI_RESID)) return -1;
-            if (run_ln_gemm(h, h->x, w.ln2_w, w.ln2_b, h->ln, w.fc_w, w.fc_b, h->hid, (int)rows,
-                            4 * C, EPI_BIAS_GELU))
-                return -1;
-            if (run_gemm(h, h->hid, w.mlp_w, w.mlp_b, h->x, (int)rows, C, 4 * C, EPI_RESID))
+            // the next LayerNorm after the MLP: layer l+1's first, or the
+            // final one (only in ALL mode, where the last layer is not pruned)
+            const bool end = l + 1 == L;
+            const float* nw = end ? h->lnf_w : h->layers[l + 1].ln1_w;
+            const float* nb = end ? h->lnf_b : h->layers[l + 1].ln1_b;
+            if (run_gemm(h, h->aout, w.proj_w, w.proj_b, h->x, (int)rows, C, C, EPI_RESID, 0, 0,
+                         -1, 0, nullptr, w.ln2_w, w.ln2_b, h->ln) ||
+                run_gemm(h, h->ln, w.fc_w, w.fc_b, h->hid, (int)rows, 4 * C, C, EPI_BIAS_GELU) ||
+                run_gemm(h, h->hid, w.mlp_w, w.mlp_b, h->x, (int)rows, C, 4 * C, EPI_RESID, 0, 0,
+                         -1, 0, nullptr, nw, nb, h->ln))
                 return -1;
         } else {
             // Last layer, LAST mode: the final query row of each sequence only,
@@ -554,7 +571,7 @@ int enqueue_forward(cngpt_hip_ctx* h, int B, int T, int mode, bool kv, bool want
         }
     }
     if (mode == CNGPT_ALL) {
-        if (run_ln(h, h->x, C, h->lnf_w, h->lnf_b, h->ln, (int)rows)) return -1;
+        // ln holds the final LayerNorm of every row (formed by the last proj)
         if (run_gemm(h, h->ln, h->wte, nullptr, h->logits, (int)rows, c.vocab_size, C, EPI_STORE))
             return -1;
         h->logits_count = (size_t)rows * c.vocab_size;

@@ -42,14 +42,16 @@ constexpr int BM = 128, BN = 128;
 constexpr int NTHREADS = 256;
 
 // Workgroups are dispatched round-robin over the 8 XCDs (pid % 8). Renumber
-// them so that each XCD receives a contiguous run of tile ids, then order
-// tiles in groups of 8 M-tiles so neighbours share A rows and W rows in the
-// XCD's L2.
-__device__ __forceinline__ void tile_coords(int pid, int tiles_m, int tiles_n, int& tm, int& tn) {
-    const int nt = tiles_m * tiles_n;
+// them so that each XCD receives a contiguous run of work ids (of nt).
+__device__ __forceinline__ int xcd_order(int pid, int nt) {
     const int per = nt / 8, rem = nt % 8;
     const int xcd = pid % 8, idx = pid / 8;
-    int p = (xcd < rem) ? xcd * (per + 1) + idx : rem * (per + 1) + (xcd - rem) * per + idx;
+    return (xcd < rem) ? xcd * (per + 1) + idx : rem * (per + 1) + (xcd - rem) * per + idx;
+}
+
+// Tile of work id p: tiles in groups of 8 M-tiles, so that neighbours share
+// A rows and W rows in the XCD's L2.
+__device__ __forceinline__ void group_coords(int p, int tiles_m, int tiles_n, int& tm, int& tn) {
     const int GM = 8;
     const int group = p / (GM * tiles_n);
     const int first_m = group * GM;
@@ -57,6 +59,10 @@ __device__ __forceinline__ void tile_coords(int pid, int tiles_m, int tiles_n, i
     const int in_group = p % (GM * tiles_n);
     tm = first_m + in_group % gsize;
     tn = in_group / gsize;
+}
+
+__device__ __forceinline__ void tile_coords(int pid, int tiles_m, int tiles_n, int& tm, int& tn) {
+    group_coords(xcd_order(pid, tiles_m * tiles_n), tiles_m, tiles_n, tm, tn);
 }
 
 // Epilogue of one wavefront's 64 x 64 block at (r0, c0): acc[i][j][r] is
@@ -147,8 +153,14 @@ __device__ __forceinline__ void tile_store(const GemmArgs& a, const f32x16 (&acc
 // at row g / GPR, slot g % GPR, where slot s of row r holds k quad
 // s ^ ((r / RSW) % GPR) (RSW = rows per 256 bytes). The MFMA order over k
 // is that of k_gemm with the same BK, so both give the same bits.
+//
+// Split K (KS > 1, for launches with too few tiles to fill the CUs): work id
+// ks * tiles + tile covers k in [ks * KR, min(K, (ks + 1) * KR)) and stores
+// its partial tile to a.part + ks * M * N (rows of N floats); the reduce
+// kernel sums the KS partials in order and applies the epilogue.
 template <int EPI, int BK, int S, int OCC>
-__global__ void __launch_bounds__(NTHREADS, OCC) k_gemm_dl(GemmArgs a, int tiles_m, int tiles_n) {
+__global__ void __launch_bounds__(NTHREADS, OCC) k_gemm_dl(GemmArgs a, int tiles_m, int tiles_n,
+                                                          int KR, int KS) {
     constexpr int GPR = BK / 4;      // granules per row
     constexpr int RSW = 16 / GPR;    // rows per 256 bytes
     constexpr int NI = GPR / 2;      // load instructions per operand per stage per wavefront
@@ -157,12 +169,17 @@ __global__ void __launch_bounds__(NTHREADS, OCC) k_gemm_dl(GemmArgs a, int tiles
     static_assert(BM == BN && BM * GPR == NI * 4 * 64, "one granule per lane per instruction");
     __shared__ __attribute__((aligned(1024))) float sm[S * 2 * TILE];
 
+    const int tiles = tiles_m * tiles_n;
+    int p = xcd_order(blockIdx.x, tiles * KS);
+    const int ks = p / tiles;
+    p -= ks * tiles;
     int tm, tn;
-    tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+    group_coords(p, tiles_m, tiles_n, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int K = a.K;
+    const int kb = ks * KR;
 
     // granule (i * 4 + wave) * 64 + lane of each operand, every stage
     const float* xp[NI];
@@ -171,8 +188,8 @@ __global__ void __launch_bounds__(NTHREADS, OCC) k_gemm_dl(GemmArgs a, int tiles
     for (int i = 0; i < NI; i++) {
         const int g = (i * 4 + wave) * 64 + lane;
         const int row = g / GPR, kq = (g % GPR) ^ ((row / RSW) % GPR);
-        xp[i] = a.X + (long)min(m0 + row, a.M - 1) * K + 4 * kq;
-        wp[i] = a.W + (long)min(n0 + row, a.N - 1) * K + 4 * kq;
+        xp[i] = a.X + (long)min(m0 + row, a.M - 1) * K + kb + 4 * kq;
+        wp[i] = a.W + (long)min(n0 + row, a.N - 1) * K + kb + 4 * kq;
     }
     auto issue = [&](int kt, int st) {
         float* base = sm + st * 2 * TILE;
@@ -205,7 +222,7 @@ __global__ void __launch_bounds__(NTHREADS, OCC) k_gemm_dl(GemmArgs a, int tiles
             bo[i][g] = TILE + rb * BK + 4 * (kq ^ ((rb / RSW) % GPR));
         }
 
-    const int nk = K / BK;
+    const int nk = min(KR, K - kb) / BK;
 #pragma unroll
     for (int st = 0; st < S - 1; st++)
         if (st < nk) issue(st, st);
@@ -239,7 +256,17 @@ __global__ void __launch_bounds__(NTHREADS, OCC) k_gemm_dl(GemmArgs a, int tiles
         }
     }
 
-    tile_store<EPI>(a, acc, m0 + wm, n0 + wn, lane);
+    if (KS == 1) {
+        tile_store<EPI>(a, acc, m0 + wm, n0 + wn, lane);
+        return;
+    }
+    GemmArgs pa = a;
+    pa.Y = a.part + (long)ks * a.M * a.N;
+    pa.ldy = a.N;
+    pa.seg = 0;
+    pa.row_off = 0;
+    pa.row_off_dev = nullptr;
+    tile_store<EPI_STORE>(pa, acc, m0 + wm, n0 + wn, lane);
 }
 
 template <int EPI, int BK, int PAD, int OCC>
@@ -555,23 +582,11 @@ __global__ void __launch_bounds__(256) k_stream_reduce_ln(GemmArgs a, int KS) {
     }
 }
 
-// Split K until the column tiles times the splits reach two workgroups per
-// CU (the partials must fit a.part_cap floats; ranges are whole chunks).
-template <int EPI, int MB>
-hipError_t stream_mb(const GemmArgs& a, hipStream_t s) {
-    const int tiles_n = (a.N + ST_NT - 1) / ST_NT;
-    const int kchunks = (a.K + ST_KC - 1) / ST_KC;
-    int KS = a.part ? std::max(1, std::min((512 + tiles_n - 1) / tiles_n, kchunks)) : 1;
-    while (KS > 1 && (long)KS * a.M * a.N > a.part_cap) KS--;
-    const int KR = ((kchunks + KS - 1) / KS) * ST_KC;
-    KS = (a.K + KR - 1) / KR;
-    k_stream<EPI, MB><<<tiles_n * KS, ST_NW * 64, 0, s>>>(a, tiles_n, KR, KS);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    if (KS == 1) {
-        if (!a.ln_out) return e;
-        return launch_layernorm(a.Y, a.ldy, a.ln_w, a.ln_b, a.ln_out, a.N, a.M, a.N, s);
-    }
+// After a launch whose KS K-splits left partials in a.part: Y = epi(their
+// sum in split order), and with a.ln_out the LayerNorm of each row formed
+// in the same pass (residual products, rows <= 2048 floats).
+template <int EPI>
+hipError_t reduce_splits(const GemmArgs& a, int KS, hipStream_t s) {
     if constexpr (EPI == EPI_RESID) {
         // launch_gemm admits ln_out for the residual epilogue and N <= 2048 only
         if (a.ln_out) {
@@ -582,6 +597,35 @@ hipError_t stream_mb(const GemmArgs& a, hipStream_t s) {
     }
     k_stream_reduce<EPI><<<(unsigned)(((long)a.M * a.N + 255) / 256), 256, 0, s>>>(a, KS);
     return hipGetLastError();
+}
+
+// Without splits the LayerNorm of the finished rows is a launch of its own.
+hipError_t ln_after(const GemmArgs& a, hipStream_t s) {
+    if (!a.ln_out) return hipSuccess;
+    return launch_layernorm(a.Y, a.ldy, a.ln_w, a.ln_b, a.ln_out, a.N, a.M, a.N, s);
+}
+
+// Split K until the column tiles times the splits reach two workgroups per
+// CU (the partials must fit a.part_cap floats; ranges are whole chunks):
+// returns the splits, *KR the k per split.
+int stream_splits(const GemmArgs& a, int* KR) {
+    const int tiles_n = (a.N + ST_NT - 1) / ST_NT;
+    const int kchunks = (a.K + ST_KC - 1) / ST_KC;
+    int KS = a.part ? std::max(1, std::min((512 + tiles_n - 1) / tiles_n, kchunks)) : 1;
+    while (KS > 1 && (long)KS * a.M * a.N > a.part_cap) KS--;
+    *KR = ((kchunks + KS - 1) / KS) * ST_KC;
+    return (a.K + *KR - 1) / *KR;
+}
+
+template <int EPI, int MB>
+hipError_t stream_mb(const GemmArgs& a, hipStream_t s) {
+    const int tiles_n = (a.N + ST_NT - 1) / ST_NT;
+    int KR;
+    const int KS = stream_splits(a, &KR);
+    k_stream<EPI, MB><<<tiles_n * KS, ST_NW * 64, 0, s>>>(a, tiles_n, KR, KS);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    return KS == 1 ? ln_after(a, s) : reduce_splits<EPI>(a, KS, s);
 }
 
 template <int EPI>
@@ -612,26 +656,59 @@ double round_fill(int tiles, int res) {
 // BK = 16 at 3 per CU when that fills its last round; else BK = 32 at 2
 // per CU, whose longer K steps hold up best when a round is left
 // part-empty.
+//
+// Launches of fewer than 384 tiles (M up to ~2048 rows: short prefills, the
+// reference's own B=1 T=128 shape, one GPU's share of a batch) split K over
+// the 2 x 256 workgroup slots of the BK = 32 variant: KS splits of at least
+// two K steps each, tiles * KS <= 512 so that they run in one round, and the
+// partials within a.part_cap; then reduce_splits.
+// Returns the splits, *KR the k per split (whole K steps).
+int tile_splits(const GemmArgs& a, int tiles, int* KR) {
+    const int cus = 256;
+    *KR = a.K;
+    if (!a.part || a.K % 32 || tiles >= 384) return 1;
+    int ks = std::min(a.K / 64, (2 * cus) / tiles);
+    while (ks > 1 && (long)ks * a.M * a.N > a.part_cap) ks--;
+    if (ks <= 1) return 1;
+    *KR = (a.K / 32 + ks - 1) / ks * 32;
+    return (a.K + *KR - 1) / *KR;
+}
+
 template <int EPI>
 hipError_t gemm_epi(const GemmArgs& a, hipStream_t s) {
     const int tiles_m = (a.M + BM - 1) / BM, tiles_n = (a.N + BN - 1) / BN;
     const int tiles = tiles_m * tiles_n, cus = 256;
+    int KR;
+    const int KS = tile_splits(a, tiles, &KR);
+    if (KS > 1) {
+        k_gemm_dl<EPI, 32, 2, 2><<<tiles * KS, NTHREADS, 0, s>>>(a, tiles_m, tiles_n, KR, KS);
+        const hipError_t e = hipGetLastError();
+        return e != hipSuccess ? e : reduce_splits<EPI>(a, KS, s);
+    }
     if (a.K % 32 == 0 && tiles > 2 * cus && tiles <= 4 * cus && round_fill(tiles, 2 * cus) < 0.9)
-        k_gemm_dl<EPI, 16, 2, 4><<<tiles, NTHREADS, 0, s>>>(a, tiles_m, tiles_n);
+        k_gemm_dl<EPI, 16, 2, 4><<<tiles, NTHREADS, 0, s>>>(a, tiles_m, tiles_n, a.K, 1);
     else if (a.K % 32 == 0)
-        k_gemm_dl<EPI, 32, 2, 2><<<tiles, NTHREADS, 0, s>>>(a, tiles_m, tiles_n);
+        k_gemm_dl<EPI, 32, 2, 2><<<tiles, NTHREADS, 0, s>>>(a, tiles_m, tiles_n, a.K, 1);
     else if (a.K % 16 == 0)
-        k_gemm_dl<EPI, 16, 3, 3><<<tiles, NTHREADS, 0, s>>>(a, tiles_m, tiles_n);
+        k_gemm_dl<EPI, 16, 3, 3><<<tiles, NTHREADS, 0, s>>>(a, tiles_m, tiles_n, a.K, 1);
     else if (tiles <= 4 * cus || round_fill(tiles, 4 * cus) >= 0.9)
         k_gemm<EPI, 16, 4, 4><<<tiles, NTHREADS, 0, s>>>(a, tiles_m, tiles_n);
     else if (round_fill(tiles, 3 * cus) >= 0.9)
         k_gemm<EPI, 16, 8, 3><<<tiles, NTHREADS, 0, s>>>(a, tiles_m, tiles_n);
     else
         k_gemm<EPI, 32, 4, 2><<<tiles, NTHREADS, 0, s>>>(a, tiles_m, tiles_n);
-    return hipGetLastError();
+    const hipError_t e = hipGetLastError();
+    return e != hipSuccess ? e : ln_after(a, s);
 }
 
 }  // namespace
+
+int launch_gemm_splits(const GemmArgs& a) {
+    if (a.M <= 0 || a.N <= 0 || a.K <= 0 || (a.K & 3)) return 1;
+    int KR;
+    if (a.M <= SKINNY_MAX_M) return stream_splits(a, &KR);
+    return tile_splits(a, ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN), &KR);
+}
 
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
     if (a.M <= 0 || a.N <= 0) return hipSuccess;
@@ -649,13 +726,11 @@ hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
         }
         return hipErrorInvalidValue;
     }
-    hipError_t e = hipErrorInvalidValue;
     switch (a.epi) {
-        case EPI_STORE: e = gemm_epi<EPI_STORE>(a, s); break;
-        case EPI_BIAS: e = gemm_epi<EPI_BIAS>(a, s); break;
-        case EPI_BIAS_GELU: e = gemm_epi<EPI_BIAS_GELU>(a, s); break;
-        case EPI_RESID: e = gemm_epi<EPI_RESID>(a, s); break;
+        case EPI_STORE: return gemm_epi<EPI_STORE>(a, s);
+        case EPI_BIAS: return gemm_epi<EPI_BIAS>(a, s);
+        case EPI_BIAS_GELU: return gemm_epi<EPI_BIAS_GELU>(a, s);
+        case EPI_RESID: return gemm_epi<EPI_RESID>(a, s);
     }
-    if (e != hipSuccess || !a.ln_out) return e;
-    return launch_layernorm(a.Y, a.ldy, a.ln_w, a.ln_b, a.ln_out, a.N, a.M, a.N, s);
+    return hipErrorInvalidValue;
 }

@@ -28,7 +28,8 @@ struct GemmArgs {
     int row_off;               // added to every output row index
     const int* row_off_dev;    // if set, *row_off_dev is added too (decode position)
     int epi;                   // EpiMode
-    float* part;               // split-K partials of M <= SKINNY_MAX_M (NULL: no split)
+    float* part;               // split-K partials (NULL: no split) of the few-row
+                               // products and of tile launches too small to fill the CUs
     long part_cap;             // floats available at part
     // Optional (EPI_RESID, seg = 0, no row offsets, N <= 2048, N and ldy
     // multiples of 4): also the LayerNorm of every output row with gains
@@ -42,6 +43,9 @@ struct GemmArgs {
 // 128 x 128 MFMA tiles.
 constexpr int SKINNY_MAX_M = 64;
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t s);
+// Number of K splits launch_gemm uses for a (1: none; then a LayerNorm
+// asked for with ln_out is a launch of its own after the product).
+int launch_gemm_splits(const GemmArgs& a);
 
 // decode.hip
 // Partials of the split one-query attention, merged by their consumer:

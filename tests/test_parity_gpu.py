@@ -158,6 +158,29 @@ def test_gpt2_small_b16_t1024(small):
                 what=f"ALL seq {b}")
 
 
+def test_gpt2_small_split_k_shapes(small):
+    """Products with too few 128 x 128 tiles to fill the CUs split K and sum
+    the partials in order (forming the next LayerNorm in the same pass for
+    the residual products): the reference's own shape B=1 T=128 (M = 128:
+    6 to 24 tiles per product), one GPU's share of the B=16 workload, B=2
+    T=1024 (M = 2048: c_proj and proj 96 tiles), and B=3 T=200."""
+    cfg, params, m = small
+    V = cfg.vocab_size
+    for B, T, seed in ((1, 128, 5), (3, 200, 6), (2, 1024, 7)):
+        tk = oracle.lcg_tokens(B * T, V, seed=seed).reshape(B, T)
+        say(f"small B={B} T={T} LAST")
+        compare(m.forward(tk, cngpt_amd.LAST), oracle.forward(ocfg(cfg), params, tk),
+                what=f"B={B} T={T} LAST")
+        say(f"small B={B} T={T} ALL, last sequence")
+        m.reserve(B, T, cngpt_amd.ALL)
+        m.upload_tokens(tk)
+        m.forward_resident(B, T, cngpt_amd.ALL)
+        m.synchronize()
+        got = m.read_logits((B - 1) * T * V, T * V).reshape(1, T, V)
+        compare(got, oracle.forward(ocfg(cfg), params, tk[B - 1:], oracle.ALL),
+                what=f"B={B} T={T} ALL")
+
+
 def test_gpt2_small_b17_t512(small):
     """8704 rows: 68 row tiles leave the last round of the QKV (1224 tiles)
     and fc (1632 tiles) products under 90 % full at 4 and at 3 workgroups
