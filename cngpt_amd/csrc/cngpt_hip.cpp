@@ -57,18 +57,19 @@ struct ProfRec {
 
 constexpr size_t ALIGN = 256;
 // split-K partials of the few-row products and of the tile launches too
-// small to fill the CUs (32 MB)
-constexpr long GEMM_PART_FLOATS = 1l << 23;
+// small to fill the CUs, and the stream-K partial tiles (two per workgroup,
+// 512 workgroups): 64 MB
+constexpr long GEMM_PART_FLOATS = 1l << 24;
 size_t align_up(size_t n) { return (n + ALIGN - 1) & ~(ALIGN - 1); }
 
 // Scratch of cngpt_hip_forward_noalloc: every activation of one forward
-// (96 MiB: the B*T rows of x, ln, qkv, aout and hid, the B gathered rows,
+// (128 MiB: the B*T rows of x, ln, qkv, aout and hid, the B gathered rows,
 // the attention split partials and the split-K partials). Each device the
 // library runs on holds its own copy from the first use until the process
 // ends. Host code never uses the array's name as an address: it is a
 // host-side stand-in; the device address of each device's copy comes from
 // hipGetSymbolAddress, once per device, in cngpt_hip_create.
-constexpr long SCRATCH_FLOATS = 24l << 20;
+constexpr long SCRATCH_FLOATS = 32l << 20;
 __device__ __align__(256) float scratch[SCRATCH_FLOATS];
 
 constexpr int MAX_DEVICES = 64;

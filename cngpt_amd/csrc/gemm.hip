@@ -149,37 +149,38 @@ __device__ __forceinline__ void tile_store(const GemmArgs& a, const f32x16 (&acc
         }
 }
 
+// One output element of row `row` (mapped through seg / row offsets) with
+// the epilogue.
+template <int EPI>
+__device__ __forceinline__ void store_out(const GemmArgs& a, long roff, int row, int col, float v) {
+    long orow = a.seg ? (long)(row / a.seg) * a.seg_stride + row % a.seg : row;
+    orow += roff;
+    float* y = a.Y + orow * a.ldy + col;
+    *y = apply_epi<EPI>(v, a.bias, col, y);
+}
+
 // Stage layout: operand tile of BM rows x BK floats, granule (16 bytes) g
 // at row g / GPR, slot g % GPR, where slot s of row r holds k quad
 // s ^ ((r / RSW) % GPR) (RSW = rows per 256 bytes). The MFMA order over k
 // is that of k_gemm with the same BK, so both give the same bits.
-//
-// Split K (KS > 1, for launches with too few tiles to fill the CUs): work id
-// ks * tiles + tile covers k in [ks * KR, min(K, (ks + 1) * KR)) and stores
-// its partial tile to a.part + ks * M * N (rows of N floats); the reduce
-// kernel sums the KS partials in order and applies the epilogue.
-template <int EPI, int BK, int S, int OCC>
-__global__ void __launch_bounds__(NTHREADS, OCC) k_gemm_dl(GemmArgs a, int tiles_m, int tiles_n,
-                                                          int KR, int KS) {
+template <int BK, int S>
+struct DlSmem {
+    float sm[S * 2 * BM * BK];
+};
+
+// acc = X[m0.., kb..] . W[n0.., kb..]^T over nk steps of BK (acc zeroed
+// first). On return every wavefront is done reading the stages it used only
+// once the caller passes a barrier.
+template <int BK, int S>
+__device__ __forceinline__ void dl_tile(const GemmArgs& a, int m0, int n0, int kb, int nk,
+                                        float* sm, int wave, int lane, f32x16 (&acc)[2][2]) {
     constexpr int GPR = BK / 4;      // granules per row
     constexpr int RSW = 16 / GPR;    // rows per 256 bytes
     constexpr int NI = GPR / 2;      // load instructions per operand per stage per wavefront
     constexpr int NG = BK / 8;       // MFMA groups per step
     constexpr int TILE = BM * BK;    // floats per operand per stage
     static_assert(BM == BN && BM * GPR == NI * 4 * 64, "one granule per lane per instruction");
-    __shared__ __attribute__((aligned(1024))) float sm[S * 2 * TILE];
-
-    const int tiles = tiles_m * tiles_n;
-    int p = xcd_order(blockIdx.x, tiles * KS);
-    const int ks = p / tiles;
-    p -= ks * tiles;
-    int tm, tn;
-    group_coords(p, tiles_m, tiles_n, tm, tn);
-    const int m0 = tm * BM, n0 = tn * BN;
-    const int tid = threadIdx.x;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int K = a.K;
-    const int kb = ks * KR;
 
     // granule (i * 4 + wave) * 64 + lane of each operand, every stage
     const float* xp[NI];
@@ -204,7 +205,6 @@ __global__ void __launch_bounds__(NTHREADS, OCC) k_gemm_dl(GemmArgs a, int tiles
 
     const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
     const int lr = lane & 31, lh = lane >> 5;
-    f32x16 acc[2][2];
 #pragma unroll
     for (int i = 0; i < 2; i++)
 #pragma unroll
@@ -222,7 +222,6 @@ __global__ void __launch_bounds__(NTHREADS, OCC) k_gemm_dl(GemmArgs a, int tiles
             bo[i][g] = TILE + rb * BK + 4 * (kq ^ ((rb / RSW) % GPR));
         }
 
-    const int nk = min(KR, K - kb) / BK;
 #pragma unroll
     for (int st = 0; st < S - 1; st++)
         if (st < nk) issue(st, st);
@@ -255,7 +254,39 @@ __global__ void __launch_bounds__(NTHREADS, OCC) k_gemm_dl(GemmArgs a, int tiles
                                                                           acc[i][j], 0, 0, 0);
         }
     }
+}
 
+// A partial tile (all BM x BN values, rows of BN floats) at p.
+__device__ __forceinline__ void store_partial(float* p, const f32x16 (&acc)[2][2], int wave,
+                                              int lane) {
+    GemmArgs pa{};
+    pa.Y = p;
+    pa.M = BM; pa.N = BN; pa.ldy = BN;
+    tile_store<EPI_STORE>(pa, acc, (wave >> 1) * 64, (wave & 1) * 64, lane);
+}
+
+// One 128 x 128 tile per workgroup. Split K (KS > 1, for launches with too
+// few tiles to fill the CUs): work id ks * tiles + tile covers k in
+// [ks * KR, min(K, (ks + 1) * KR)) and stores its partial tile to a.part +
+// ks * M * N (rows of N floats); the reduce kernel sums the KS partials in
+// order and applies the epilogue.
+template <int EPI, int BK, int S, int OCC>
+__global__ void __launch_bounds__(NTHREADS, OCC) k_gemm_dl(GemmArgs a, int tiles_m, int tiles_n,
+                                                          int KR, int KS) {
+    __shared__ __attribute__((aligned(1024))) DlSmem<BK, S> sh;
+    const int tiles = tiles_m * tiles_n;
+    int p = xcd_order(blockIdx.x, tiles * KS);
+    const int ks = p / tiles;
+    p -= ks * tiles;
+    int tm, tn;
+    group_coords(p, tiles_m, tiles_n, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int kb = ks * KR;
+    f32x16 acc[2][2];
+    dl_tile<BK, S>(a, m0, n0, kb, min(KR, a.K - kb) / BK, sh.sm, wave, lane, acc);
+    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
     if (KS == 1) {
         tile_store<EPI>(a, acc, m0 + wm, n0 + wn, lane);
         return;
@@ -267,6 +298,126 @@ __global__ void __launch_bounds__(NTHREADS, OCC) k_gemm_dl(GemmArgs a, int tiles
     pa.row_off = 0;
     pa.row_off_dev = nullptr;
     tile_store<EPI_STORE>(pa, acc, m0 + wm, n0 + wn, lane);
+}
+
+// Stream-K (launches whose last round of tiles would leave workgroup slots
+// idle): the I = tiles * nkt steps of BK, tile-major, are cut into G equal
+// contiguous ranges, one per workgroup. A workgroup computes the tiles its
+// range covers whole and stores them with the epilogue; the part of a tile
+// at either end of its range goes to a partial slot (2g for the first tile
+// of workgroup g, 2g + 1 for its last), and k_sk_fixup sums each split
+// tile's partials in k order and applies the epilogue. Workgroup ids are
+// renumbered XCD-contiguously and tiles taken in the 8-row groups, so each
+// XCD's workgroups walk neighbouring tiles.
+__device__ __forceinline__ long sk_begin(long g, long I, int G) { return g * I / G; }
+// workgroup whose range holds step i
+__device__ __forceinline__ int sk_owner(long i, long I, int G) {
+    return (int)(((i + 1) * G - 1) / I);
+}
+
+template <int EPI>
+__global__ void __launch_bounds__(NTHREADS, 2) k_gemm_sk(GemmArgs a, int tiles_m, int tiles_n,
+                                                         int nkt, int G) {
+    constexpr int BK = 32, S = 2;
+    __shared__ __attribute__((aligned(1024))) DlSmem<BK, S> sh;
+    const int tiles = tiles_m * tiles_n;
+    const long I = (long)tiles * nkt;
+    const int g = xcd_order(blockIdx.x, G);
+    const long beg = sk_begin(g, I, G), end = sk_begin(g + 1, I, G);
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+    const int first = (int)(beg / nkt);
+    for (long it = beg; it < end;) {
+        const int t = (int)(it / nkt), k0 = (int)(it - (long)t * nkt);
+        const int k1 = (int)min((long)nkt, k0 + (end - it));
+        int tm, tn;
+        group_coords(t, tiles_m, tiles_n, tm, tn);
+        f32x16 acc[2][2];
+        dl_tile<BK, S>(a, tm * BM, tn * BN, k0 * BK, k1 - k0, sh.sm, wave, lane, acc);
+        if (k0 == 0 && k1 == nkt)
+            tile_store<EPI>(a, acc, tm * BM + wm, tn * BN + wn, lane);
+        else
+            store_partial(a.part + (long)(2 * g + (t == first ? 0 : 1)) * BM * BN, acc, wave, lane);
+        it += k1 - k0;
+        // the next tile's first loads overwrite stages this one read
+        __syncthreads();
+    }
+}
+
+// Every tile split over workgroups: its partials summed in k order (the
+// workgroups in order), then the epilogue. SK_RPW rows of a tile per
+// workgroup; tiles that one workgroup computed whole return at once. A tile
+// meets at most SK_SEGS workgroup ranges (each range holds at least nkt / 2
+// steps, since stream-K runs with more tiles than half its workgroups).
+constexpr int SK_RPW = 16;
+constexpr int SK_SEGS = 4;
+template <int EPI>
+__global__ void __launch_bounds__(256) k_sk_fixup(GemmArgs a, int tiles_m, int tiles_n, int nkt,
+                                                  int G) {
+    const int tiles = tiles_m * tiles_n;
+    const long I = (long)tiles * nkt;
+    const int t = blockIdx.x / (BM / SK_RPW), rb = blockIdx.x % (BM / SK_RPW);
+    const int g0 = sk_owner((long)t * nkt, I, G), g1 = sk_owner((long)(t + 1) * nkt - 1, I, G);
+    if (g0 == g1) return;
+    int slot[SK_SEGS];
+    const int ns = min(g1 - g0 + 1, SK_SEGS);
+#pragma unroll
+    for (int q = 0; q < SK_SEGS; q++) {
+        const int g = min(g0 + q, g1);
+        slot[q] = 2 * g + ((int)(sk_begin(g, I, G) / nkt) == t ? 0 : 1);
+    }
+    int tm, tn;
+    group_coords(t, tiles_m, tiles_n, tm, tn);
+    const long roff = a.row_off + (a.row_off_dev ? *a.row_off_dev : 0);
+    // float4 c4 = tid + 256 i of this workgroup's SK_RPW rows: row
+    // rb * SK_RPW + c4 / 32, columns 4 (c4 % 32) ..
+    constexpr int NI = SK_RPW * BN / 4 / 256;
+    f32x4 p[NI][SK_SEGS], old[NI];
+    int row[NI], col[NI];
+    long yo[NI];
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        const int c4 = threadIdx.x + 256 * i;
+        const int r = rb * SK_RPW + (c4 >> 5), c = (c4 & 31) * 4;
+        row[i] = tm * BM + r;
+        col[i] = tn * BN + c;
+#pragma unroll
+        for (int q = 0; q < SK_SEGS; q++)
+            p[i][q] = q < ns ? *(const f32x4*)(a.part + (long)slot[q] * BM * BN + r * BN + c)
+                             : f32x4{0.f, 0.f, 0.f, 0.f};
+        const int rr = min(row[i], a.M - 1);
+        long orow = a.seg ? (long)(rr / a.seg) * a.seg_stride + rr % a.seg : rr;
+        yo[i] = (orow + roff) * a.ldy;
+        if (EPI == EPI_RESID)
+#pragma unroll
+            for (int e = 0; e < 4; e++) old[i][e] = a.Y[yo[i] + min(col[i] + e, a.N - 1)];
+    }
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        f32x4 v = p[i][0];
+        for (int q = 1; q < ns; q++) v += p[i][q];
+        // a tile met by more ranges than SK_SEGS (not produced by the
+        // stream-K launch's shapes) sums the rest here
+        for (int g = g0 + SK_SEGS; g <= g1; g++) {
+            const int sl = 2 * g + ((int)(sk_begin(g, I, G) / nkt) == t ? 0 : 1);
+            const int c4 = threadIdx.x + 256 * i;
+            v += *(const f32x4*)(a.part + (long)sl * BM * BN + (rb * SK_RPW + (c4 >> 5)) * BN +
+                                 (c4 & 31) * 4);
+        }
+        if (row[i] >= a.M) continue;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int c = col[i] + e;
+            if (c < a.N) {
+                float y = v[e];
+                if (EPI == EPI_BIAS) y += a.bias[c];
+                else if (EPI == EPI_BIAS_GELU) y = gelu_tanh(y + a.bias[c]);
+                else if (EPI == EPI_RESID) y = (old[i][e] + y) + a.bias[c];
+                a.Y[yo[i] + c] = y;
+            }
+        }
+    }
 }
 
 template <int EPI, int BK, int PAD, int OCC>
@@ -383,13 +534,6 @@ constexpr int ST_KC = 128;
 constexpr int ST_PF = ST_KC / 16;   // weight steps in flight = steps per chunk
 constexpr int ST_XP = ST_KC + 4;    // padded LDS row (floats)
 
-template <int EPI>
-__device__ __forceinline__ void store_out(const GemmArgs& a, long roff, int row, int col, float v) {
-    long orow = a.seg ? (long)(row / a.seg) * a.seg_stride + row % a.seg : row;
-    orow += roff;
-    float* y = a.Y + orow * a.ldy + col;
-    *y = apply_epi<EPI>(v, a.bias, col, y);
-}
 
 template <int EPI, int MB>
 __global__ void __launch_bounds__(ST_NW * 64) k_stream(GemmArgs a, int tiles_n, int KR, int KS) {
@@ -674,6 +818,21 @@ int tile_splits(const GemmArgs& a, int tiles, int* KR) {
     return (a.K + *KR - 1) / *KR;
 }
 
+// Stream-K instead of whole tiles in rounds of 2 x 256 when the last round
+// would leave more than a tenth of the slots idle (more than 256 tiles, K a
+// multiple of 32, partial slots for every workgroup within a.part_cap):
+// the number of workgroups, 0 for none.
+int sk_workgroups(const GemmArgs& a, int tiles) {
+    const int cus = 256, G = 2 * cus;
+    if (!a.part || a.K % 32 || tiles <= cus) return 0;
+    if (tiles > G && tiles <= 2 * G) return 0;  // one round of the BK = 16 variant
+    const int rounds = (tiles + G - 1) / G;
+    if ((double)tiles / ((double)rounds * G) >= 0.9) return 0;
+    if (2L * G * BM * BN > a.part_cap || (long)tiles * (a.K / 32) < G) return 0;
+    // fewer tiles than slots: one workgroup per CU (half the partial tiles)
+    return tiles < G ? cus : G;
+}
+
 template <int EPI>
 hipError_t gemm_epi(const GemmArgs& a, hipStream_t s) {
     const int tiles_m = (a.M + BM - 1) / BM, tiles_n = (a.N + BN - 1) / BN;
@@ -684,6 +843,14 @@ hipError_t gemm_epi(const GemmArgs& a, hipStream_t s) {
         k_gemm_dl<EPI, 32, 2, 2><<<tiles * KS, NTHREADS, 0, s>>>(a, tiles_m, tiles_n, KR, KS);
         const hipError_t e = hipGetLastError();
         return e != hipSuccess ? e : reduce_splits<EPI>(a, KS, s);
+    }
+    if (const int G = sk_workgroups(a, tiles)) {
+        k_gemm_sk<EPI><<<G, NTHREADS, 0, s>>>(a, tiles_m, tiles_n, a.K / 32, G);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        k_sk_fixup<EPI><<<tiles * (BM / SK_RPW), 256, 0, s>>>(a, tiles_m, tiles_n, a.K / 32, G);
+        e = hipGetLastError();
+        return e != hipSuccess ? e : ln_after(a, s);
     }
     if (a.K % 32 == 0 && tiles > 2 * cus && tiles <= 4 * cus && round_fill(tiles, 2 * cus) < 0.9)
         k_gemm_dl<EPI, 16, 2, 4><<<tiles, NTHREADS, 0, s>>>(a, tiles_m, tiles_n, a.K, 1);

@@ -122,7 +122,7 @@ int  cngpt_hip_synchronize(cngpt_hip_ctx *h);
  * results as cngpt_hip_forward_resident, but tokens [B, T] (device int32,
  * ids in [0, vocab_size)) and logits (device; [B, V] for CNGPT_LAST,
  * [B, T, V] for CNGPT_ALL) are the caller's, and every activation lives in a
- * 96 MiB scratch array of the library that each device holds from its first
+ * 128 MiB scratch array of the library that each device holds from its first
  * use until the process ends (a 1024-token window of GPT-2 small or medium
  * fits; larger B * T * n_embd is refused with an error). Needs parameters
  * (cngpt_hip_load_params or _load_file) but no cngpt_hip_reserve. Enqueues

@@ -75,14 +75,14 @@ int kat_gemm(const float* X, const float* W, const float* bias, float* Y, int M,
     float* dw = d.put(W, (size_t)N * K);
     float* db = d.put(bias, bias ? (size_t)N : 0);
     float* dy = d.put(epi == EPI_RESID ? Y : nullptr, (size_t)M * N);
-    float* part = path == 0 ? d.put<float>(nullptr, 1 << 23) : nullptr;
+    float* part = path == 0 ? d.put<float>(nullptr, 1 << 24) : nullptr;
     if (!dx || !dw || !db || !dy || (path == 0 && !part)) return fail("device allocation failed");
     if (path == 0) {
         GemmArgs a{};
         a.X = dx; a.W = dw; a.bias = db; a.Y = dy;
         a.M = M; a.N = N; a.K = K; a.ldy = N;
         a.epi = epi;
-        a.part = part; a.part_cap = 1 << 23;  // the forward's 32 MB
+        a.part = part; a.part_cap = 1 << 24;  // the forward's 64 MB
         TRY(launch_gemm(a, nullptr));
     } else {
         DecGemvArgs a{};

@@ -239,6 +239,8 @@ def test_softmax_error_bound_dense_grid(kat, kind):
     (0, 257, 129, 768, 3),    # direct-to-LDS BK = 32, residual
     (0, 128, 2304, 768, 1),   # tiles with K split 12 ways (M = 128), in-order reduce
     (0, 2048, 768, 3072, 3),  # tiles with K split 5 ways (M = 2048), residual reduce
+    (0, 2048, 2304, 768, 1),  # stream-K: 288 tiles over 512 workgroups, fixup
+    (0, 1100, 4000, 1600, 3), # stream-K: 9 x 32 ragged tiles, residual
     (0, 37, 100, 3072, 3),    # weight-streaming product, split over K
     (0, 5, 2304, 768, 1),     # weight-streaming, QKV width
     (1, 2, 771, 1024, 3),     # decode product
