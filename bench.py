@@ -67,19 +67,20 @@ def weights(name: str, cfg):
     return p, "N(0,0.02) weights from numpy PCG64 seed 1234"
 
 
-def prefill(m: cngpt_amd.Model, cfg, B: int, T: int, steps: int, warmup: int):
+def prefill(m: cngpt_amd.Model, cfg, B: int, T: int, steps: int, warmup: int,
+            mode: int = cngpt_amd.ALL):
     tokens = lcg_tokens(B * T, cfg.vocab_size, 12345).reshape(B, T)
-    m.reserve(B, T, cngpt_amd.ALL)
+    m.reserve(B, T, mode)
     m.upload_tokens(tokens)
     for _ in range(warmup):
-        m.forward_resident(B, T, cngpt_amd.ALL)
+        m.forward_resident(B, T, mode)
     m.synchronize()
     m.profile_reset()
     m.profile(True)
     m.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
-        m.forward_resident(B, T, cngpt_amd.ALL)
+        m.forward_resident(B, T, mode)
     m.synchronize()
     dt = time.perf_counter() - t0
     m.profile(False)
@@ -208,16 +209,17 @@ def dp_share(m: cngpt_amd.Model, cfg, steps: int = 10, warmup: int = 2):
             "gemm_ms_per_forward": round(g["ms"] / steps, 3)}
 
 
-def cpu_baseline(name: str, cfg, params, budget_s: float):
+def cpu_baseline(name: str, cfg, params, budget_s: float, B: int, T: int):
     """The oracle (C restatement of the reference's gpt_forward_fast with
-    OpenBLAS, one pinned thread per physical core) on a bounded sample of the
-    same workload: B=1 sequences of T=1024 tokens, all-position logits."""
+    OpenBLAS, one pinned thread per physical core) on the workload itself:
+    B x T tokens, all-position logits, one warm-up forward and then as many
+    timed forwards as fit the budget (at least one)."""
     import oracle
 
     ocfg = oracle.Cfg(cfg.n_layer, cfg.n_head, cfg.n_embd, cfg.vocab_size, cfg.block_size)
     cores = oracle.set_threads(0)
-    tk = lcg_tokens(1024, cfg.vocab_size, 12345).reshape(1, 1024)
-    oracle.forward(ocfg, params, tk, oracle.ALL)            # warm-up
+    tk = lcg_tokens(B * T, cfg.vocab_size, 12345).reshape(B, T)
+    oracle.forward(ocfg, params, tk, oracle.ALL)            # warm-up (first touch)
     n, t0 = 0, time.perf_counter()
     while True:
         oracle.forward(ocfg, params, tk, oracle.ALL)
@@ -225,15 +227,16 @@ def cpu_baseline(name: str, cfg, params, budget_s: float):
         dt = time.perf_counter() - t0
         if dt >= budget_s or n >= 20:
             break
-    tok_s = n * 1024 / dt
+    tok_s = n * B * T / dt
     # the reference's own semantics: final-position logits (gpt_forward_fast)
     t1 = time.perf_counter()
     oracle.forward(ocfg, params, tk, oracle.LAST)
     last_s = time.perf_counter() - t1
     return {"value": round(tok_s, 2), "unit": "tokens/s", "cores": cores, "kind": "port",
-            "sample": f"{n} forward(s) of B=1 x T=1024 {NAMES[name]} fp32, all-position logits "
-                      f"({dt:.1f} s); oracle C restatement of fast.c + {oracle.blas_info()}",
-            "last_position_tok_s": round(1024 / last_s, 2)}
+            "sample": f"{n} timed forward(s) of the workload itself, B={B} x T={T} {NAMES[name]} "
+                      f"fp32, all-position logits ({dt:.1f} s, after one warm-up forward); oracle "
+                      f"C restatement of fast.c + {oracle.blas_info()}",
+            "last_position_tok_s": round(B * T / last_s, 2)}
 
 
 def copy_calibration(nbytes: int) -> int:
@@ -269,6 +272,11 @@ def main():
                     help="also run one plain device copy of this size (counter calibration)")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the decode legs (for kernel traces of the decode step)")
+    ap.add_argument("--prefill", type=int, nargs=2, metavar=("B", "T"), default=None,
+                    help="only time all-position forwards of B x T tokens of the workload's "
+                         "model (for kernel traces of one prefill shape)")
+    ap.add_argument("--last", action="store_true",
+                    help="with --prefill: final-position logits (gpt_forward_fast's mode)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); "
@@ -281,6 +289,23 @@ def main():
         dsteps = args.decode_steps
     params, data = weights(name, cfg)
     m = cngpt_amd.Model(cfg, params)
+
+    if args.prefill:
+        pB, pT = args.prefill
+        mode = cngpt_amd.LAST if args.last else cngpt_amd.ALL
+        dt, prof = prefill(m, cfg, pB, pT, args.steps, args.warmup, mode)
+        g = prof["gemm"]
+        m.close()
+        print(json.dumps({"workload": name, "B": pB, "T": pT,
+                          "logits": "final position" if args.last else "all positions",
+                          "tok_s": round(pB * pT * args.steps / dt, 1),
+                          "ms_per_forward": round(dt * 1e3 / args.steps, 3),
+                          "gemm_tflops": round(g["flops"] / (g["ms"] * 1e-3) / 1e12, 2),
+                          "gemm_frac": round(g["flops"] / (g["ms"] * 1e-3) / PEAK_FP32_MFMA, 4),
+                          "kernel_ms_per_forward": {k: round(v["ms"] / args.steps, 3)
+                                                    for k, v in prof.items() if v["launches"]}}),
+              flush=True)
+        return
 
     if args.decode_only:
         dec_dt, dec_path = decode(m, cfg, dB, prompt, dsteps)
@@ -338,11 +363,15 @@ def main():
 
     # HBM-side bytes per GEMM launch from the committed rocprofv3 --pmc
     # summary of this workload (FETCH_SIZE + WRITE_SIZE, calibrated).
-    traffic = None
+    # (not measured in this run: rocprofv3 counters need a profiler run of
+    # their own; the file names the commit and date of the kernels it read)
+    traffic, tsrc = None, None
     tpath = os.path.join(ROOT, "profiles", "gemm_traffic.json")
     if name == "small" and os.path.exists(tpath):
         with open(tpath) as f:
-            traffic = json.load(f).get("measured_bytes_per_launch")
+            tj = json.load(f)
+        traffic = tj.get("measured_bytes_per_launch")
+        tsrc = {k: tj.get(k) for k in ("source", "kernels_commit", "measured_on")}
 
     line = {
         "metric": f"forward tokens/sec + GEMM MFMA util %, {NAMES[name]} fp32 B={B} T={T}; "
@@ -366,6 +395,7 @@ def main():
                      "peak": PEAK_FP32_MFMA / 1e12, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_FP32_MFMA, 4), "traffic": traffic,
                      "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE+WRITE_SIZE)",
+                     "traffic_source": tsrc,
                      "kernel": "k_gemm (all MFMA linear layers + lm_head)",
                      "avg_launch_ms": round(gemm_ms_avg, 4),
                      "launches": g["launches"], "share_of_step": round(gemm_share, 4)},
@@ -395,7 +425,7 @@ def main():
     if share:
         line["dp_share"] = share
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(name, cfg, params, args.cpu_budget)
+        line["cpu_baseline"] = cpu_baseline(name, cfg, params, args.cpu_budget, B, T)
     if args.copy_calibration:
         line["copy_calibration_bytes"] = copy_calibration(args.copy_calibration << 20)
     print(json.dumps(line), flush=True)
