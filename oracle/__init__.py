@@ -117,6 +117,20 @@ def lib():
     L.orc_cross_entropy.restype = ctypes.c_float
     L.orc_srand.argtypes = [ctypes.c_uint]
     L.orc_rand_uniform.restype = ctypes.c_float
+    i = ctypes.c_int
+    L.orc_linear_bwd_dx.argtypes = [_F, _F, _F, i, i, i]
+    L.orc_linear_bwd_dw.argtypes = [_F, _F, _F, _F, i, i, i]
+    L.orc_layernorm_bwd.argtypes = [_F, _F, _F, _F, _F, _F, _F, _F, i, i]
+    L.orc_gelu_bwd.argtypes = [_F, _F, _F, i]
+    L.orc_train_new.argtypes = [ctypes.POINTER(OrcCfg), i, i]
+    L.orc_train_new.restype = ctypes.c_void_p
+    L.orc_train_free.argtypes = [ctypes.c_void_p]
+    L.orc_train_forward.argtypes = [ctypes.c_void_p, _F, _I, _I]
+    L.orc_train_forward.restype = ctypes.c_float
+    L.orc_train_backward.argtypes = [ctypes.c_void_p, _F, _I, _I, _F]
+    L.orc_adamw.argtypes = [ctypes.POINTER(OrcCfg), _F, _F, _F, _F, i, ctypes.c_float,
+                            ctypes.c_float, ctypes.c_float, ctypes.c_float, ctypes.c_float,
+                            ctypes.c_float]
     blas = os.environ.get("CNGPT_ORACLE_BLAS") or find_openblas()
     if blas and blas != "builtin":
         L.orc_use_blas(blas.encode())
@@ -266,3 +280,97 @@ def lcg_tokens(n: int, vocab: int, seed: int = 12345) -> np.ndarray:
         s = (s * 1664525 + 1013904223) & 0xFFFFFFFF
         out[i] = (s >> 8) % vocab
     return out
+
+
+# ---------------------------------------------------------------- training
+
+def linear_bwd_dx(dY, W, dX=None):
+    """linear_bwd_dx (src/ops.c:125-133): dX [M,K] += dY [M,N] . W [N,K]."""
+    dY = np.ascontiguousarray(dY, np.float32)
+    W = np.ascontiguousarray(W, np.float32)
+    M, N = dY.shape
+    K = W.shape[1]
+    dX = np.zeros((M, K), np.float32) if dX is None else np.array(dX, np.float32, order="C")
+    lib().orc_linear_bwd_dx(_fp(dY), _fp(W), _fp(dX), M, K, N)
+    return dX
+
+
+def linear_bwd_dw(dY, X, dW=None, db=None):
+    """linear_bwd_dw (src/ops.c:135-153): dW [N,K] += dY^T X, db += sum_rows dY."""
+    dY = np.ascontiguousarray(dY, np.float32)
+    X = np.ascontiguousarray(X, np.float32)
+    M, N = dY.shape
+    K = X.shape[1]
+    dW = np.zeros((N, K), np.float32) if dW is None else np.array(dW, np.float32, order="C")
+    db = np.zeros(N, np.float32) if db is None else np.array(db, np.float32, order="C")
+    lib().orc_linear_bwd_dw(_fp(dY), _fp(X), _fp(dW), _fp(db), M, K, N)
+    return dW, db
+
+
+def layernorm_bwd(dout, x, w, mean, rstd):
+    """layernorm_bwd (src/ops.c:250-331) into zeroed dx, dw, db."""
+    dout = np.ascontiguousarray(dout, np.float32)
+    x = np.ascontiguousarray(x, np.float32)
+    T, C = x.shape
+    dx = np.zeros_like(x)
+    dw = np.zeros(C, np.float32)
+    db = np.zeros(C, np.float32)
+    lib().orc_layernorm_bwd(_fp(dout), _fp(x), _fp(np.ascontiguousarray(w, np.float32)),
+                            _fp(np.ascontiguousarray(mean, np.float32)),
+                            _fp(np.ascontiguousarray(rstd, np.float32)), _fp(dx), _fp(dw),
+                            _fp(db), T, C)
+    return dx, dw, db
+
+
+def gelu_bwd(dout, x):
+    """gelu_bwd (src/ops.c:382-422) into a zeroed dx."""
+    dout = np.ascontiguousarray(dout, np.float32)
+    x = np.ascontiguousarray(x, np.float32)
+    dx = np.zeros_like(x)
+    lib().orc_gelu_bwd(_fp(dout), _fp(x), _fp(dx), x.size)
+    return dx
+
+
+class Trainer:
+    """The reference's training step on the CPU: gpt_forward with targets,
+    gpt_backward and gpt_adamw (src/model.c:442-921), over params, grads, m,
+    v arrays of the flat layout."""
+
+    def __init__(self, cfg: Cfg, params: np.ndarray, B: int, T: int):
+        self.cfg, self.B, self.T = cfg, B, T
+        self.params = np.array(params, np.float32, order="C")
+        n = self.params.size
+        self.grads = np.zeros(n, np.float32)
+        self.m = np.zeros(n, np.float32)
+        self.v = np.zeros(n, np.float32)
+        self.step = 0
+        self._t = lib().orc_train_new(ctypes.byref(cfg.c()), B, T)
+        if not self._t:
+            raise ValueError("orc_train_new failed")
+
+    def close(self):
+        if getattr(self, "_t", None):
+            lib().orc_train_free(self._t)
+            self._t = None
+
+    def __del__(self):
+        self.close()
+
+    def zero_grad(self):                                # model.c:879-886
+        self.grads[:] = 0
+
+    def forward(self, tokens, targets) -> float:        # model.c:442-625
+        tokens = np.ascontiguousarray(tokens, np.int32).reshape(-1)
+        targets = np.ascontiguousarray(targets, np.int32).reshape(-1)
+        self._tok, self._tgt = tokens, targets
+        return float(lib().orc_train_forward(self._t, _fp(self.params), _ip(tokens), _ip(targets)))
+
+    def backward(self):                                 # model.c:634-877
+        lib().orc_train_backward(self._t, _fp(self.params), _ip(self._tok), _ip(self._tgt),
+                                 _fp(self.grads))
+
+    def adamw(self, lr, beta1=0.9, beta2=0.95, eps=1e-8, wd=0.1, grad_clip=1.0):
+        self.step += 1                                  # model.c:888-921
+        lib().orc_adamw(ctypes.byref(self.cfg.c()), _fp(self.params), _fp(self.grads),
+                        _fp(self.m), _fp(self.v), self.step, lr, beta1, beta2, eps, wd,
+                        grad_clip)

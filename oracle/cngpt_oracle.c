@@ -114,6 +114,30 @@ static void sgemm(int tb, int M, int N, int K, float alpha,
         builtin_sgemm(tb, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc);
 }
 
+/* C = alpha * op(A) * op(B) + beta * C with either operand transposed (the
+ * backward's products, src/ops.c:125-153 and src/model.c:768-799). */
+static void sgemm_t(int ta, int tb, int M, int N, int K, float alpha,
+                    const float *A, int lda, const float *B, int ldb,
+                    float beta, float *C, int ldc)
+{
+    if (M <= 0 || N <= 0) return;
+    if (g_sgemm) {
+        g_sgemm(ROW_MAJOR, ta, tb, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc);
+        return;
+    }
+    for (int i = 0; i < M; i++)
+        for (int j = 0; j < N; j++) {
+            float s = 0.0f;
+            for (int k = 0; k < K; k++) {
+                const float a = ta == TRANS ? A[(size_t)k * lda + i] : A[(size_t)i * lda + k];
+                const float b = tb == TRANS ? B[(size_t)j * ldb + k] : B[(size_t)k * ldb + j];
+                s += a * b;
+            }
+            float *c = C + (size_t)i * ldc + j;
+            *c = alpha * s + (beta == 0.0f ? 0.0f : beta * *c);
+        }
+}
+
 /* ------------------------------------------------------------------ */
 /* Parameters: count, layout, seeded init                              */
 /* ------------------------------------------------------------------ */
@@ -526,4 +550,375 @@ float orc_cross_entropy(const float *logits, const int *targets, float *probs,
         loss -= term;
     }
     return loss / (float)BT;                              /* ops.c:573 */
+}
+
+/* ------------------------------------------------------------------ */
+/* Training: gpt_forward with targets, gpt_backward, gpt_adamw         */
+/* (src/model.c:442-921) and the backward ops of src/ops.c, scalar     */
+/* paths. Dropout 0, the default of `cngpt train` (src/cngpt.c:94).    */
+/* ------------------------------------------------------------------ */
+
+void orc_linear_bwd_dx(const float *dY, const float *W, float *dX, int M, int K, int N)
+{                                                       /* ops.c:125-133 */
+    /* dX [M,K] += dY [M,N] . W [N,K] */
+    sgemm_t(NO_TRANS, NO_TRANS, M, K, N, 1.0f, dY, N, W, K, 1.0f, dX, K);
+}
+
+void orc_linear_bwd_dw(const float *dY, const float *X, float *dW, float *db, int M, int K, int N)
+{                                                       /* ops.c:135-153 */
+    /* dW [N,K] += dY^T [N,M] . X [M,K] */
+    sgemm_t(TRANS, NO_TRANS, N, K, M, 1.0f, dY, N, X, K, 1.0f, dW, K);
+    if (db)
+        for (int i = 0; i < M; i++)
+            for (int j = 0; j < N; j++) db[j] += dY[(size_t)i * N + j];
+}
+
+void orc_layernorm_bwd(const float *dout, const float *x, const float *w, const float *mean,
+                       const float *rstd, float *dx, float *dw, float *db, int T, int C)
+{                                                       /* ops.c:310-331 (scalar path) */
+    for (int t = 0; t < T; t++) {
+        const float *doutr = dout + (size_t)t * C;
+        const float *xr = x + (size_t)t * C;
+        float *dxr = dx + (size_t)t * C;
+        const float m = mean[t], rs = rstd[t];
+        float sum1 = 0.0f, sum2 = 0.0f;
+        for (int c = 0; c < C; c++) {
+            const float xhat = (xr[c] - m) * rs;
+            const float dn = doutr[c] * w[c];
+            sum1 += dn;
+            sum2 += dn * xhat;
+        }
+        sum1 /= (float)C;
+        sum2 /= (float)C;
+        for (int c = 0; c < C; c++) {
+            const float xhat = (xr[c] - m) * rs;
+            const float dn = doutr[c] * w[c];
+            dxr[c] += rs * (dn - sum1 - xhat * sum2);
+            dw[c] += doutr[c] * xhat;
+            db[c] += doutr[c];
+        }
+    }
+}
+
+static inline float gelu_grad1(float x)                 /* ops.c:347-355 */
+{
+    const float x3 = x * x * x;
+    const float inner = 0.7978845608028654f * (x + 0.044715f * x3);
+    const float tv = tanhf(inner);
+    const float sech2 = 1.0f - tv * tv;
+    const float dinner = 0.7978845608028654f * (1.0f + 3.0f * 0.044715f * x * x);
+    return 0.5f * (1.0f + tv) + 0.5f * x * sech2 * dinner;
+}
+
+void orc_gelu_bwd(const float *dout, const float *x, float *dx, int n)
+{                                                       /* ops.c:382-422 (scalar path) */
+    for (int i = 0; i < n; i++) dx[i] += dout[i] * gelu_grad1(x[i]);
+}
+
+/* Activations gpt_forward keeps for gpt_backward (GPTActivations,
+ * src/model.h:86-115), for one B x T shape. */
+struct orc_train {
+    orc_cfg c;
+    int B, T;
+    float *emb, *ln_f_out, *ln_f_mean, *ln_f_rstd, *logits, *probs;
+    float **ln1_out, **ln1_mean, **ln1_rstd, **qkv, **attn_probs, **attn_out, **attn_proj;
+    float **res1, **ln2_out, **ln2_mean, **ln2_rstd, **fc_out, **gelu, **mlp_out, **res2;
+};
+
+static float **alloc_layers(int L, size_t n, int *ok)
+{
+    float **p = calloc((size_t)L, sizeof(float *));
+    if (!p) { *ok = 0; return NULL; }
+    for (int l = 0; l < L; l++)
+        if (!(p[l] = malloc(n * sizeof(float)))) *ok = 0;
+    return p;
+}
+
+static void free_layers(float **p, int L)
+{
+    if (!p) return;
+    for (int l = 0; l < L; l++) free(p[l]);
+    free(p);
+}
+
+void orc_train_free(orc_train *t)
+{
+    if (!t) return;
+    const int L = t->c.n_layer;
+    free(t->emb); free(t->ln_f_out); free(t->ln_f_mean); free(t->ln_f_rstd);
+    free(t->logits); free(t->probs);
+    float **all[] = { t->ln1_out, t->ln1_mean, t->ln1_rstd, t->qkv, t->attn_probs, t->attn_out,
+                      t->attn_proj, t->res1, t->ln2_out, t->ln2_mean, t->ln2_rstd, t->fc_out,
+                      t->gelu, t->mlp_out, t->res2 };
+    for (size_t i = 0; i < sizeof(all) / sizeof(all[0]); i++) free_layers(all[i], L);
+    free(t);
+}
+
+orc_train *orc_train_new(const orc_cfg *c, int B, int T)
+{                                                       /* model.c:333-440 */
+    if (!c || B <= 0 || T <= 0 || T > c->block_size || c->n_embd % c->n_head) return NULL;
+    orc_train *t = calloc(1, sizeof(*t));
+    if (!t) return NULL;
+    t->c = *c;
+    t->B = B;
+    t->T = T;
+    const int L = c->n_layer, C = c->n_embd, H = c->n_head;
+    const size_t N = (size_t)B * T, V = (size_t)c->vocab_size;
+    int ok = 1;
+    t->emb = malloc(N * C * sizeof(float));
+    t->ln_f_out = malloc(N * C * sizeof(float));
+    t->ln_f_mean = malloc(N * sizeof(float));
+    t->ln_f_rstd = malloc(N * sizeof(float));
+    t->logits = malloc(N * V * sizeof(float));
+    t->probs = malloc(N * V * sizeof(float));
+    ok = t->emb && t->ln_f_out && t->ln_f_mean && t->ln_f_rstd && t->logits && t->probs;
+    t->ln1_out = alloc_layers(L, N * C, &ok);
+    t->ln1_mean = alloc_layers(L, N, &ok);
+    t->ln1_rstd = alloc_layers(L, N, &ok);
+    t->qkv = alloc_layers(L, N * 3 * C, &ok);
+    t->attn_probs = alloc_layers(L, (size_t)B * H * T * T, &ok);
+    t->attn_out = alloc_layers(L, N * C, &ok);
+    t->attn_proj = alloc_layers(L, N * C, &ok);
+    t->res1 = alloc_layers(L, N * C, &ok);
+    t->ln2_out = alloc_layers(L, N * C, &ok);
+    t->ln2_mean = alloc_layers(L, N, &ok);
+    t->ln2_rstd = alloc_layers(L, N, &ok);
+    t->fc_out = alloc_layers(L, N * 4 * C, &ok);
+    t->gelu = alloc_layers(L, N * 4 * C, &ok);
+    t->mlp_out = alloc_layers(L, N * C, &ok);
+    t->res2 = alloc_layers(L, N * C, &ok);
+    if (!ok) { orc_train_free(t); return NULL; }
+    return t;
+}
+
+/* linear_fwd (ops.c:109-123): Y = X . W^T, then b added row by row. */
+static void linear_seq(const float *X, const float *W, const float *b, float *Y, int M, int K,
+                       int N)
+{
+    sgemm(TRANS, M, N, K, 1.0f, X, K, W, K, 0.0f, Y, N);
+    if (b)
+        for (int i = 0; i < M; i++)
+            for (int j = 0; j < N; j++) Y[(size_t)i * N + j] += b[j];
+}
+
+float orc_train_forward(orc_train *t, const float *params, const int *tokens, const int *targets)
+{                                                       /* model.c:442-625 */
+    const orc_cfg *c = &t->c;
+    const int B = t->B, T = t->T, C = c->n_embd, V = c->vocab_size, L = c->n_layer;
+    const int H = c->n_head, hs = C / H;
+    const size_t N = (size_t)B * T;
+    long *off = malloc(sizeof(long) * (size_t)(4 + 12 * L));
+    float *Qh = malloc((size_t)T * hs * sizeof(float)), *Kh = malloc((size_t)T * hs * sizeof(float));
+    float *Vh = malloc((size_t)T * hs * sizeof(float)), *oh = malloc((size_t)T * hs * sizeof(float));
+    float *sc = malloc((size_t)T * T * sizeof(float));
+    orc_offsets(c, off);
+    const float *wte = params + off[0], *wpe = params + off[1];
+    for (int b = 0; b < B; b++)                           /* model.c:458-471 */
+        for (int p = 0; p < T; p++) {
+            const float *e = wte + (size_t)tokens[b * T + p] * C, *q = wpe + (size_t)p * C;
+            float *d = t->emb + ((size_t)b * T + p) * C;
+            for (int k = 0; k < C; k++) d[k] = e[k] + q[k];
+        }
+    const float *x = t->emb;
+    const float scale = 1.0f / sqrtf((float)hs);
+    for (int l = 0; l < L; l++) {
+        const long *o = off + 2 + 12 * l;
+        orc_layernorm(x, params + o[0], params + o[1], t->ln1_out[l], t->ln1_mean[l],
+                      t->ln1_rstd[l], (int)N, C);
+        linear_seq(t->ln1_out[l], params + o[2], params + o[3], t->qkv[l], (int)N, C, 3 * C);
+        for (int b = 0; b < B; b++)                       /* model.c:510-566 */
+            for (int h = 0; h < H; h++) {
+                float *pr = t->attn_probs[l] + ((size_t)b * H + h) * T * T;
+                for (int p = 0; p < T; p++) {
+                    const float *row = t->qkv[l] + ((size_t)b * T + p) * 3 * C;
+                    memcpy(Qh + (size_t)p * hs, row + h * hs, hs * sizeof(float));
+                    memcpy(Kh + (size_t)p * hs, row + C + h * hs, hs * sizeof(float));
+                    memcpy(Vh + (size_t)p * hs, row + 2 * C + h * hs, hs * sizeof(float));
+                }
+                sgemm(TRANS, T, T, hs, scale, Qh, hs, Kh, hs, 0.0f, sc, T);
+                orc_causal_mask(sc, T);
+                memcpy(pr, sc, (size_t)T * T * sizeof(float));
+                orc_softmax_inplace(pr, T, T);
+                sgemm(NO_TRANS, T, hs, T, 1.0f, pr, T, Vh, hs, 0.0f, oh, hs);
+                for (int p = 0; p < T; p++)
+                    memcpy(t->attn_out[l] + ((size_t)b * T + p) * C + h * hs, oh + (size_t)p * hs,
+                           hs * sizeof(float));
+            }
+        linear_seq(t->attn_out[l], params + o[4], params + o[5], t->attn_proj[l], (int)N, C, C);
+        for (size_t i = 0; i < N * C; i++) t->res1[l][i] = x[i] + t->attn_proj[l][i];   /* :572-573 */
+        orc_layernorm(t->res1[l], params + o[6], params + o[7], t->ln2_out[l], t->ln2_mean[l],
+                      t->ln2_rstd[l], (int)N, C);
+        linear_seq(t->ln2_out[l], params + o[8], params + o[9], t->fc_out[l], (int)N, C, 4 * C);
+        orc_gelu(t->fc_out[l], t->gelu[l], (int)(N * 4 * C));
+        linear_seq(t->gelu[l], params + o[10], params + o[11], t->mlp_out[l], (int)N, 4 * C, C);
+        for (size_t i = 0; i < N * C; i++) t->res2[l][i] = t->res1[l][i] + t->mlp_out[l][i];  /* :597-598 */
+        x = t->res2[l];
+    }
+    const long *of = off + 2 + 12 * L;                    /* model.c:608-614 */
+    orc_layernorm(x, params + of[0], params + of[1], t->ln_f_out, t->ln_f_mean, t->ln_f_rstd,
+                  (int)N, C);
+    linear_seq(t->ln_f_out, wte, NULL, t->logits, (int)N, C, V);
+    free(off); free(Qh); free(Kh); free(Vh); free(oh); free(sc);
+    if (!targets) return 0.0f;                            /* model.c:619-624 */
+    return orc_cross_entropy(t->logits, targets, t->probs, NULL, B, T, V);
+}
+
+void orc_train_backward(orc_train *t, const float *params, const int *tokens, const int *targets,
+                        float *grads)
+{                                                       /* model.c:634-877 */
+    const orc_cfg *c = &t->c;
+    const int B = t->B, T = t->T, C = c->n_embd, V = c->vocab_size, L = c->n_layer;
+    const int H = c->n_head, hs = C / H;
+    const size_t N = (size_t)B * T;
+    const float scale = 1.0f / (float)(B * T);
+    long *off = malloc(sizeof(long) * (size_t)(4 + 12 * L));
+    orc_offsets(c, off);
+    float *dlogits = calloc(N * V, sizeof(float)), *d_ln_f = calloc(N * C, sizeof(float));
+    float *d_x = calloc(N * C, sizeof(float)), *d_res1 = calloc(N * C, sizeof(float));
+    float *d_ln2 = calloc(N * C, sizeof(float)), *d_mlp4 = calloc(N * 4 * C, sizeof(float));
+    float *d_gelu = calloc(N * 4 * C, sizeof(float)), *d_ln1 = calloc(N * C, sizeof(float));
+    float *d_qkv = calloc(N * 3 * C, sizeof(float)), *d_attn_o = calloc(N * C, sizeof(float));
+    float *Qh = malloc((size_t)T * hs * sizeof(float)), *Kh = malloc((size_t)T * hs * sizeof(float));
+    float *Vh = malloc((size_t)T * hs * sizeof(float)), *d_o_h = malloc((size_t)T * hs * sizeof(float));
+    float *d_V_h = malloc((size_t)T * hs * sizeof(float)), *d_p = malloc((size_t)T * T * sizeof(float));
+    float *d_Q_h = malloc((size_t)T * hs * sizeof(float)), *d_K_h = malloc((size_t)T * hs * sizeof(float));
+    const float *wte = params + off[0];
+    float *g_wte = grads + off[0], *g_wpe = grads + off[1];
+
+    for (size_t bt = 0; bt < N; bt++)                     /* ops.c:576-589 via model.c:665 */
+        for (int v = 0; v < V; v++)
+            dlogits[bt * V + v] += scale * (t->probs[bt * V + v] - (v == targets[bt] ? 1.0f : 0.0f));
+    orc_linear_bwd_dx(dlogits, wte, d_ln_f, (int)N, C, V);                /* model.c:673-675 */
+    orc_linear_bwd_dw(dlogits, t->ln_f_out, g_wte, NULL, (int)N, C, V);
+    const long *of = off + 2 + 12 * L;
+    orc_layernorm_bwd(d_ln_f, L > 0 ? t->res2[L - 1] : t->emb, params + of[0], t->ln_f_mean,
+                      t->ln_f_rstd, d_x, grads + of[0], grads + of[1], (int)N, C);
+
+    for (int l = L - 1; l >= 0; l--) {                    /* model.c:690-857 */
+        const long *o = off + 2 + 12 * l;
+        const float *x_in = l == 0 ? t->emb : t->res2[l - 1];
+        memcpy(d_res1, d_x, N * C * sizeof(float));
+        memset(d_gelu, 0, N * 4 * C * sizeof(float));
+        orc_linear_bwd_dx(d_x, params + o[10], d_gelu, (int)N, 4 * C, C);
+        orc_linear_bwd_dw(d_x, t->gelu[l], grads + o[10], grads + o[11], (int)N, 4 * C, C);
+        memset(d_mlp4, 0, N * 4 * C * sizeof(float));
+        orc_gelu_bwd(d_gelu, t->fc_out[l], d_mlp4, (int)(N * 4 * C));
+        memset(d_ln2, 0, N * C * sizeof(float));
+        orc_linear_bwd_dx(d_mlp4, params + o[8], d_ln2, (int)N, C, 4 * C);
+        orc_linear_bwd_dw(d_mlp4, t->ln2_out[l], grads + o[8], grads + o[9], (int)N, C, 4 * C);
+        orc_layernorm_bwd(d_ln2, t->res1[l], params + o[6], t->ln2_mean[l], t->ln2_rstd[l],
+                          d_res1, grads + o[6], grads + o[7], (int)N, C);
+        memset(d_attn_o, 0, N * C * sizeof(float));
+        orc_linear_bwd_dx(d_res1, params + o[4], d_attn_o, (int)N, C, C);
+        orc_linear_bwd_dw(d_res1, t->attn_out[l], grads + o[4], grads + o[5], (int)N, C, C);
+        memset(d_qkv, 0, N * 3 * C * sizeof(float));
+        const float sc = 1.0f / sqrtf((float)hs);
+        for (int b = 0; b < B; b++)                       /* model.c:747-818 */
+            for (int h = 0; h < H; h++) {
+                const float *pr = t->attn_probs[l] + ((size_t)b * H + h) * T * T;
+                for (int p = 0; p < T; p++) {
+                    const float *qr = t->qkv[l] + ((size_t)b * T + p) * 3 * C;
+                    memcpy(Qh + (size_t)p * hs, qr + h * hs, hs * sizeof(float));
+                    memcpy(Kh + (size_t)p * hs, qr + C + h * hs, hs * sizeof(float));
+                    memcpy(Vh + (size_t)p * hs, qr + 2 * C + h * hs, hs * sizeof(float));
+                    memcpy(d_o_h + (size_t)p * hs, d_attn_o + ((size_t)b * T + p) * C + h * hs,
+                           hs * sizeof(float));
+                }
+                memset(d_V_h, 0, (size_t)T * hs * sizeof(float));
+                memset(d_p, 0, (size_t)T * T * sizeof(float));
+                memset(d_Q_h, 0, (size_t)T * hs * sizeof(float));
+                memset(d_K_h, 0, (size_t)T * hs * sizeof(float));
+                sgemm_t(TRANS, NO_TRANS, T, hs, T, 1.0f, pr, T, d_o_h, hs, 1.0f, d_V_h, hs);
+                sgemm_t(NO_TRANS, TRANS, T, T, hs, 1.0f, d_o_h, hs, Vh, hs, 0.0f, d_p, T);
+                for (int p = 0; p < T; p++) {             /* model.c:787-795 */
+                    const float *prr = pr + (size_t)p * T;
+                    float *dp = d_p + (size_t)p * T;
+                    float dot = 0.0f;
+                    for (int q = 0; q <= p; q++) dot += prr[q] * dp[q];
+                    for (int q = 0; q <= p; q++) dp[q] = prr[q] * (dp[q] - dot);
+                    for (int q = p + 1; q < T; q++) dp[q] = 0.0f;
+                }
+                sgemm_t(NO_TRANS, NO_TRANS, T, hs, T, sc, d_p, T, Kh, hs, 1.0f, d_Q_h, hs);
+                sgemm_t(TRANS, NO_TRANS, T, hs, T, sc, d_p, T, Qh, hs, 1.0f, d_K_h, hs);
+                for (int p = 0; p < T; p++) {
+                    float *dqr = d_qkv + ((size_t)b * T + p) * 3 * C;
+                    for (int i = 0; i < hs; i++) {
+                        dqr[h * hs + i] += d_Q_h[(size_t)p * hs + i];
+                        dqr[C + h * hs + i] += d_K_h[(size_t)p * hs + i];
+                        dqr[2 * C + h * hs + i] += d_V_h[(size_t)p * hs + i];
+                    }
+                }
+            }
+        memset(d_ln1, 0, N * C * sizeof(float));          /* model.c:822-841 */
+        orc_linear_bwd_dx(d_qkv, params + o[2], d_ln1, (int)N, C, 3 * C);
+        orc_linear_bwd_dw(d_qkv, t->ln1_out[l], grads + o[2], grads + o[3], (int)N, C, 3 * C);
+        memset(d_x, 0, N * C * sizeof(float));
+        orc_layernorm_bwd(d_ln1, x_in, params + o[0], t->ln1_mean[l], t->ln1_rstd[l], d_x,
+                          grads + o[0], grads + o[1], (int)N, C);
+        for (size_t i = 0; i < N * C; i++) d_x[i] += d_res1[i];
+    }
+    for (int b = 0; b < B; b++)                           /* model.c:850-866 */
+        for (int p = 0; p < T; p++) {
+            const float *dr = d_x + ((size_t)b * T + p) * C;
+            for (int k = 0; k < C; k++) g_wpe[(size_t)p * C + k] += dr[k];
+        }
+    for (int b = 0; b < B; b++)
+        for (int p = 0; p < T; p++) {
+            const float *dr = d_x + ((size_t)b * T + p) * C;
+            float *gw = g_wte + (size_t)tokens[b * T + p] * C;
+            for (int k = 0; k < C; k++) gw[k] += dr[k];
+        }
+    free(off); free(dlogits); free(d_ln_f); free(d_x); free(d_res1); free(d_ln2); free(d_mlp4);
+    free(d_gelu); free(d_ln1); free(d_qkv); free(d_attn_o); free(Qh); free(Kh); free(Vh);
+    free(d_o_h); free(d_V_h); free(d_p); free(d_Q_h); free(d_K_h);
+}
+
+/* The weight-decay mask of gpt_init (src/model.c:143-172): matrices and
+ * embeddings (wte, wpe, c_attn_w, c_proj_w, mlp_fc_w, mlp_proj_w) decay,
+ * LayerNorm gains and all biases do not. */
+static unsigned char *decay_mask(const orc_cfg *c, const long *off, long n)
+{
+    unsigned char *d = calloc((size_t)n, 1);
+    if (!d) return NULL;
+    memset(d, 1, (size_t)off[2]);                         /* wte, wpe */
+    for (int l = 0; l < c->n_layer; l++) {
+        const long *o = off + 2 + 12 * l;
+        memset(d + o[2], 1, (size_t)(o[3] - o[2]));       /* c_attn_w */
+        memset(d + o[4], 1, (size_t)(o[5] - o[4]));       /* c_proj_w */
+        memset(d + o[8], 1, (size_t)(o[9] - o[8]));       /* mlp_fc_w */
+        memset(d + o[10], 1, (size_t)(o[11] - o[10]));    /* mlp_proj_w */
+    }
+    return d;
+}
+
+void orc_adamw(const orc_cfg *c, float *params, float *grads, float *m, float *v, int step,
+               float lr, float beta1, float beta2, float eps, float wd, float grad_clip)
+{                                                       /* model.c:888-921 */
+    const long n = orc_num_params(c);
+    long *off = malloc(sizeof(long) * (size_t)(4 + 12 * c->n_layer));
+    orc_offsets(c, off);
+    unsigned char *dmask = decay_mask(c, off, n);
+    if (grad_clip > 0.0f) {                               /* ops.c:631-640 */
+        /* the reference's cblas_snrm2; here the sum of squares in double */
+        double ss = 0.0;
+        for (long i = 0; i < n; i++) ss += (double)grads[i] * grads[i];
+        const float norm = (float)sqrt(ss);
+        if (norm > grad_clip) {
+            const float s = grad_clip / norm;
+            for (long i = 0; i < n; i++) grads[i] *= s;
+        }
+    }
+    const float bc1 = 1.0f - powf(beta1, (float)step);
+    const float bc2 = 1.0f - powf(beta2, (float)step);
+    for (long i = 0; i < n; i++) {
+        const float g = grads[i];
+        m[i] = beta1 * m[i] + (1.0f - beta1) * g;
+        v[i] = beta2 * v[i] + (1.0f - beta2) * g * g;
+        const float m_hat = m[i] / bc1;
+        const float v_hat = v[i] / bc2;
+        const float ewd = dmask[i] ? wd : 0.0f;
+        params[i] = params[i] * (1.0f - lr * ewd) - lr * m_hat / (sqrtf(v_hat) + eps);
+    }
+    free(dmask);
+    free(off);
 }

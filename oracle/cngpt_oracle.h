@@ -1,5 +1,6 @@
 /*
- * cngpt_oracle.h - CPU restatement of cngpt's inference forward pass.
+ * cngpt_oracle.h - CPU restatement of cngpt's inference forward pass and of
+ * its training step (forward with targets, backward, AdamW).
  *
  * TEST INFRASTRUCTURE ONLY. This library is the checker the HIP path is
  * compared against, and the CPU baseline that bench.py times beside it.
@@ -85,6 +86,38 @@ int  orc_sample_top_k(const float *logits, int V, float temp, int top_k, float r
  * the negated term of each row. */
 float orc_cross_entropy(const float *logits, const int *targets, float *probs,
                         float *row_loss, int B, int T, int V);
+
+/* Training (dropout 0, the default of `cngpt train`, src/cngpt.c:94). */
+
+/* Backward ops, scalar paths: linear_bwd_dx / linear_bwd_dw
+ * (src/ops.c:125-153; both accumulate, db may be NULL), layernorm_bwd
+ * (ops.c:250-331, accumulates into dx, dw, db), gelu_bwd (ops.c:382-422,
+ * accumulates into dx). */
+void orc_linear_bwd_dx(const float *dY, const float *W, float *dX, int M, int K, int N);
+void orc_linear_bwd_dw(const float *dY, const float *X, float *dW, float *db, int M, int K, int N);
+void orc_layernorm_bwd(const float *dout, const float *x, const float *w, const float *mean,
+                       const float *rstd, float *dx, float *dw, float *db, int T, int C);
+void orc_gelu_bwd(const float *dout, const float *x, float *dx, int n);
+
+/* The activations gpt_forward keeps (GPTActivations, src/model.h:86-115)
+ * for one B x T shape. NULL on a bad shape or allocation failure. */
+typedef struct orc_train orc_train;
+orc_train *orc_train_new(const orc_cfg *c, int B, int T);
+void orc_train_free(orc_train *t);
+/* gpt_forward with targets (src/model.c:442-625): the mean loss; keeps the
+ * activations and the softmax of the logits. targets NULL: returns 0. */
+float orc_train_forward(orc_train *t, const float *params, const int *tokens, const int *targets);
+/* gpt_backward (src/model.c:634-877) for the last orc_train_forward:
+ * accumulates every parameter's gradient into grads (flat, the layout of
+ * params). */
+void orc_train_backward(orc_train *t, const float *params, const int *tokens, const int *targets,
+                        float *grads);
+/* gpt_adamw (src/model.c:888-921) with the step count already advanced:
+ * clips grads in place to grad_clip by their global norm (if > 0), then
+ * the AdamW update of params, m and v; weight decay on the matrices and
+ * embeddings only (src/model.c:143-172). */
+void orc_adamw(const orc_cfg *c, float *params, float *grads, float *m, float *v, int step,
+               float lr, float beta1, float beta2, float eps, float wd, float grad_clip);
 
 /* The draw sample_top_k makes (src/model.c:979): rand()/(RAND_MAX+1.0f). */
 void  orc_srand(unsigned seed);
