@@ -19,6 +19,9 @@
 // exp2 of (score - running max); the causal mask is applied only on the
 // tiles that cross the diagonal.
 //
+// k_attn_ks (below) splits the keys of 32 queries over four wavefronts
+// for launches with few blocks.
+//
 // The one-query form (the last-position pass, fast.c:287-297, and a decode
 // step) is k_attn_dec in decode.hip.
 #include "common.h"
@@ -193,12 +196,171 @@ __global__ void __launch_bounds__(256, 2)
     }
 }
 
+// k_attn_ks: the same product for launches with too few (sequence, head,
+// 128-query) blocks to occupy the CUs (one sequence of up to ~2500 tokens).
+// There a block's latency is its last wavefront's chain of matrix-core
+// steps over every key up to the diagonal, so a workgroup takes 32 queries
+// and its four wavefronts split the keys: wavefront w takes the 32-key
+// blocks w, w + 4, .. up to the diagonal, each loaded from global memory
+// straight into registers (K rows as the A operand of S^T = K Q^T, V rows
+// in the key order of the S^T accumulator for O^T += V^T P^T), the next
+// block's loads in flight during the current one. Each wavefront keeps its
+// running max m, sum l and O^T as above; the four are merged through LDS
+// in wavefront order (O = sum_w 2^(m_w - M) O_w / sum_w 2^(m_w - M) l_w,
+// M = max_w m_w; a wavefront with no block has m = -inf and adds zero).
+template <int HS>
+__global__ void __launch_bounds__(256, 2)
+    k_attn_ks(const float* __restrict__ qkv, long seq_stride, float* __restrict__ out, int B,
+              int T, int C, int H, int nqb, float scale) {
+    constexpr int HALF = HS / 2;
+    constexpr int NDB = (HS + 31) / 32;
+    constexpr int OS = NDB * 32 + 1;  // LDS row of a merged query
+    __shared__ float om[4][32], ol[4][32];
+    __shared__ float oo[4][32 * OS];
+
+    const int BH = B * H;
+    const int qb = nqb - 1 - (int)(blockIdx.x / BH);  // longest query blocks first
+    const int bh = blockIdx.x % BH;
+    const int b = bh / H, h = bh % H;
+    const long C3 = 3L * C;
+    const float* base = qkv + (long)b * seq_stride * C3;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int lr = lane & 31, lh = lane >> 5;
+    const int q0 = qb * 32, qi = q0 + lr;
+    const int nkb = min(q0 + 31, T - 1) / 32 + 1;  // key blocks up to the diagonal
+
+    float qreg[HALF];
+    {
+        const float* qp = base + (long)min(qi, T - 1) * C3 + h * HS + lh * HALF;
+        const float qs = scale * 1.4426950408889634f;  // scores in units of log2
+#pragma unroll
+        for (int d = 0; d < HALF; d += 4) {
+            const f32x4 v = *(const f32x4*)(qp + d);
+            qreg[d] = v.x * qs; qreg[d + 1] = v.y * qs; qreg[d + 2] = v.z * qs; qreg[d + 3] = v.w * qs;
+        }
+    }
+    // key block kb: K row kb*32 + lr, d in [lh*HALF, +HALF); V rows of the
+    // S^T accumulator's keys kb*32 + 8 (r/4) + 4 lh + r%4, d = 32 j + lr
+    f32x4 kr[HALF / 4];
+    float vr[NDB][16];
+    auto load = [&](int kb) {
+        const float* kp = base + (long)min(kb * 32 + lr, T - 1) * C3 + C + h * HS + lh * HALF;
+#pragma unroll
+        for (int d = 0; d < HALF / 4; d++) kr[d] = *(const f32x4*)(kp + 4 * d);
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int key = min(kb * 32 + 8 * (r >> 2) + 4 * lh + (r & 3), T - 1);
+            const float* vp = base + (long)key * C3 + 2 * C + h * HS;
+#pragma unroll
+            for (int j = 0; j < NDB; j++) vr[j][r] = vp[min(32 * j + lr, HS - 1)];
+        }
+    };
+
+    f32x16 o[NDB];
+#pragma unroll
+    for (int j = 0; j < NDB; j++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) o[j][r] = 0.f;
+    float m_run = -INFINITY, l_run = 0.f;
+    if (wave < nkb) load(wave);
+    for (int kb = wave; kb < nkb; kb += 4) {
+        f32x4 kc[HALF / 4];
+        float vc[NDB][16];
+#pragma unroll
+        for (int d = 0; d < HALF / 4; d++) kc[d] = kr[d];
+#pragma unroll
+        for (int j = 0; j < NDB; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) vc[j][r] = vr[j][r];
+        if (kb + 4 < nkb) load(kb + 4);
+        f32x16 sc;
+#pragma unroll
+        for (int r = 0; r < 16; r++) sc[r] = 0.f;
+#pragma unroll
+        for (int d = 0; d < HALF / 4; d++) {
+            sc = __builtin_amdgcn_mfma_f32_32x32x2f32(kc[d].x, qreg[4 * d], sc, 0, 0, 0);
+            sc = __builtin_amdgcn_mfma_f32_32x32x2f32(kc[d].y, qreg[4 * d + 1], sc, 0, 0, 0);
+            sc = __builtin_amdgcn_mfma_f32_32x32x2f32(kc[d].z, qreg[4 * d + 2], sc, 0, 0, 0);
+            sc = __builtin_amdgcn_mfma_f32_32x32x2f32(kc[d].w, qreg[4 * d + 3], sc, 0, 0, 0);
+        }
+        if (kb * 32 + 31 > q0) {
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int key = kb * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                sc[r] = (key > qi) ? -INFINITY : sc[r];
+            }
+        }
+        float mt = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; r++) mt = fmaxf(mt, sc[r]);
+        mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+        const float m_new = fmaxf(m_run, mt);
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+        float ps = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const float pr = __builtin_amdgcn_exp2f(sc[r] - m_new);
+            sc[r] = pr;
+            ps += pr;
+        }
+        ps += __shfl_xor(ps, 32, 64);
+        l_run = l_run * alpha + ps;
+        m_run = m_new;
+#pragma unroll
+        for (int j = 0; j < NDB; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) o[j][r] *= alpha;
+#pragma unroll
+        for (int r = 0; r < 16; r++)
+#pragma unroll
+            for (int j = 0; j < NDB; j++) {
+                const float va = (HS >= 32 || 32 * j + lr < HS) ? vc[j][r] : 0.f;
+                o[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(va, sc[r], o[j], 0, 0, 0);
+            }
+    }
+
+    // o[j][r] = O^T[d = 32 j + 8 (r/4) + 4 lh + r%4][query lr]
+    if (lh == 0) {
+        om[wave][lr] = m_run;
+        ol[wave][lr] = l_run;
+    }
+#pragma unroll
+    for (int j = 0; j < NDB; j++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int d = 32 * j + 8 * (r >> 2) + 4 * lh + (r & 3);
+            if (d < HS) oo[wave][lr * OS + d] = o[j][r];
+        }
+    __syncthreads();
+    for (int i = tid; i < 32 * HS; i += 256) {
+        const int q = i / HS, d = i % HS;
+        if (q0 + q >= T) break;
+        const float mx = fmaxf(fmaxf(om[0][q], om[1][q]), fmaxf(om[2][q], om[3][q]));
+        float l = 0.f, v = 0.f;
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            const float f = __builtin_amdgcn_exp2f(om[w][q] - mx);
+            l += f * ol[w][q];
+            v += f * oo[w][q * OS + d];
+        }
+        out[((long)b * T + q0 + q) * C + h * HS + d] = v / l;
+    }
+}
+
 template <int HS>
 hipError_t causal_hs(const float* qkv, long seq_stride, float* out, int B, int T, int C, int H,
                      hipStream_t s) {
     const int nqb = (T + 127) / 128;
     const float scale = 1.0f / sqrtf((float)HS);
-    k_attn_causal<HS><<<nqb * B * H, 256, 0, s>>>(qkv, seq_stride, out, B, T, C, H, nqb, scale);
+    // (the key split holds a 32-key block of K and V per lane: up to HS = 64)
+    if ((long)nqb * B * H >= 256 || HS > 64) {
+        k_attn_causal<HS><<<nqb * B * H, 256, 0, s>>>(qkv, seq_stride, out, B, T, C, H, nqb,
+                                                       scale);
+    } else {
+        const int nqb32 = (T + 31) / 32;
+        k_attn_ks<HS><<<nqb32 * B * H, 256, 0, s>>>(qkv, seq_stride, out, B, T, C, H, nqb32,
+                                                     scale);
+    }
     return hipGetLastError();
 }
 
