@@ -85,6 +85,9 @@ EXPORTS = [
     "cngpt_hip_decode_length", "cngpt_hip_set_decode_path", "cngpt_hip_decode_path",
     "cngpt_hip_profile_enable", "cngpt_hip_profile_reset", "cngpt_hip_profile_read",
     "cngpt_hip_host_alloc", "cngpt_hip_host_free", "cngpt_hip_init_weights",
+    "cngpt_hip_train_create", "cngpt_hip_train_destroy", "cngpt_hip_train_forward",
+    "cngpt_hip_train_backward", "cngpt_hip_train_zero_grad", "cngpt_hip_train_adamw",
+    "cngpt_hip_train_read", "cngpt_hip_train_write", "cngpt_hip_train_steps",
     "fast_init", "fast_free", "fast_set_threads", "gpt_forward_fast", "gpt_forward_fast_all",
     "fast_params_changed", "fast_last_error",
     "gpt_num_params", "gpt_init", "gpt_init_weights", "gpt_load", "gpt_save", "gpt_free",
@@ -142,6 +145,16 @@ def lib():
     L.cngpt_hip_host_free.argtypes = [_VP]
     L.cngpt_hip_host_free.restype = None
     L.cngpt_hip_init_weights.argtypes = [ctypes.POINTER(_Cfg), _F, ctypes.c_uint]
+    L.cngpt_hip_train_create.argtypes = [_VP, ctypes.c_int, ctypes.c_int, ctypes.POINTER(_VP)]
+    L.cngpt_hip_train_destroy.argtypes = [_VP]
+    L.cngpt_hip_train_destroy.restype = None
+    L.cngpt_hip_train_forward.argtypes = [_VP, _I, _I, _F]
+    L.cngpt_hip_train_backward.argtypes = [_VP]
+    L.cngpt_hip_train_zero_grad.argtypes = [_VP]
+    L.cngpt_hip_train_adamw.argtypes = [_VP] + [ctypes.c_float] * 6 + [_F]
+    L.cngpt_hip_train_read.argtypes = [_VP, ctypes.c_int, _F, ctypes.c_long]
+    L.cngpt_hip_train_write.argtypes = [_VP, ctypes.c_int, _F, ctypes.c_long]
+    L.cngpt_hip_train_steps.argtypes = [_VP]
     _lib = L
     return L
 
@@ -431,3 +444,85 @@ class Model:
             res[name] = {"ms": ms.value, "launches": n.value, "flops": fl.value,
                          "bytes": by.value}
         return res
+
+
+# ---------------------------------------------------------------- training
+
+TRAIN_PARAMS, TRAIN_GRADS, TRAIN_M, TRAIN_V = 0, 1, 2, 3
+
+
+class Trainer:
+    """The reference's training step on the device (cngpt_hip_train_*):
+    gpt_forward with targets, gpt_backward, gpt_zero_grad and gpt_adamw
+    (src/model.c:442-921) over a Model's parameters, which adamw updates in
+    place, for one batch shape B x T."""
+
+    def __init__(self, model: Model, B: int, T: int):
+        self.model, self.B, self.T = model, B, T
+        self.n = num_params(model.cfg)
+        t = _VP()
+        _check(lib().cngpt_hip_train_create(model._h, B, T, ctypes.byref(t)), "train_create")
+        self._t = t
+
+    def close(self) -> None:
+        if getattr(self, "_t", None):
+            lib().cngpt_hip_train_destroy(self._t)
+            self._t = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def forward(self, tokens, targets) -> float:       # model.c:442-625
+        tokens = np.ascontiguousarray(tokens, np.int32).reshape(-1)
+        targets = np.ascontiguousarray(targets, np.int32).reshape(-1)
+        if tokens.size != self.B * self.T or targets.size != self.B * self.T:
+            raise CngptError(f"tokens and targets must hold {self.B} x {self.T} ids")
+        loss = ctypes.c_float()
+        _check(lib().cngpt_hip_train_forward(self._t, _ip(tokens), _ip(targets),
+                                             ctypes.byref(loss)), "train_forward")
+        return float(loss.value)
+
+    def backward(self) -> None:                         # model.c:634-877
+        _check(lib().cngpt_hip_train_backward(self._t), "train_backward")
+
+    def zero_grad(self) -> None:                        # model.c:879-886
+        _check(lib().cngpt_hip_train_zero_grad(self._t), "train_zero_grad")
+
+    def adamw(self, lr, beta1=0.9, beta2=0.95, eps=1e-8, wd=0.1, grad_clip=1.0) -> float:
+        """model.c:888-921; returns the gradient norm before clipping."""
+        norm = ctypes.c_float()
+        _check(lib().cngpt_hip_train_adamw(self._t, lr, beta1, beta2, eps, wd, grad_clip,
+                                           ctypes.byref(norm)), "train_adamw")
+        return float(norm.value)
+
+    def read(self, which: int) -> np.ndarray:
+        out = np.empty(self.n, np.float32)
+        _check(lib().cngpt_hip_train_read(self._t, which, _fp(out), self.n), "train_read")
+        return out
+
+    def write(self, which: int, values) -> None:
+        values = np.ascontiguousarray(values, np.float32)
+        _check(lib().cngpt_hip_train_write(self._t, which, _fp(values), values.size),
+               "train_write")
+
+    @property
+    def params(self) -> np.ndarray:
+        return self.read(TRAIN_PARAMS)
+
+    @property
+    def grads(self) -> np.ndarray:
+        return self.read(TRAIN_GRADS)
+
+    @property
+    def steps(self) -> int:
+        return lib().cngpt_hip_train_steps(self._t)
+

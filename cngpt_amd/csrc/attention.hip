@@ -34,7 +34,7 @@ constexpr int KT = 64;  // keys per LDS tile
 template <int HS>
 __global__ void __launch_bounds__(256, 2)
     k_attn_causal(const float* __restrict__ qkv, long seq_stride, float* __restrict__ out, int B,
-                  int T, int C, int H, int nqb, float scale) {
+                  int T, int C, int H, int nqb, float scale, float* __restrict__ lse) {
     constexpr int HALF = HS / 2;            // d values per lane half in Q K^T
     constexpr int F4 = HS / 4;              // float4 per head row
     constexpr int ROW = HS + 4;             // padded LDS row
@@ -180,6 +180,7 @@ __global__ void __launch_bounds__(256, 2)
     }
 
     if (qi < T) {
+        if (lse && lh == 0) lse[((long)b * H + h) * T + qi] = m_run + log2f(l_run);
         const float inv = 1.0f / l_run;
         float* op = out + ((long)b * T + qi) * C + h * HS;
 #pragma unroll
@@ -211,7 +212,7 @@ __global__ void __launch_bounds__(256, 2)
 template <int HS>
 __global__ void __launch_bounds__(256, 2)
     k_attn_ks(const float* __restrict__ qkv, long seq_stride, float* __restrict__ out, int B,
-              int T, int C, int H, int nqb, float scale) {
+              int T, int C, int H, int nqb, float scale, float* __restrict__ lse) {
     constexpr int HALF = HS / 2;
     constexpr int NDB = (HS + 31) / 32;
     constexpr int OS = NDB * 32 + 1;  // LDS row of a merged query
@@ -344,37 +345,40 @@ __global__ void __launch_bounds__(256, 2)
             v += f * oo[w][q * OS + d];
         }
         out[((long)b * T + q0 + q) * C + h * HS + d] = v / l;
+        if (lse && d == 0) lse[((long)b * H + h) * T + q0 + q] = mx + log2f(l);
     }
 }
 
 template <int HS>
 hipError_t causal_hs(const float* qkv, long seq_stride, float* out, int B, int T, int C, int H,
-                     hipStream_t s) {
+                     float* lse, hipStream_t s) {
     const int nqb = (T + 127) / 128;
     const float scale = 1.0f / sqrtf((float)HS);
     // (the key split holds a 32-key block of K and V per lane: up to HS = 64)
-    if ((long)nqb * B * H >= 256 || HS > 64) {
-        k_attn_causal<HS><<<nqb * B * H, 256, 0, s>>>(qkv, seq_stride, out, B, T, C, H, nqb,
-                                                       scale);
-    } else {
-        const int nqb32 = (T + 31) / 32;
-        k_attn_ks<HS><<<nqb32 * B * H, 256, 0, s>>>(qkv, seq_stride, out, B, T, C, H, nqb32,
-                                                     scale);
+    if constexpr (HS <= 64) {
+        if ((long)nqb * B * H < 256) {
+            const int nqb32 = (T + 31) / 32;
+            k_attn_ks<HS><<<nqb32 * B * H, 256, 0, s>>>(qkv, seq_stride, out, B, T, C, H, nqb32,
+                                                         scale, lse);
+            return hipGetLastError();
+        }
     }
+    k_attn_causal<HS><<<nqb * B * H, 256, 0, s>>>(qkv, seq_stride, out, B, T, C, H, nqb, scale,
+                                                   lse);
     return hipGetLastError();
 }
 
 }  // namespace
 
 hipError_t launch_attention_causal(const float* qkv, long seq_stride, float* out, int B, int T,
-                                   int C, int H, hipStream_t s) {
+                                   int C, int H, hipStream_t s, float* lse) {
     if (B <= 0 || T <= 0) return hipSuccess;
     switch (C / H) {
-        case 8: return causal_hs<8>(qkv, seq_stride, out, B, T, C, H, s);
-        case 16: return causal_hs<16>(qkv, seq_stride, out, B, T, C, H, s);
-        case 32: return causal_hs<32>(qkv, seq_stride, out, B, T, C, H, s);
-        case 64: return causal_hs<64>(qkv, seq_stride, out, B, T, C, H, s);
-        case 128: return causal_hs<128>(qkv, seq_stride, out, B, T, C, H, s);
+        case 8: return causal_hs<8>(qkv, seq_stride, out, B, T, C, H, lse, s);
+        case 16: return causal_hs<16>(qkv, seq_stride, out, B, T, C, H, lse, s);
+        case 32: return causal_hs<32>(qkv, seq_stride, out, B, T, C, H, lse, s);
+        case 64: return causal_hs<64>(qkv, seq_stride, out, B, T, C, H, lse, s);
+        case 128: return causal_hs<128>(qkv, seq_stride, out, B, T, C, H, lse, s);
     }
     return hipErrorInvalidValue;
 }

@@ -27,6 +27,7 @@
 
 #include "../../include/cngpt_hip.h"
 #include "common.h"
+#include "ctx_view.h"
 #include "kernels.h"
 
 namespace {
@@ -1070,6 +1071,30 @@ long carve_scratch(const cngpt_hip_config& c, int B, int T, float* base, FwdBufs
 }
 
 }  // namespace
+
+// Internal view for train_host.cpp (ctx_view.h).
+int ctx_view(cngpt_hip_ctx* h, CtxView* v) {
+    if (need_params(h)) return -1;
+    v->device = h->device;
+    v->stream = h->stream;
+    v->cfg = h->cfg;
+    v->params = h->d_params;
+    v->n_params = h->n_params;
+    v->wte = h->wte;
+    v->wpe = h->wpe;
+    v->lnf_w = h->lnf_w;
+    v->lnf_b = h->lnf_b;
+    v->layers = h->layers.data();
+    return 0;
+}
+
+int ctx_fail(const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return -1;
+}
 
 // ==================================================================== C ABI
 

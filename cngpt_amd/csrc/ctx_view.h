@@ -1,0 +1,23 @@
+// ctx_view.h - what the training step (train_host.cpp) reads of a handle of
+// cngpt_hip.cpp: its device, stream, shape and parameter views. Internal to
+// the library (hidden symbols).
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include "../../include/cngpt_hip.h"
+#include "kernels.h"
+
+struct CtxView {
+    int device;
+    hipStream_t stream;
+    cngpt_hip_config cfg;
+    float* params;  // device, n_params floats in the weight-file layout
+    long n_params;
+    const float *wte, *wpe, *lnf_w, *lnf_b;
+    const LayerW* layers;  // host array of n_layer views into params
+};
+
+// Fills v from h; -1 (message set) when h is null or holds no parameters.
+__attribute__((visibility("hidden"))) int ctx_view(cngpt_hip_ctx* h, CtxView* v);
+// Sets the message cngpt_hip_last_error() returns; returns -1.
+__attribute__((visibility("hidden"))) int ctx_fail(const char* fmt, ...);

@@ -7,8 +7,10 @@
 hipError_t launch_embed(const int* tok, const float* wte, const float* wpe, float* x, long rows,
                         int T, int C, int V, int pos0, const int* pos_dev, int* err,
                         int* hist, long hist_stride, hipStream_t s);
+// With mean / rstd set (both or neither), also each row's mean and rstd.
 hipError_t launch_layernorm(const float* x, long in_stride, const float* w, const float* b,
-                            float* out, long out_stride, int rows, int C, hipStream_t s);
+                            float* out, long out_stride, int rows, int C, hipStream_t s,
+                            float* mean = nullptr, float* rstd = nullptr);
 hipError_t launch_gather_rows(const float* src, long src_stride, float* dst, int rows, int C,
                               hipStream_t s);
 
@@ -195,8 +197,11 @@ hipError_t launch_decode_persist(const PersistArgs& a, int G, hipStream_t s);
 // attention.hip
 // qkv rows hold [q | k | v] (3C floats); sequence b's row t sits at
 // qkv + (b * seq_stride + t) * 3C. out row (b*T + t) gets the merged heads.
+// With lse set, also the log-sum-exp of every query's scores in base 2 (of
+// the scores times scale * log2(e)) at lse[(b * H + h) * T + t], which the
+// attention backward uses to recompute the probabilities.
 hipError_t launch_attention_causal(const float* qkv, long seq_stride, float* out, int B, int T,
-                                   int C, int H, hipStream_t s);
+                                   int C, int H, hipStream_t s, float* lse = nullptr);
 
 // loss.hip
 // Cross-entropy of rows x V logits against targets [rows]: row_loss[r] =
@@ -205,3 +210,47 @@ hipError_t launch_attention_causal(const float* qkv, long seq_stride, float* out
 // [0, V) are clamped and reported through *err (bit 2).
 hipError_t launch_cross_entropy(float* logits, long rows, int V, const int* targets,
                                 float* row_loss, float* loss, int probs, int* err, hipStream_t s);
+
+// train.hip: the training step's elementwise, row and reduction kernels.
+// out = gelu(in); d = d * gelu'(x) (n a multiple of 4).
+hipError_t launch_gelu_fwd(const float* in, float* out, long n, hipStream_t s);
+hipError_t launch_gelu_bwd(float* d, const float* x, long n, hipStream_t s);
+// dst [cols_p][ldd] = src [rows][lds]^T, zero in the padding (rows <= rows_p
+// <= ldd, cols <= cols_p).
+hipError_t launch_transpose(const float* src, long lds, int rows, int cols, float* dst, long ldd,
+                            int rows_p, int cols_p, hipStream_t s);
+// out[c] += sum over rows of Y[r][c] (partials of colsum_part_floats floats
+// at part, summed in row-chunk order).
+long colsum_part_floats(int rows, int cols);
+hipError_t launch_colsum_add(const float* Y, long ldy, int rows, int cols, float* part,
+                             float* out, hipStream_t s);
+// layernorm_bwd: dx += ..., dw += sum dout * xhat, db += sum dout over the
+// rows (partials of ln_bwd_part_floats floats at part). C a multiple of 4,
+// at most 2048.
+long ln_bwd_part_floats(int rows, int C);
+hipError_t launch_layernorm_bwd(const float* dout, const float* x, const float* w,
+                                const float* mean, const float* rstd, float* dx, float* dw,
+                                float* db, int rows, int C, float* part, hipStream_t s);
+// dl [rows][ldd] = scale * (probs - onehot(targets)), zero for columns >= V.
+hipError_t launch_ce_bwd(const float* probs, int V, const int* targets, float scale, float* dl,
+                         long ldd, long rows, hipStream_t s);
+// g_wpe[t] += sum_b dx[b][t]; g_wte[uniq[u]] += dx rows pos[start[u] ..
+// start[u+1]) in order, for each of the nuniq distinct tokens.
+hipError_t launch_embed_bwd(const float* dx, int B, int T, int C, float* g_wpe, float* g_wte,
+                            const int* uniq, const int* start, const int* pos, int nuniq,
+                            hipStream_t s);
+// gpt_adamw over n parameters: the global gradient norm into *norm (from
+// grad_norm_parts(n) double partials at part), the clip coefficient into
+// *coef, then the update of p, g (clipped in place), m and v.
+int grad_norm_parts(long n);
+hipError_t launch_adamw(float* p, float* g, float* m, float* v, const unsigned char* decay,
+                        long n, double* part, float* norm, float* coef, float lr, float beta1,
+                        float beta2, float eps, float wd, float clip, float bc1, float bc2,
+                        hipStream_t s);
+
+// attn_bwd.hip: dQ, dK, dV of every head into the qkv gradient rows [B*T][3C]
+// from the forward's qkv rows, its output rows `out` [B*T][C], their
+// gradient dout and the forward's lse; D [B*H*T] is scratch.
+hipError_t launch_attention_bwd(const float* qkv, const float* out, const float* dout,
+                                const float* lse, float* D, float* dqkv, int B, int T, int C,
+                                int H, hipStream_t s);

@@ -36,7 +36,9 @@ __global__ void __launch_bounds__(256) k_embed(const int* __restrict__ tok,
 }
 
 // LayerNorm of one row per wavefront (reference ops.c:191-248): mean, biased
-// variance of (x - mean), rstd = 1/sqrtf(var + 1e-5), out = (x-m)*rstd*w + b.
+// variance of (x - mean), rstd = 1/sqrtf(var + 1e-5), out = (x-m)*rstd*w + b;
+// with mean_out / rstd_out set, also each row's mean and rstd (the training
+// forward keeps them for the backward, as layernorm_fwd does).
 // NCH = float4 chunks per lane, so C <= 256 * NCH. Rows are read at stride
 // in_stride and written at stride out_stride (floats), which lets the final
 // LayerNorm of the last-position pass gather rows b*T + T-1.
@@ -44,7 +46,9 @@ template <int NCH>
 __global__ void __launch_bounds__(256) k_layernorm(const float* __restrict__ x, long in_stride,
                                                    const float* __restrict__ w,
                                                    const float* __restrict__ b, float* __restrict__ out,
-                                                   long out_stride, int rows, int C) {
+                                                   long out_stride, int rows, int C,
+                                                   float* __restrict__ mean_out,
+                                                   float* __restrict__ rstd_out) {
     const int lane = threadIdx.x & 63;
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= rows) return;
@@ -72,6 +76,10 @@ __global__ void __launch_bounds__(256) k_layernorm(const float* __restrict__ x, 
         }
     }
     const float rs = 1.0f / sqrtf(wave_sum(q) / (float)C + 1e-5f);
+    if (mean_out && lane == 0) {
+        mean_out[row] = m;
+        rstd_out[row] = rs;
+    }
     float* orow = out + (long)row * out_stride;
 #pragma unroll
     for (int j = 0; j < NCH; j++) {
@@ -104,20 +112,22 @@ hipError_t launch_embed(const int* tok, const float* wte, const float* wpe, floa
 }
 
 hipError_t launch_layernorm(const float* x, long in_stride, const float* w, const float* b,
-                            float* out, long out_stride, int rows, int C, hipStream_t s) {
+                            float* out, long out_stride, int rows, int C, hipStream_t s,
+                            float* mean, float* rstd) {
     if (rows == 0) return hipSuccess;
+    if (!mean != !rstd) return hipErrorInvalidValue;
     dim3 grid((rows + 3) / 4), block(256);
     int nch = (C + 255) / 256;
     if (nch <= 1)
-        k_layernorm<1><<<grid, block, 0, s>>>(x, in_stride, w, b, out, out_stride, rows, C);
+        k_layernorm<1><<<grid, block, 0, s>>>(x, in_stride, w, b, out, out_stride, rows, C, mean, rstd);
     else if (nch <= 2)
-        k_layernorm<2><<<grid, block, 0, s>>>(x, in_stride, w, b, out, out_stride, rows, C);
+        k_layernorm<2><<<grid, block, 0, s>>>(x, in_stride, w, b, out, out_stride, rows, C, mean, rstd);
     else if (nch <= 3)
-        k_layernorm<3><<<grid, block, 0, s>>>(x, in_stride, w, b, out, out_stride, rows, C);
+        k_layernorm<3><<<grid, block, 0, s>>>(x, in_stride, w, b, out, out_stride, rows, C, mean, rstd);
     else if (nch <= 4)
-        k_layernorm<4><<<grid, block, 0, s>>>(x, in_stride, w, b, out, out_stride, rows, C);
+        k_layernorm<4><<<grid, block, 0, s>>>(x, in_stride, w, b, out, out_stride, rows, C, mean, rstd);
     else if (nch <= 8)
-        k_layernorm<8><<<grid, block, 0, s>>>(x, in_stride, w, b, out, out_stride, rows, C);
+        k_layernorm<8><<<grid, block, 0, s>>>(x, in_stride, w, b, out, out_stride, rows, C, mean, rstd);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();

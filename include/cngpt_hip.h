@@ -1,5 +1,6 @@
 /*
- * cngpt_hip.h - C ABI of the MI355X (gfx950) inference forward pass.
+ * cngpt_hip.h - C ABI of the MI355X (gfx950) inference forward pass (and,
+ * at the end, of the training step on the device).
  *
  * Plain C: opaque handles, plain pointers and sizes, int status codes
  * (0 = success, -1 = failure with a message from cngpt_hip_last_error()).
@@ -221,6 +222,58 @@ void  cngpt_hip_host_free(void *p);
  * (src/model.c:275-331), into a host buffer of cngpt_hip_num_params floats.
  * Needs no GPU. */
 int  cngpt_hip_init_weights(const cngpt_hip_config *cfg, float *params, unsigned seed);
+
+/* ------------------------------------------------------------------
+ * Training on the device: the reference's gpt_forward with targets,
+ * gpt_backward, gpt_zero_grad and gpt_adamw (src/model.h:163-187,
+ * src/model.c:333-921) over the handle's parameters, which the update
+ * changes in place (later forwards and decodes on the handle see them).
+ * A trainer holds, for one B x T, the activations gpt_forward keeps for
+ * gpt_backward (GPTActivations, src/model.h:86-115, with each attention's
+ * log-sum-exp in place of its T x T probabilities), the gradients
+ * (GPTGrads) and the AdamW moments (m_buf, v_buf, decay_buf,
+ * src/model.h:120-141). Dropout is not supported (the default of
+ * `cngpt train`, src/cngpt.c:94): the configuration carries none.
+ * ------------------------------------------------------------------ */
+typedef struct cngpt_hip_train cngpt_hip_train;
+
+/* gpt_resize_acts (model.c:333-440) for B x T plus the gradient and moment
+ * buffers (gpt_init's grad_buf, m_buf, v_buf, zeroed); the handle must
+ * hold parameters and outlive the trainer. */
+int  cngpt_hip_train_create(cngpt_hip_ctx *h, int B, int T, cngpt_hip_train **out);
+void cngpt_hip_train_destroy(cngpt_hip_train *t);
+
+/* gpt_forward(m, tokens, targets, B, T) (model.c:442-625): host token and
+ * target ids [B*T], the mean cross-entropy in *loss (synchronizes). Ids
+ * outside [0, V) fail before any work. */
+int  cngpt_hip_train_forward(cngpt_hip_train *t, const int *tokens, const int *targets,
+                             float *loss);
+
+/* gpt_backward (model.c:634-877) for the last forward: gradients add to
+ * the held ones, as in the reference. */
+int  cngpt_hip_train_backward(cngpt_hip_train *t);
+
+/* gpt_zero_grad (model.c:879-886). */
+int  cngpt_hip_train_zero_grad(cngpt_hip_train *t);
+
+/* gpt_adamw(m, lr, beta1, beta2, eps, weight_decay, grad_clip)
+ * (model.c:888-921): step += 1; with grad_clip > 0 the gradients are
+ * scaled by grad_clip / norm when their global L2 norm exceeds it; then
+ * AdamW with bias correction and decoupled weight decay on the matrices
+ * and embeddings (the decay mask of model.c:143-172). The norm before
+ * clipping goes to *grad_norm when that is not NULL (synchronizes then). */
+int  cngpt_hip_train_adamw(cngpt_hip_train *t, float lr, float beta1, float beta2, float eps,
+                           float weight_decay, float grad_clip, float *grad_norm);
+
+/* Flat buffers of cngpt_hip_num_params floats in the weight-file layout. */
+enum { CNGPT_TRAIN_PARAMS = 0, CNGPT_TRAIN_GRADS = 1, CNGPT_TRAIN_M = 2, CNGPT_TRAIN_V = 3 };
+/* Copy n floats of buffer `which` to the host (synchronizes). */
+int  cngpt_hip_train_read(cngpt_hip_train *t, int which, float *dst, long n);
+/* Overwrite the gradients or a moment buffer (not the parameters: load
+ * them through cngpt_hip_load_params) with n host floats. */
+int  cngpt_hip_train_write(cngpt_hip_train *t, int which, const float *src, long n);
+/* Optimizer steps taken (gpt_adamw's m->step). */
+int  cngpt_hip_train_steps(cngpt_hip_train *t);
 
 #ifdef __cplusplus
 }
