@@ -89,6 +89,57 @@ def prefill(m: cngpt_amd.Model, cfg, B: int, T: int, steps: int, warmup: int,
     return dt, prof
 
 
+def train_flops(cfg, B: int, T: int) -> float:
+    """Algorithmic FLOPs of one training step: the forward's products
+    (linear layers, lm_head, causal attention) and twice that for the
+    backward (dX and dW of each product; dV, dP, dQ, dK of attention),
+    without the attention's recomputed scores."""
+    C, L, V = cfg.n_embd, cfg.n_layer, cfg.vocab_size
+    N = B * T
+    linear = 2.0 * N * (12 * C * C * L + V * C)
+    attn = 2.0 * C * T * (T + 1) * B * L
+    return 3.0 * (linear + attn)
+
+
+def train_leg(m: cngpt_amd.Model, cfg, B: int, T: int, steps: int, warmup: int) -> dict:
+    """Training steps on the device (cngpt_amd.Trainer): zero_grad, forward
+    with next-token targets, backward, AdamW (lr 3e-4, clip 1.0: `cngpt
+    train`'s defaults, src/cngpt.c:94-162). The forward reads its loss and
+    AdamW the gradient norm back, so each step ends synchronized, as the
+    reference's loop does."""
+    ids = lcg_tokens(B * T + 1, cfg.vocab_size, 4321)
+    tok, tgt = ids[:-1].reshape(B, T), ids[1:].reshape(B, T)
+    with cngpt_amd.Trainer(m, B, T) as tr:
+        for _ in range(warmup):
+            tr.zero_grad()
+            tr.forward(tok, tgt)
+            tr.backward()
+            tr.adamw(3e-4, 0.9, 0.95, 1e-8, 0.1, 1.0)
+        m.synchronize()
+        t0 = time.perf_counter()
+        losses = []
+        for _ in range(steps):
+            tr.zero_grad()
+            losses.append(tr.forward(tok, tgt))
+            tr.backward()
+            norm = tr.adamw(3e-4, 0.9, 0.95, 1e-8, 0.1, 1.0)
+        m.synchronize()
+        dt = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            tr.forward(tok, tgt)
+        m.synchronize()
+        dt_f = time.perf_counter() - t0
+    fl = train_flops(cfg, B, T)
+    return {"train_B": B, "train_T": T, "tok_s": round(B * T * steps / dt, 1),
+            "ms_per_step": round(dt * 1e3 / steps, 3),
+            "forward_ms": round(dt_f * 1e3 / steps, 3),
+            "tflops": round(fl * steps / dt / 1e12, 2),
+            "mfma_frac": round(fl * steps / dt / PEAK_FP32_MFMA, 4),
+            "first_loss": round(losses[0], 5), "last_loss": round(losses[-1], 5),
+            "last_grad_norm": round(norm, 5)}
+
+
 def loss_leg(m: cngpt_amd.Model, cfg, B: int, T: int, steps: int):
     """Cross-entropy (cross_entropy_fwd semantics) of the [B, T, V] logits the
     last forward left in HBM against next-token targets: `steps` launches,
@@ -277,6 +328,9 @@ def main():
                          "model (for kernel traces of one prefill shape)")
     ap.add_argument("--last", action="store_true",
                     help="with --prefill: final-position logits (gpt_forward_fast's mode)")
+    ap.add_argument("--train", type=int, nargs=2, metavar=("B", "T"), default=None,
+                    help="only time training steps (zero_grad, forward with targets, backward, "
+                         "AdamW) of B x T tokens of the workload's model")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); "
@@ -305,6 +359,13 @@ def main():
                           "kernel_ms_per_forward": {k: round(v["ms"] / args.steps, 3)
                                                     for k, v in prof.items() if v["launches"]}}),
               flush=True)
+        return
+
+    if args.train:
+        tB, tT = args.train
+        res = train_leg(m, cfg, tB, tT, args.steps, args.warmup)
+        m.close()
+        print(json.dumps({"workload": name, **res}), flush=True)
         return
 
     if args.decode_only:

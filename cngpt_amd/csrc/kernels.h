@@ -219,11 +219,12 @@ hipError_t launch_gelu_bwd(float* d, const float* x, long n, hipStream_t s);
 // <= ldd, cols <= cols_p).
 hipError_t launch_transpose(const float* src, long lds, int rows, int cols, float* dst, long ldd,
                             int rows_p, int cols_p, hipStream_t s);
-// out[c] += sum over rows of Y[r][c] (partials of colsum_part_floats floats
-// at part, summed in row-chunk order).
-long colsum_part_floats(int rows, int cols);
-hipError_t launch_colsum_add(const float* Y, long ldy, int rows, int cols, float* part,
-                             float* out, hipStream_t s);
+// The same transpose, and out[c] += the column sums of src over its rows
+// (partials of transpose_colsum_floats floats at part, summed in row order).
+long transpose_colsum_floats(int rows, int cols);
+hipError_t launch_transpose_colsum(const float* src, long lds, int rows, int cols, float* dst,
+                                   long ldd, int rows_p, int cols_p, float* part, float* out,
+                                   hipStream_t s);
 // layernorm_bwd: dx += ..., dw += sum dout * xhat, db += sum dout over the
 // rows (partials of ln_bwd_part_floats floats at part). C a multiple of 4,
 // at most 2048.

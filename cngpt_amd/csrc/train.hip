@@ -54,18 +54,32 @@ __global__ void __launch_bounds__(256) k_gelu_bwd(f32x4* __restrict__ d,
 // dX = dY W) is transposed, with K padded to whole product steps. 64 x 64
 // tiles through LDS (one padded column per row keeps the column reads
 // conflict-free); reads along c and writes along r are both coalesced.
+// With colpart set, the tile's column sums over its 64 rows (in row order)
+// go to colpart[blockIdx.y][c]: the bias gradient's partial sums, formed
+// while dY passes through anyway.
 __global__ void __launch_bounds__(256) k_transpose(const float* __restrict__ src, long lds,
                                                    int rows, int cols, float* __restrict__ dst,
-                                                   long ldd, int rows_p, int cols_p) {
+                                                   long ldd, int rows_p, int cols_p,
+                                                   float* __restrict__ colpart) {
     __shared__ float t[64][65];
+    __shared__ float cs[4][64];
     const int c0 = blockIdx.x * 64, r0 = blockIdx.y * 64;
     const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
 #pragma unroll
     for (int i = 0; i < 16; i++) {
-        const int r = r0 + ty + 4 * i, c = c0 + tx;
-        t[ty + 4 * i][tx] = (r < rows && c < cols) ? src[(long)r * lds + c] : 0.f;
+        const int r = r0 + 16 * ty + i, c = c0 + tx;
+        t[16 * ty + i][tx] = (r < rows && c < cols) ? src[(long)r * lds + c] : 0.f;
     }
     __syncthreads();
+    if (colpart) {
+        float sum = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) sum += t[16 * ty + i][tx];
+        cs[ty][tx] = sum;
+        __syncthreads();
+        if (ty == 0 && c0 + tx < cols)
+            colpart[(long)blockIdx.y * cols + c0 + tx] = ((cs[0][tx] + cs[1][tx]) + cs[2][tx]) + cs[3][tx];
+    }
 #pragma unroll
     for (int i = 0; i < 16; i++) {
         const int c = c0 + ty + 4 * i, r = r0 + tx;
@@ -75,28 +89,35 @@ __global__ void __launch_bounds__(256) k_transpose(const float* __restrict__ src
 
 // ---------------------------------------------------------------- column sums
 
-constexpr int CS_ROWS = 64;  // rows per partial sum
-
-// part[chunk][c] = sum of Y[r][c] over the chunk's CS_ROWS rows, in order.
-__global__ void __launch_bounds__(256) k_colsum_part(const float* __restrict__ Y, long ldy,
-                                                     int rows, int cols,
-                                                     float* __restrict__ part) {
-    const int c = blockIdx.x * 256 + threadIdx.x;
-    if (c >= cols) return;
-    const int r0 = blockIdx.y * CS_ROWS, r1 = min(rows, r0 + CS_ROWS);
-    float s = 0.f;
-    for (int r = r0; r < r1; r++) s += Y[(long)r * ldy + c];
-    part[(long)blockIdx.y * cols + c] = s;
-}
-
-// out[c] += sum over the nparts partials of column c, in chunk order.
+// out[c] += sum over the nparts partials of column c: eight threads per
+// column each sum a contiguous run of partials (eight loads in flight),
+// then the eight run sums are added in run order.
+constexpr int FIN_SPLIT = 8;
 __global__ void __launch_bounds__(256) k_colsum_fin(const float* __restrict__ part, int nparts,
                                                     int cols, float* __restrict__ out) {
-    const int c = blockIdx.x * 256 + threadIdx.x;
-    if (c >= cols) return;
+    __shared__ float rs[FIN_SPLIT][256 / FIN_SPLIT];
+    const int cl = threadIdx.x % (256 / FIN_SPLIT), q = threadIdx.x / (256 / FIN_SPLIT);
+    const int c = blockIdx.x * (256 / FIN_SPLIT) + cl;
+    const int per = (nparts + FIN_SPLIT - 1) / FIN_SPLIT;
+    const int p0 = q * per, p1 = min(nparts, p0 + per);
     float s = 0.f;
-    for (int p = 0; p < nparts; p++) s += part[(long)p * cols + c];
-    out[c] += s;
+    if (c < cols)
+        for (int p = p0; p < p1; p += 8) {
+            float v[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[j] = part[(long)min(p + j, p1 - 1) * cols + c];
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                if (p + j < p1) s += v[j];
+        }
+    rs[q][cl] = s;
+    __syncthreads();
+    if (q == 0 && c < cols) {
+        float t = rs[0][cl];
+#pragma unroll
+        for (int k = 1; k < FIN_SPLIT; k++) t += rs[k][cl];
+        out[c] += t;
+    }
 }
 
 // ---------------------------------------------------------------- LayerNorm backward
@@ -255,14 +276,25 @@ __global__ void __launch_bounds__(256) k_sumsq_part(const float* __restrict__ g,
 // norm[0] = sqrt(sum of the partials, in order); coef[0] = clip / norm when
 // clip > 0 and norm > clip, else 1 (global_grad_norm / scale_grads,
 // ops.c:631-640, as gpt_adamw applies them, model.c:893-900).
-__global__ void k_norm_fin(const double* __restrict__ part, int nparts, float clip,
-                           float* __restrict__ norm, float* __restrict__ coef) {
-    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+// One workgroup: thread i sums partials i, i + 256, .. in order, then a
+// fixed-order tree.
+__global__ void __launch_bounds__(256) k_norm_fin(const double* __restrict__ part, int nparts,
+                                                  float clip, float* __restrict__ norm,
+                                                  float* __restrict__ coef) {
+    __shared__ double red[256];
     double s = 0.0;
-    for (int p = 0; p < nparts; p++) s += part[p];
-    const float nv = (float)sqrt(s);
-    norm[0] = nv;
-    coef[0] = (clip > 0.0f && nv > clip) ? clip / nv : 1.0f;
+    for (int p = threadIdx.x; p < nparts; p += 256) s += part[p];
+    red[threadIdx.x] = s;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if (threadIdx.x < o) red[threadIdx.x] += red[threadIdx.x + o];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        const float nv = (float)sqrt(red[0]);
+        norm[0] = nv;
+        coef[0] = (clip > 0.0f && nv > clip) ? clip / nv : 1.0f;
+    }
 }
 
 // gpt_adamw's update (model.c:901-919) with the gradient scaled by *coef
@@ -316,22 +348,23 @@ hipError_t launch_transpose(const float* src, long lds, int rows, int cols, floa
     if (rows_p <= 0 || cols_p <= 0) return hipSuccess;
     if (rows_p < rows || cols_p < cols || ldd < rows_p) return hipErrorInvalidValue;
     dim3 grid((cols_p + 63) / 64, (rows_p + 63) / 64);
-    k_transpose<<<grid, 256, 0, s>>>(src, lds, rows, cols, dst, ldd, rows_p, cols_p);
+    k_transpose<<<grid, 256, 0, s>>>(src, lds, rows, cols, dst, ldd, rows_p, cols_p, nullptr);
     return hipGetLastError();
 }
 
-long colsum_part_floats(int rows, int cols) {
-    return (long)((rows + CS_ROWS - 1) / CS_ROWS) * cols;
-}
+long transpose_colsum_floats(int rows, int cols) { return (long)((rows + 63) / 64) * cols; }
 
-hipError_t launch_colsum_add(const float* Y, long ldy, int rows, int cols, float* part,
-                             float* out, hipStream_t s) {
-    if (rows <= 0 || cols <= 0) return hipSuccess;
-    const int nparts = (rows + CS_ROWS - 1) / CS_ROWS;
-    k_colsum_part<<<dim3((cols + 255) / 256, nparts), 256, 0, s>>>(Y, ldy, rows, cols, part);
+hipError_t launch_transpose_colsum(const float* src, long lds, int rows, int cols, float* dst,
+                                   long ldd, int rows_p, int cols_p, float* part, float* out,
+                                   hipStream_t s) {
+    if (rows_p <= 0 || cols_p <= 0) return hipSuccess;
+    if (rows_p < rows || cols_p < cols || ldd < rows_p) return hipErrorInvalidValue;
+    dim3 grid((cols_p + 63) / 64, (rows_p + 63) / 64);
+    k_transpose<<<grid, 256, 0, s>>>(src, lds, rows, cols, dst, ldd, rows_p, cols_p, part);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    k_colsum_fin<<<(cols + 255) / 256, 256, 0, s>>>(part, nparts, cols, out);
+    const int nparts = (rows_p + 63) / 64;
+    k_colsum_fin<<<(cols + 31) / 32, 256, 0, s>>>(part, nparts, cols, out);
     return hipGetLastError();
 }
 
@@ -358,10 +391,10 @@ hipError_t launch_layernorm_bwd(const float* dout, const float* x, const float* 
 #undef LNB
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    k_colsum_fin<<<(C + 255) / 256, 256, 0, s>>>(pdw, nb, C, dw);
+    k_colsum_fin<<<(C + 31) / 32, 256, 0, s>>>(pdw, nb, C, dw);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
-    k_colsum_fin<<<(C + 255) / 256, 256, 0, s>>>(pdb, nb, C, db);
+    k_colsum_fin<<<(C + 31) / 32, 256, 0, s>>>(pdb, nb, C, db);
     return hipGetLastError();
 }
 
@@ -399,7 +432,7 @@ hipError_t launch_adamw(float* p, float* g, float* m, float* v, const unsigned c
     k_sumsq_part<<<np, 256, 0, s>>>(g, n, part);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    k_norm_fin<<<1, 64, 0, s>>>(part, np, clip, norm, coef);
+    k_norm_fin<<<1, 256, 0, s>>>(part, np, clip, norm, coef);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     k_adamw<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(p, g, m, v, decay, n, coef, lr, beta1,

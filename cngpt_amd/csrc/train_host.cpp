@@ -131,11 +131,12 @@ int linear_dx(cngpt_hip_train* t, hipStream_t s, const float* dY, const float* W
 int linear_dw(cngpt_hip_train* t, hipStream_t s, const float* dY, long ldy, const float* X,
               float* dW, float* db, long out, long in) {
     const int N = (int)t->N, Np = (int)t->Np;
-    TRY(launch_transpose(dY, ldy, N, (int)out, t->tA, Np, Np, (int)out, s));
+    if (db)
+        TRY(launch_transpose_colsum(dY, ldy, N, (int)out, t->tA, Np, Np, (int)out, t->red, db, s));
+    else
+        TRY(launch_transpose(dY, ldy, N, (int)out, t->tA, Np, Np, (int)out, s));
     TRY(launch_transpose(X, in, N, (int)in, t->tB, Np, Np, (int)in, s));
-    if (gemm(t, s, t->tA, t->tB, t->zeros, dW, out, in, Np, EPI_RESID)) return -1;
-    if (db) TRY(launch_colsum_add(dY, ldy, N, (int)out, t->red, db, s));
-    return 0;
+    return gemm(t, s, t->tA, t->tB, t->zeros, dW, out, in, Np, EPI_RESID);
 }
 
 int check_ids(const int* ids, long n, int V, const char* what) {
@@ -201,7 +202,8 @@ int cngpt_hip_train_create(cngpt_hip_ctx* h, int B, int T, cngpt_hip_train** out
     fl(4 * C * Np);                           // tB
     fl(std::max(C * Vp, 4 * C * C));          // tW
     fl(PART_FLOATS);                          // part
-    fl(std::max(colsum_part_floats((int)N, (int)(4 * C)), ln_bwd_part_floats((int)N, (int)C)));
+    fl(std::max(transpose_colsum_floats((int)Np, (int)(4 * C)),
+                ln_bwd_part_floats((int)N, (int)C)));
     fl(4 * C);                                // zeros
     sz.push_back((size_t)grad_norm_parts(n) * sizeof(double));
     fl(1); fl(1);                             // norm, coef
