@@ -9,6 +9,9 @@ logits [16, 1024, 50257] left in HBM. Prints one JSON line:
   loss      cross-entropy of those logits against next-token targets, on
             the device (HBM-bound; GB/s of one read of the logits);
   load      the weights as a weight file streamed to the device;
+  train     training steps on the device (zero_grad, forward with targets,
+            backward, AdamW) at B=4 T=1024, tokens/s and the algorithmic
+            FLOPs against the fp32 matrix peak;
   decode    greedy single-token steps with the KV cache (B=1: all steps in
             one persistent launch; otherwise one replayed HIP graph per
             step), tok/s and algorithmic HBM bytes / time;
@@ -420,6 +423,8 @@ def main():
     ref_shape = reference_shape(m) if name == "small" else None
     share = dp_share(m, cfg) if name == "small" else None
     load = load_leg(m, cfg, params)
+    # training steps on the device at `cngpt train`'s default batch (4 x 1024)
+    train = train_leg(m, cfg, 4, 1024, 5, 2) if name == "small" else None
     m.close()
 
     # HBM-side bytes per GEMM launch from the committed rocprofv3 --pmc
@@ -463,6 +468,7 @@ def main():
         "gemm_mfma_util_pct": round(100 * achieved / PEAK_FP32_MFMA, 2),
         "loss": loss,
         "load": load,
+        "train": train,
         "decode": {"tok_s": round(dsteps * dB / dec_dt, 1),
                    "ms_per_step": round(dec_dt * 1e3 / dsteps, 4),
                    "prompt": prompt, "steps": dsteps, "B": dB, "sampling": "greedy", "path": dec_path,
