@@ -27,3 +27,10 @@ def test_reference_layout_fastctx():
     """The library driven through the reference's 80-byte FastCtx
     (src/fast.h:35-45), guard bytes on both sides."""
     _run("check_refctx")
+
+
+def test_training_step_from_c():
+    """cngpt_hip_train_* in the reference's training-loop order from a C
+    host (src/cngpt.c:150-165), against the oracle's step."""
+    _run("check_train_hip")
+
