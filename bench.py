@@ -353,6 +353,7 @@ def main():
         dt, prof = prefill(m, cfg, pB, pT, args.steps, args.warmup, mode)
         g = prof["gemm"]
         m.close()
+        calib = copy_calibration(args.copy_calibration << 20) if args.copy_calibration else None
         print(json.dumps({"workload": name, "B": pB, "T": pT,
                           "logits": "final position" if args.last else "all positions",
                           "tok_s": round(pB * pT * args.steps / dt, 1),
@@ -360,7 +361,8 @@ def main():
                           "gemm_tflops": round(g["flops"] / (g["ms"] * 1e-3) / 1e12, 2),
                           "gemm_frac": round(g["flops"] / (g["ms"] * 1e-3) / PEAK_FP32_MFMA, 4),
                           "kernel_ms_per_forward": {k: round(v["ms"] / args.steps, 3)
-                                                    for k, v in prof.items() if v["launches"]}}),
+                                                    for k, v in prof.items() if v["launches"]},
+                          "copy_calibration_bytes": calib}),
               flush=True)
         return
 
