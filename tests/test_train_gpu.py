@@ -85,6 +85,36 @@ def test_forward_backward_vs_oracle(name):
     ref.close()
 
 
+def test_gpt2_small_full_depth_step():
+    """GPT-2 small at full depth and width (the bench's training model),
+    B=2 T=128, seeded weights with LayerNorm gains and biases randomised:
+    loss and every parameter's gradient, then one AdamW step."""
+    cfg, B, T = cngpt_amd.GPT2_SMALL, 2, 128
+    params = randomize(cfg, cngpt_amd.init_weights(cfg, 1234), 5)
+    tok, tgt = batch(cfg, B, T, 17)
+    say("gpt2 small full depth: oracle step")
+    ref = oracle.Trainer(ocfg(cfg), params, B, T)
+    ref.zero_grad()
+    ref_loss = ref.forward(tok, tgt)
+    ref.backward()
+    with cngpt_amd.Model(cfg, params) as m, cngpt_amd.Trainer(m, B, T) as tr:
+        loss = tr.forward(tok, tgt)
+        tr.backward()
+        grads = tr.grads
+        norm = tr.adamw(3e-4, 0.9, 0.95, 1e-8, 0.1, 1.0)
+        p = tr.params
+    say(f"  loss {loss:.6f} vs {ref_loss:.6f}")
+    assert abs(loss - ref_loss) <= 1e-5 * abs(ref_loss)
+    compare_grads(cfg, grads, ref.grads, what="gpt2 small")
+    want = float(np.sqrt((ref.grads.astype(np.float64) ** 2).sum()))
+    assert abs(norm - want) <= 1e-4 * want
+    ref.adamw(3e-4, 0.9, 0.95, 1e-8, 0.1, 1.0)
+    err = np.abs(p - ref.params)
+    say(f"  after AdamW: max|dparam| {err.max():.2e}, {int((err > 1e-5).sum())} above 1e-5")
+    assert err.max() <= 2 * 3e-4 and np.mean(err > 1e-5) < 1e-3
+    ref.close()
+
+
 def test_gradients_accumulate_reproducibly_and_zero_grad_clears():
     cfg, B, T = CASES["hs64"]
     params = randomize(cfg, cngpt_amd.init_weights(cfg, 21), 22)
