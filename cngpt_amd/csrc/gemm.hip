@@ -171,7 +171,16 @@ struct DlSmem {
 // acc = X[m0.., kb..] . W[n0.., kb..]^T over nk steps of BK (acc zeroed
 // first). On return every wavefront is done reading the stages it used only
 // once the caller passes a barrier.
-template <int BK, int S>
+//
+// KM (bit 0: X, bit 1: W) marks an operand stored K-major, row k of
+// a.ldx / a.ldw floats holding the tile's rows as columns (the backward's
+// dW = dY^T X reads dY and X this way instead of transposing them). Its
+// stage holds BK rows of k, 32 granules of 4 rows (m or n) each; the
+// granule order of the second half of the rows (the k the upper half
+// wavefront reads) is XORed with 8, which puts the two half-wavefronts'
+// reads of one row range 128 bytes apart, in different LDS banks. A lane
+// then reads its 4 k one row apart instead of as one 16-byte read.
+template <int BK, int S, int KM = 0>
 __device__ __forceinline__ void dl_tile(const GemmArgs& a, int m0, int n0, int kb, int nk,
                                         float* sm, int wave, int lane, f32x16 (&acc)[2][2]) {
     constexpr int GPR = BK / 4;      // granules per row
@@ -179,6 +188,7 @@ __device__ __forceinline__ void dl_tile(const GemmArgs& a, int m0, int n0, int k
     constexpr int NI = GPR / 2;      // load instructions per operand per stage per wavefront
     constexpr int NG = BK / 8;       // MFMA groups per step
     constexpr int TILE = BM * BK;    // floats per operand per stage
+    constexpr bool XKM = KM & 1, WKM = KM & 2;
     static_assert(BM == BN && BM * GPR == NI * 4 * 64, "one granule per lane per instruction");
     const int K = a.K;
 
@@ -189,17 +199,23 @@ __device__ __forceinline__ void dl_tile(const GemmArgs& a, int m0, int n0, int k
     for (int i = 0; i < NI; i++) {
         const int g = (i * 4 + wave) * 64 + lane;
         const int row = g / GPR, kq = (g % GPR) ^ ((row / RSW) % GPR);
-        xp[i] = a.X + (long)min(m0 + row, a.M - 1) * K + kb + 4 * kq;
-        wp[i] = a.W + (long)min(n0 + row, a.N - 1) * K + kb + 4 * kq;
+        // K-major: row k = g / 32 of the stage, columns 4 * mq .. + 3
+        const int kr = g / (BM / 4), mq = (g % (BM / 4)) ^ ((((2 * kr) / BK) & 1) << 3);
+        if (XKM) xp[i] = a.X + (long)(kb + kr) * a.ldx + min(m0 + 4 * mq, (int)a.ldx - 4);
+        else xp[i] = a.X + (long)min(m0 + row, a.M - 1) * K + kb + 4 * kq;
+        if (WKM) wp[i] = a.W + (long)(kb + kr) * a.ldw + min(n0 + 4 * mq, (int)a.ldw - 4);
+        else wp[i] = a.W + (long)min(n0 + row, a.N - 1) * K + kb + 4 * kq;
     }
+    const long xstep = XKM ? BK * a.ldx : BK, wstep = WKM ? BK * a.ldw : BK;
     auto issue = [&](int kt, int st) {
         float* base = sm + st * 2 * TILE;
 #pragma unroll
         for (int i = 0; i < NI; i++) {
             float* la = base + (i * 4 + wave) * 64 * 4;
-            __builtin_amdgcn_global_load_lds((const void*)(xp[i] + kt * BK), (lds_void*)la, 16, 0, 0);
-            __builtin_amdgcn_global_load_lds((const void*)(wp[i] + kt * BK), (lds_void*)(la + TILE), 16,
-                                             0, 0);
+            __builtin_amdgcn_global_load_lds((const void*)(xp[i] + kt * xstep), (lds_void*)la, 16, 0,
+                                             0);
+            __builtin_amdgcn_global_load_lds((const void*)(wp[i] + kt * wstep), (lds_void*)(la + TILE),
+                                             16, 0, 0);
         }
     };
 
@@ -240,10 +256,25 @@ __device__ __forceinline__ void dl_tile(const GemmArgs& a, int m0, int n0, int k
 #pragma unroll
         for (int g = 0; g < NG; g++) {
             f32x4 av[2], bv[2];
+            const int ka = 4 * (lh * NG + g);  // first k of this lane's 4 (K-major stages)
 #pragma unroll
-            for (int i = 0; i < 2; i++) av[i] = *(const f32x4*)&base[ao[i][g]];
+            for (int i = 0; i < 2; i++) {
+                if (XKM) {
+                    const float* p = base + ka * BM + ((wm + i * 32 + lr) ^ (32 * lh));
+                    av[i] = f32x4{p[0], p[BM], p[2 * BM], p[3 * BM]};
+                } else {
+                    av[i] = *(const f32x4*)&base[ao[i][g]];
+                }
+            }
 #pragma unroll
-            for (int j = 0; j < 2; j++) bv[j] = *(const f32x4*)&base[bo[j][g]];
+            for (int j = 0; j < 2; j++) {
+                if (WKM) {
+                    const float* p = base + TILE + ka * BN + ((wn + j * 32 + lr) ^ (32 * lh));
+                    bv[j] = f32x4{p[0], p[BN], p[2 * BN], p[3 * BN]};
+                } else {
+                    bv[j] = *(const f32x4*)&base[bo[j][g]];
+                }
+            }
 #pragma unroll
             for (int e = 0; e < 4; e++)
 #pragma unroll
@@ -270,7 +301,7 @@ __device__ __forceinline__ void store_partial(float* p, const f32x16 (&acc)[2][2
 // [ks * KR, min(K, (ks + 1) * KR)) and stores its partial tile to a.part +
 // ks * M * N (rows of N floats); the reduce kernel sums the KS partials in
 // order and applies the epilogue.
-template <int EPI, int BK, int S, int OCC>
+template <int EPI, int BK, int S, int OCC, int KM = 0>
 __global__ void __launch_bounds__(NTHREADS, OCC) k_gemm_dl(GemmArgs a, int tiles_m, int tiles_n,
                                                           int KR, int KS) {
     __shared__ __attribute__((aligned(1024))) DlSmem<BK, S> sh;
@@ -285,7 +316,7 @@ __global__ void __launch_bounds__(NTHREADS, OCC) k_gemm_dl(GemmArgs a, int tiles
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int kb = ks * KR;
     f32x16 acc[2][2];
-    dl_tile<BK, S>(a, m0, n0, kb, min(KR, a.K - kb) / BK, sh.sm, wave, lane, acc);
+    dl_tile<BK, S, KM>(a, m0, n0, kb, min(KR, a.K - kb) / BK, sh.sm, wave, lane, acc);
     const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
     if (KS == 1) {
         tile_store<EPI>(a, acc, m0 + wm, n0 + wn, lane);
@@ -833,6 +864,18 @@ int sk_workgroups(const GemmArgs& a, int tiles) {
     return tiles < G ? cus : G;
 }
 
+// Both operands K-major (a.km == 3), the residual epilogue: whole 128 x 128
+// tiles, or K split over the CUs when the tiles are too few (no stream-K).
+hipError_t gemm_km(const GemmArgs& a, hipStream_t s) {
+    const int tiles_m = (a.M + BM - 1) / BM, tiles_n = (a.N + BN - 1) / BN;
+    const int tiles = tiles_m * tiles_n;
+    int KR;
+    const int KS = tile_splits(a, tiles, &KR);
+    k_gemm_dl<EPI_RESID, 32, 2, 2, 3><<<tiles * KS, NTHREADS, 0, s>>>(a, tiles_m, tiles_n, KS > 1 ? KR : a.K, KS);
+    const hipError_t e = hipGetLastError();
+    return e != hipSuccess || KS == 1 ? e : reduce_splits<EPI_RESID>(a, KS, s);
+}
+
 template <int EPI>
 hipError_t gemm_epi(const GemmArgs& a, hipStream_t s) {
     const int tiles_m = (a.M + BM - 1) / BM, tiles_n = (a.N + BN - 1) / BN;
@@ -884,6 +927,16 @@ hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
     if (a.ln_out && (a.epi != EPI_RESID || a.seg || a.row_off || a.row_off_dev || (a.N & 3) ||
                      (a.ldy & 3) || a.N > 2048 || !a.ln_w || !a.ln_b))
         return hipErrorInvalidValue;
+    if (a.km) {
+        // K-major operands: the residual (accumulating) epilogue of the dW
+        // products, plain row-major output, K whole steps, rows of whole
+        // granules (ld a multiple of 4 covering the tile's rows rounded to 4)
+        if (a.km != 3 || a.epi != EPI_RESID || a.M <= SKINNY_MAX_M || a.K % 32 || a.seg ||
+            a.row_off || a.row_off_dev || a.ln_out || (a.ldx & 3) || (a.ldw & 3) ||
+            a.ldx < ((a.M + 3) & ~3) || a.ldw < ((a.N + 3) & ~3))
+            return hipErrorInvalidValue;
+        return gemm_km(a, s);
+    }
     if (a.M <= SKINNY_MAX_M) {
         switch (a.epi) {
             case EPI_STORE: return skinny_epi<EPI_STORE>(a, s);

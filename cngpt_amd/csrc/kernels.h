@@ -40,6 +40,12 @@ struct GemmArgs {
     const float* ln_w;
     const float* ln_b;
     float* ln_out;
+    // Optional K-major operands (km = 3: both; the residual epilogue, M >
+    // SKINNY_MAX_M, K a multiple of 32): X is [K][ldx] (row k holds the M
+    // rows' k-th values), W is [K][ldw]; ldx and ldw multiples of 4, at
+    // least M and N rounded up to 4. 0: both K-contiguous, rows of K floats.
+    int km;
+    long ldx, ldw;
 };
 // M <= SKINNY_MAX_M rows take the weight-streaming k_stream, larger M the
 // 128 x 128 MFMA tiles.
@@ -219,6 +225,11 @@ hipError_t launch_gelu_bwd(float* d, const float* x, long n, hipStream_t s);
 // <= ldd, cols <= cols_p).
 hipError_t launch_transpose(const float* src, long lds, int rows, int cols, float* dst, long ldd,
                             int rows_p, int cols_p, hipStream_t s);
+// out[c] += sum over rows of Y[r][c] (partials of colsum_part_floats floats
+// at part, summed in row-chunk order).
+long colsum_part_floats(int rows, int cols);
+hipError_t launch_colsum_add(const float* Y, long ldy, int rows, int cols, float* part,
+                             float* out, hipStream_t s);
 // The same transpose, and out[c] += the column sums of src over its rows
 // (partials of transpose_colsum_floats floats at part, summed in row order).
 long transpose_colsum_floats(int rows, int cols);

@@ -89,6 +89,28 @@ __global__ void __launch_bounds__(256) k_transpose(const float* __restrict__ src
 
 // ---------------------------------------------------------------- column sums
 
+constexpr int CS_ROWS = 64;  // rows per partial column sum
+
+// part[chunk][c] = sum of Y[r][c] over the chunk's CS_ROWS rows, in order
+// (eight loads in flight per thread).
+__global__ void __launch_bounds__(256) k_colsum_part(const float* __restrict__ Y, long ldy,
+                                                     int rows, int cols,
+                                                     float* __restrict__ part) {
+    const int c = blockIdx.x * 256 + threadIdx.x;
+    if (c >= cols) return;
+    const int r0 = blockIdx.y * CS_ROWS, r1 = min(rows, r0 + CS_ROWS);
+    float s = 0.f;
+    for (int r = r0; r < r1; r += 8) {
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[j] = Y[(long)min(r + j, r1 - 1) * ldy + c];
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            if (r + j < r1) s += v[j];
+    }
+    part[(long)blockIdx.y * cols + c] = s;
+}
+
 // out[c] += sum over the nparts partials of column c: eight threads per
 // column each sum a contiguous run of partials (eight loads in flight),
 // then the eight run sums are added in run order.
@@ -364,6 +386,21 @@ hipError_t launch_transpose_colsum(const float* src, long lds, int rows, int col
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int nparts = (rows_p + 63) / 64;
+    k_colsum_fin<<<(cols + 31) / 32, 256, 0, s>>>(part, nparts, cols, out);
+    return hipGetLastError();
+}
+
+long colsum_part_floats(int rows, int cols) {
+    return (long)((rows + CS_ROWS - 1) / CS_ROWS) * cols;
+}
+
+hipError_t launch_colsum_add(const float* Y, long ldy, int rows, int cols, float* part,
+                             float* out, hipStream_t s) {
+    if (rows <= 0 || cols <= 0) return hipSuccess;
+    const int nparts = (rows + CS_ROWS - 1) / CS_ROWS;
+    k_colsum_part<<<dim3((cols + 255) / 256, nparts), 256, 0, s>>>(Y, ldy, rows, cols, part);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
     k_colsum_fin<<<(cols + 31) / 32, 256, 0, s>>>(part, nparts, cols, out);
     return hipGetLastError();
 }

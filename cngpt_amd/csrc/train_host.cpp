@@ -127,10 +127,26 @@ int linear_dx(cngpt_hip_train* t, hipStream_t s, const float* dY, const float* W
 }
 
 // dW [out, in] += dY^T . X, db [out] += column sums of dY (db may be null);
-// dY rows are ldy floats apart, X rows `in`.
+// dY rows are ldy floats apart, X rows `in`. Over more than SKINNY_MAX_M
+// outputs the product reads dY and X K-major, straight from their row
+// buffers (rows N .. Np-1 of which are zero); fewer go through transposed
+// copies (the few-row products take K-contiguous operands only).
 int linear_dw(cngpt_hip_train* t, hipStream_t s, const float* dY, long ldy, const float* X,
               float* dW, float* db, long out, long in) {
     const int N = (int)t->N, Np = (int)t->Np;
+    if (out > SKINNY_MAX_M) {
+        if (db) TRY(launch_colsum_add(dY, ldy, N, (int)out, t->red, db, s));
+        GemmArgs a{};
+        a.X = dY; a.ldx = ldy; a.W = X; a.ldw = in; a.km = 3;
+        a.bias = t->zeros; a.Y = dW;
+        a.M = (int)out; a.N = (int)in; a.K = Np;
+        a.ldy = in;
+        a.epi = EPI_RESID;
+        a.part = t->part;
+        a.part_cap = PART_FLOATS;
+        TRY(launch_gemm(a, s));
+        return 0;
+    }
     if (db)
         TRY(launch_transpose_colsum(dY, ldy, N, (int)out, t->tA, Np, Np, (int)out, t->red, db, s));
     else
@@ -178,32 +194,42 @@ int cngpt_hip_train_create(cngpt_hip_ctx* h, int B, int T, cngpt_hip_train** out
     t->device = v.device;
     const long N = t->N, Np = t->Np, Vp = t->Vp, n = v.n_params;
 
-    // one allocation, carved in this order
+    // one allocation, carved in this order; buffers of B*T rows hold Np rows
+    // (the padding rows stay zero: the dW products read them as K)
     std::vector<size_t> sz;
     auto fl = [&](long count) { sz.push_back((size_t)std::max(count, 1L) * sizeof(float)); };
     fl(n); fl(n); fl(n);                     // grads, m, v
     sz.push_back((size_t)n);                  // decay mask
-    fl(N * C);                                // emb
+    fl(Np * C);                               // emb
     for (long l = 0; l < L; l++) {
-        fl(N * C); fl(N); fl(N);              // ln1_out, mean, rstd
-        fl(N * 3 * C); fl(B * H * T);         // qkv, lse
-        fl(N * C); fl(N * C);                 // attn_out, res1
-        fl(N * C); fl(N); fl(N);              // ln2_out, mean, rstd
-        fl(N * 4 * C); fl(N * 4 * C);         // fc_out, gelu
-        fl(N * C);                            // res2
+        fl(Np * C); fl(N); fl(N);             // ln1_out, mean, rstd
+        fl(Np * 3 * C); fl(B * H * T);        // qkv, lse
+        fl(Np * C); fl(Np * C);               // attn_out, res1
+        fl(Np * C); fl(N); fl(N);             // ln2_out, mean, rstd
+        fl(Np * 4 * C); fl(Np * 4 * C);       // fc_out, gelu
+        fl(Np * C);                           // res2
     }
-    fl(N * C); fl(N); fl(N); fl(N * V);       // lnf_out, mean, rstd, logits
+    fl(Np * C); fl(N); fl(N); fl(N * V);      // lnf_out, mean, rstd, logits
     for (int i = 0; i < 5; i++) fl(N + 1);    // tok, tgt, uniq, ustart, upos
     fl(N); fl(1); fl(4);                      // row_loss, loss, err
-    fl(N * Vp);                               // dlog
-    fl(N * C); fl(N * C); fl(N * C); fl(N * C);  // d_x, d_res1, d_ln, d_attn
-    fl(N * 3 * C); fl(N * 4 * C); fl(B * H * T); // d_qkv, d_hid, D
-    fl(std::max(V, 4 * C) * Np);              // tA
-    fl(4 * C * Np);                           // tB
+    fl(Np * Vp);                              // dlog
+    fl(Np * C); fl(Np * C); fl(Np * C); fl(Np * C);  // d_x, d_res1, d_ln, d_attn
+    fl(Np * 3 * C); fl(Np * 4 * C); fl(B * H * T);   // d_qkv, d_hid, D
+    // transposed operands of the dW products with at most SKINNY_MAX_M
+    // outputs (dY^T, X^T), and of every dX product (W^T)
+    long ta = 0, tb = 0;
+    const long dw_shapes[5][2] = {{C, 4 * C}, {4 * C, C}, {C, C}, {3 * C, C}, {V, C}};
+    for (const auto& d : dw_shapes)
+        if (d[0] <= SKINNY_MAX_M) {
+            ta = std::max(ta, d[0] * Np);
+            tb = std::max(tb, d[1] * Np);
+        }
+    fl(ta); fl(tb);                           // tA, tB
     fl(std::max(C * Vp, 4 * C * C));          // tW
     fl(PART_FLOATS);                          // part
-    fl(std::max(transpose_colsum_floats((int)Np, (int)(4 * C)),
-                ln_bwd_part_floats((int)N, (int)C)));
+    fl(std::max({transpose_colsum_floats((int)Np, (int)(4 * C)),
+                 colsum_part_floats((int)N, (int)(4 * C)),
+                 ln_bwd_part_floats((int)N, (int)C)}));
     fl(4 * C);                                // zeros
     sz.push_back((size_t)grad_norm_parts(n) * sizeof(double));
     fl(1); fl(1);                             // norm, coef
@@ -263,12 +289,10 @@ int cngpt_hip_train_create(cngpt_hip_ctx* h, int B, int T, cngpt_hip_train** out
     }
     hipStream_t s = v.stream;
     int rc = 0;
-    if (hipMemcpyAsync(t->decay, mask.data(), (size_t)n, hipMemcpyHostToDevice, s) != hipSuccess ||
-        hipMemsetAsync(t->grads, 0, (size_t)n * sizeof(float), s) != hipSuccess ||
-        hipMemsetAsync(t->m, 0, (size_t)n * sizeof(float), s) != hipSuccess ||
-        hipMemsetAsync(t->v, 0, (size_t)n * sizeof(float), s) != hipSuccess ||
-        hipMemsetAsync(t->zeros, 0, (size_t)4 * C * sizeof(float), s) != hipSuccess ||
-        hipMemsetAsync(t->err, 0, 4 * sizeof(int), s) != hipSuccess ||
+    // everything starts at zero: gradients, moments, the zero bias, the
+    // error flags and the padding rows
+    if (hipMemsetAsync(t->arena, 0, total, s) != hipSuccess ||
+        hipMemcpyAsync(t->decay, mask.data(), (size_t)n, hipMemcpyHostToDevice, s) != hipSuccess ||
         hipStreamSynchronize(s) != hipSuccess)
         rc = ctx_fail("trainer set-up failed: %s", hipGetErrorString(hipGetLastError()));
     if (rc) {
