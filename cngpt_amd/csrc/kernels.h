@@ -214,8 +214,12 @@ hipError_t launch_attention_causal(const float* qkv, long seq_stride, float* out
 // log(sum_v exp(x_v - max)) - (x[target] - max), loss[0] = their mean.
 // probs != 0 overwrites the logits with their softmax. Targets outside
 // [0, V) are clamped and reported through *err (bit 2).
+// dl != 0 (probs 0): the logits stay, and dl [rows][ldd] (ldd >= V, a
+// multiple of 4) gets the mean loss's gradient (p - onehot) / rows, zero in
+// columns V .. ldd-1.
 hipError_t launch_cross_entropy(float* logits, long rows, int V, const int* targets,
-                                float* row_loss, float* loss, int probs, int* err, hipStream_t s);
+                                float* row_loss, float* loss, int probs, int* err, hipStream_t s,
+                                float* dl = nullptr, long ldd = 0);
 
 // train.hip: the training step's elementwise, row and reduction kernels.
 // out = gelu(in); d = d * gelu'(x) (n a multiple of 4).
@@ -243,9 +247,6 @@ long ln_bwd_part_floats(int rows, int C);
 hipError_t launch_layernorm_bwd(const float* dout, const float* x, const float* w,
                                 const float* mean, const float* rstd, float* dx, float* dw,
                                 float* db, int rows, int C, float* part, hipStream_t s);
-// dl [rows][ldd] = scale * (probs - onehot(targets)), zero for columns >= V.
-hipError_t launch_ce_bwd(const float* probs, int V, const int* targets, float scale, float* dl,
-                         long ldd, long rows, hipStream_t s);
 // g_wpe[t] += sum_b dx[b][t]; g_wte[uniq[u]] += dx rows pos[start[u] ..
 // start[u+1]) in order, for each of the nuniq distinct tokens.
 hipError_t launch_embed_bwd(const float* dx, int B, int T, int C, float* g_wpe, float* g_wte,

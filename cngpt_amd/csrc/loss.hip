@@ -65,11 +65,16 @@ __device__ __forceinline__ float rescale(float m, float M) {
 
 // One workgroup per row. Writes the row term log(sum) - (x[target] - max)
 // to row_loss[row]; with probs, overwrites the row with
-// exp(x - max) * (1 / sum) (ops.c:557-566).
+// exp(x - max) * (1 / sum) (ops.c:557-566); with dl, leaves the logits and
+// writes the gradient of the mean loss instead, dl[row][v] = gscale *
+// (p_v - [v == target]) (cross_entropy_bwd, ops.c:576-589, with gscale = 1 /
+// rows), zero for V <= v < ldd (rows of ldd floats, 16-byte aligned).
 __global__ void __launch_bounds__(CE_THREADS) k_ce_rows(float* __restrict__ logits, int V,
                                                          const int* __restrict__ targets,
                                                          float* __restrict__ row_loss, int probs,
-                                                         int* __restrict__ err) {
+                                                         int* __restrict__ err,
+                                                         float* __restrict__ dl, long ldd,
+                                                         float gscale) {
     __shared__ float sm[CE_WAVES], ss[CE_WAVES];
     __shared__ float s_max, s_inv;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -134,9 +139,23 @@ __global__ void __launch_bounds__(CE_THREADS) k_ce_rows(float* __restrict__ logi
         s_max = M;
         s_inv = 1.0f / S;
     }
-    if (!probs) return;
+    if (!probs && !dl) return;
     __syncthreads();
     const float M = s_max, inv = s_inv;
+    if (dl) {
+        f32x4* d4 = (f32x4*)(dl + row * ldd);
+        for (int k = tid; k < (int)(ldd >> 2); k += CE_THREADS) {
+            f32x4 g;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int v = 4 * k + e;
+                const float x = lg[min(v, V - 1)];
+                g[e] = v < V ? gscale * (exp_of(x - M) * inv - (v == tg ? 1.0f : 0.0f)) : 0.f;
+            }
+            __builtin_nontemporal_store(g, d4 + k);
+        }
+        return;
+    }
     if (tid < head) lg[tid] = exp_of(lg[tid] - M) * inv;
     if (tid < V - tail0) lg[tail0 + tid] = exp_of(lg[tail0 + tid] - M) * inv;
     f32x4* w4 = (f32x4*)(lg + head);
@@ -170,10 +189,13 @@ __global__ void __launch_bounds__(MEAN_THREADS) k_ce_mean(const float* __restric
 }  // namespace
 
 hipError_t launch_cross_entropy(float* logits, long rows, int V, const int* targets,
-                                float* row_loss, float* loss, int probs, int* err, hipStream_t s) {
+                                float* row_loss, float* loss, int probs, int* err, hipStream_t s,
+                                float* dl, long ldd) {
     if (rows <= 0 || V <= 0) return hipErrorInvalidValue;
     if (rows > 0x7fffffffL) return hipErrorInvalidValue;
-    k_ce_rows<<<(unsigned)rows, CE_THREADS, 0, s>>>(logits, V, targets, row_loss, probs, err);
+    if (dl && (probs || ldd < V || (ldd & 3))) return hipErrorInvalidValue;
+    k_ce_rows<<<(unsigned)rows, CE_THREADS, 0, s>>>(logits, V, targets, row_loss, probs, err, dl,
+                                                    ldd, 1.0f / (float)rows);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     k_ce_mean<<<1, MEAN_THREADS, 0, s>>>(row_loss, rows, loss);

@@ -220,27 +220,6 @@ __global__ void __launch_bounds__(256) k_ln_bwd(const float* __restrict__ dout,
     }
 }
 
-// ---------------------------------------------------------------- cross-entropy backward
-
-// cross_entropy_bwd (ops.c:576-589): dlogits[r][v] = scale * (probs[r][v]
-// - [v == target[r]]) for v < V, zero for V <= v < ldd (the padding that
-// makes K of the lm_head's dX product whole steps). Targets were clamped
-// and reported by the forward's cross-entropy.
-__global__ void __launch_bounds__(256) k_ce_bwd(const float* __restrict__ probs, int V,
-                                                const int* __restrict__ targets, float scale,
-                                                float* __restrict__ dl, long ldd, long rows) {
-    const long i = (long)blockIdx.x * 256 + threadIdx.x;
-    if (i >= rows * ldd) return;
-    const long r = i / ldd;
-    const int v = (int)(i - r * ldd);
-    float d = 0.f;
-    if (v < V) {
-        const int t = min(max(targets[r], 0), V - 1);
-        d = scale * (probs[r * V + v] - (v == t ? 1.0f : 0.0f));
-    }
-    dl[i] = d;
-}
-
 // ---------------------------------------------------------------- embedding backward
 
 // g_wpe[t][c] += sum over b of dx[b][t][c], in b order (model.c:850-858).
@@ -432,15 +411,6 @@ hipError_t launch_layernorm_bwd(const float* dout, const float* x, const float* 
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     k_colsum_fin<<<(C + 31) / 32, 256, 0, s>>>(pdb, nb, C, db);
-    return hipGetLastError();
-}
-
-hipError_t launch_ce_bwd(const float* probs, int V, const int* targets, float scale, float* dl,
-                         long ldd, long rows, hipStream_t s) {
-    if (rows <= 0) return hipSuccess;
-    if (ldd < V) return hipErrorInvalidValue;
-    const long n = rows * ldd;
-    k_ce_bwd<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(probs, V, targets, scale, dl, ldd, rows);
     return hipGetLastError();
 }
 

@@ -6,7 +6,8 @@
 // QKV product -> causal attention (its base-2 log-sum-exp kept) -> res1 =
 // x + c_proj product -> LN2 -> fc product (pre-activation kept) -> GELU ->
 // res2 = res1 + proj product } -> LN_f -> lm_head -> cross-entropy, whose
-// pass leaves the probabilities in place of the logits.
+// pass also writes the gradient of the loss over the logits (the
+// reference keeps the probabilities and forms it in gpt_backward).
 //
 // Backward (model.c:634-877), per linear layer Y = X W^T + b:
 //   dX = dY W           product of dY [rows, out] and W^T [in, out]
@@ -366,7 +367,11 @@ int cngpt_hip_train_forward(cngpt_hip_train* t, const int* tokens, const int* ta
     TRY(launch_layernorm(x, C, v.lnf_w, v.lnf_b, t->lnf_out, C, (int)N, C, s, t->lnf_mean,
                          t->lnf_rstd));
     if (gemm(t, s, t->lnf_out, v.wte, nullptr, t->logits, N, V, C, EPI_STORE)) return -1;
-    TRY(launch_cross_entropy(t->logits, N, V, t->tgt, t->row_loss, t->loss, 1, t->err, s));
+    // the loss, and the gradient of the mean loss for the backward
+    // (cross_entropy_bwd) into the padded dlogits rows, from one read of the
+    // logits
+    TRY(launch_cross_entropy(t->logits, N, V, t->tgt, t->row_loss, t->loss, 0, t->err, s, t->dlog,
+                             t->Vp));
     float lv = 0.f;
     int e = 0;
     TRY(hipMemcpyAsync(&lv, t->loss, sizeof(float), hipMemcpyDeviceToHost, s));
@@ -388,9 +393,9 @@ int cngpt_hip_train_backward(cngpt_hip_train* t) {
     hipStream_t s = v.stream;
     const size_t xbytes = (size_t)N * C * sizeof(float);
 
-    // dlogits = (probs - onehot) / (B T) (model.c:660-666), then the tied
-    // lm_head: d ln_f = dlogits . wte, d wte += dlogits^T . ln_f_out
-    TRY(launch_ce_bwd(t->logits, V, t->tgt, 1.0f / (float)N, t->dlog, t->Vp, N, s));
+    // dlogits = (probs - onehot) / (B T) (model.c:660-666) was formed by the
+    // forward's loss pass; the tied lm_head: d ln_f = dlogits . wte,
+    // d wte += dlogits^T . ln_f_out
     TRY(launch_transpose(v.wte, C, V, C, t->tW, t->Vp, (int)t->Vp, C, s));
     if (gemm(t, s, t->dlog, t->tW, nullptr, t->d_ln, N, C, t->Vp, EPI_STORE)) return -1;
     if (linear_dw(t, s, t->dlog, t->Vp, t->lnf_out, grad_of(t, v, v.wte), nullptr, V, C))
