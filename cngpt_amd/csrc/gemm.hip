@@ -834,15 +834,22 @@ double round_fill(int tiles, int res) {
 //
 // Launches of fewer than 384 tiles (M up to ~2048 rows: short prefills, the
 // reference's own B=1 T=128 shape, one GPU's share of a batch) split K over
-// the 2 x 256 workgroup slots of the BK = 32 variant: KS splits of at least
-// two K steps each, tiles * KS <= 512 so that they run in one round, and the
-// partials within a.part_cap; then reduce_splits.
+// the workgroup slots of the BK = 32 variant: KS splits of at least two K
+// steps each, the partials within a.part_cap; then reduce_splits. One
+// workgroup per CU (tiles * KS <= 256) while that leaves each at most 8 K
+// steps, else up to the 2 x 256 slots of one round: a split workgroup's time
+// is mostly fixed cost (launch, the first operand round trip, its partial
+// store), so a second one on a CU costs about as much as the first until
+// the K steps dominate. Measured per product (+ its reduce) at M = 128:
+// fc 24.2 -> 19.0 us, proj 25.6 -> 20.5 us; at M = 256 QKV 27.9 -> 22.6 us.
 // Returns the splits, *KR the k per split (whole K steps).
 int tile_splits(const GemmArgs& a, int tiles, int* KR) {
     const int cus = 256;
     *KR = a.K;
     if (!a.part || a.K % 32 || tiles >= 384) return 1;
-    int ks = std::min(a.K / 64, (2 * cus) / tiles);
+    const int nsteps = a.K / 32;
+    int ks = std::min(a.K / 64, cus / tiles);
+    if (ks <= 1 || (nsteps + ks - 1) / ks > 8) ks = std::min(a.K / 64, (2 * cus) / tiles);
     while (ks > 1 && (long)ks * a.M * a.N > a.part_cap) ks--;
     if (ks <= 1) return 1;
     *KR = (a.K / 32 + ks - 1) / ks * 32;
