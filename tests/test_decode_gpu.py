@@ -158,6 +158,28 @@ def test_decode_layernorm_formed_by_the_residual_products(C, H, B):
     compare(np.stack(logits, 1), ref, what=f"C={C} B={B} decode")
 
 
+@pytest.mark.parametrize("C,H,B", [(256, 4, 5), (256, 8, 20), (256, 2, 3), (384, 6, 33)])
+def test_decode_split_products_widths(C, H, B):
+    """Batched decode over widths whose products split K two or three ways
+    (the in-order reduce of each split product writes row t of the cache,
+    which every later step reads back), 3 to 33 sequences (one and two
+    16-row blocks of the few-row products, then three), head sizes 64, 32
+    and 128."""
+    cfg = cngpt_amd.Config(2, H, C, 300, 48)
+    params = randomize(cfg, cngpt_amd.init_weights(cfg, 31), 32)
+    prompt = np.random.default_rng(17).integers(0, cfg.vocab_size, size=(B, 9), dtype=np.int32)
+    with cngpt_amd.Model(cfg, params) as m:
+        logits = [m.decode_begin(prompt, capacity=40)]
+        toks = [logits[0].argmax(-1).astype(np.int32)]
+        for _ in range(20):
+            logits.append(m.decode_step(toks[-1]))
+            toks.append(logits[-1].argmax(-1).astype(np.int32))
+    seq = np.concatenate([prompt, np.stack(toks[:-1], 1)], axis=1)
+    ref = oracle.forward(ocfg(cfg), params, seq, oracle.ALL)[:, 8:]
+    say(f"decode C={C} H={H} B={B}")
+    compare(np.stack(logits, 1), ref, what=f"C={C} H={H} B={B} decode")
+
+
 SAMPLE_CASES = [(0.8, 40), (1.0, 40), (0.0, 40), (1.0, 1), (1.3, 0), (0.7, 50257),
                 (1.0, 5000)]
 
