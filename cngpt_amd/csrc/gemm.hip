@@ -832,27 +832,46 @@ double round_fill(int tiles, int res) {
 // per CU, whose longer K steps hold up best when a round is left
 // part-empty.
 //
-// Launches of fewer than 384 tiles (M up to ~2048 rows: short prefills, the
-// reference's own B=1 T=128 shape, one GPU's share of a batch) split K over
-// the workgroup slots of the BK = 32 variant: KS splits of at least two K
-// steps each, the partials within a.part_cap; then reduce_splits. One
-// workgroup per CU (tiles * KS <= 256) while that leaves each at most 8 K
-// steps, else up to the 2 x 256 slots of one round: a split workgroup's time
-// is mostly fixed cost (launch, the first operand round trip, its partial
-// store), so a second one on a CU costs about as much as the first until
-// the K steps dominate. Measured per product (+ its reduce) at M = 128:
-// fc 24.2 -> 19.0 us, proj 25.6 -> 20.5 us; at M = 256 QKV 27.9 -> 22.6 us.
-// Returns the splits, *KR the k per split (whole K steps).
+// Launches of at most 256 tiles (M up to ~2048 rows: short prefills, the
+// reference's own B=1 T=128 shape, one GPU's share of a batch, the
+// training step's N = 768 products at B=4 T=1024) split K over workgroups
+// of the BK = 32 variant when that is cheaper by a measured cost model:
+//   ceil(steps / KS) * (w == 1 ? 2.1 : 1.83 w) us, w = ceil(tiles * KS /
+//   256) workgroups on the busiest CU (a 128 x 128 x 32 step takes ~2.1 us
+//   alone on a CU, ~1.83 us each when workgroups share it and hide each
+//   other's memory waits)
+// + 0.3 us per MB of partials (KS * M * N floats written and summed),
+// over KS from 1 (whole tiles) to K / 64 (at least two K steps per split),
+// the partials within a.part_cap; then reduce_splits. Fitted to per-product
+// timings (+ reduce) of GPT-2 small's products at M = 128 .. 4096, where it
+// picks the measured best or one within 4 % of it: e.g. proj at M = 4096
+// (192 tiles) 4 splits, 203 -> 164 us; fc at M = 128 8 splits, 24.2 ->
+// 19.0 us. More tiles take stream-K or whole tiles. Returns the splits, *KR
+// the k per split (whole K steps).
 int tile_splits(const GemmArgs& a, int tiles, int* KR) {
     const int cus = 256;
     *KR = a.K;
-    if (!a.part || a.K % 32 || tiles >= 384) return 1;
+    if (!a.part || a.K % 32 || tiles > cus) return 1;
     const int nsteps = a.K / 32;
-    int ks = std::min(a.K / 64, cus / tiles);
-    if (ks <= 1 || (nsteps + ks - 1) / ks > 8) ks = std::min(a.K / 64, (2 * cus) / tiles);
-    while (ks > 1 && (long)ks * a.M * a.N > a.part_cap) ks--;
-    if (ks <= 1) return 1;
-    *KR = (a.K / 32 + ks - 1) / ks * 32;
+    const double mb_per_split = 4e-6 * a.M * a.N;
+    auto per_step = [&](int wgs) {
+        const int w = (wgs + cus - 1) / cus;
+        return w == 1 ? 2.1 : 1.83 * w;
+    };
+    int best = 1;
+    double best_cost = nsteps * per_step(tiles);
+    for (int ks = 2; ks <= a.K / 64; ks++) {
+        if ((long)ks * a.M * a.N > a.part_cap) break;
+        const int steps = (nsteps + ks - 1) / ks;
+        const int kse = (nsteps + steps - 1) / steps;  // splits of `steps` each
+        const double cost = steps * per_step(tiles * kse) + 0.3 * mb_per_split * kse;
+        if (cost < best_cost) {
+            best_cost = cost;
+            best = kse;
+        }
+    }
+    if (best <= 1) return 1;
+    *KR = (nsteps + best - 1) / best * 32;
     return (a.K + *KR - 1) / *KR;
 }
 
@@ -863,7 +882,16 @@ int tile_splits(const GemmArgs& a, int tiles, int* KR) {
 int sk_workgroups(const GemmArgs& a, int tiles) {
     const int cus = 256, G = 2 * cus;
     if (!a.part || a.K % 32 || tiles <= cus) return 0;
-    if (tiles > G && tiles <= 2 * G) return 0;  // one round of the BK = 16 variant
+    if (tiles > G && tiles <= 2 * G) {
+        // one round of the BK = 16 variant at 4 per CU, while it gives the
+        // CUs about equal numbers of tiles (768: 3 each); otherwise one
+        // stream-K workgroup per CU (M = 4096 QKV, 576 tiles: 155.6 us
+        // in one round of 2 or 3 tiles per CU, 132.0 us stream-K)
+        const int per_cu = (tiles + cus - 1) / cus;
+        if ((double)tiles / ((double)per_cu * cus) >= 0.9) return 0;
+        if (2L * cus * BM * BN > a.part_cap) return 0;
+        return cus;
+    }
     const int rounds = (tiles + G - 1) / G;
     if ((double)tiles / ((double)rounds * G) >= 0.9) return 0;
     if (2L * G * BM * BN > a.part_cap || (long)tiles * (a.K / 32) < G) return 0;
