@@ -198,7 +198,8 @@ __global__ void __launch_bounds__(256, 2)
 }
 
 // k_attn_ks: the same product for launches with too few (sequence, head,
-// 128-query) blocks to occupy the CUs (one sequence of up to ~2500 tokens).
+// 128-query) blocks to occupy the CUs evenly (fewer than 512: one sequence
+// of up to ~5000 tokens, B=4 T=1024).
 // There a block's latency is its last wavefront's chain of matrix-core
 // steps over every key up to the diagonal, so a workgroup takes 32 queries
 // and its four wavefronts split the keys: wavefront w takes the 32-key
@@ -356,7 +357,10 @@ hipError_t causal_hs(const float* qkv, long seq_stride, float* out, int B, int T
     const float scale = 1.0f / sqrtf((float)HS);
     // (the key split holds a 32-key block of K and V per lane: up to HS = 64)
     if constexpr (HS <= 64) {
-        if ((long)nqb * B * H < 256) {
+        // fewer than two 128-query blocks per CU: measured per forward of
+        // 12 layers, B=4 T=1024 (384 blocks) 1.207 -> 1.057 ms with the
+        // key split, B=8 T=1024 (768 blocks) 1.609 -> 1.973 ms
+        if ((long)nqb * B * H < 512) {
             const int nqb32 = (T + 31) / 32;
             k_attn_ks<HS><<<nqb32 * B * H, 256, 0, s>>>(qkv, seq_stride, out, B, T, C, H, nqb32,
                                                          scale, lse);

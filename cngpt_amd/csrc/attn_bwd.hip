@@ -24,7 +24,17 @@
 // to the diagonal with K and V staged in LDS, forms S^T = K Q^T and dP^T =
 // V dO^T with a lane per query, and dQ^T += K^T dS^T with dS^T as the B
 // operand from the accumulator. Both kernels write whole columns of the
-// qkv gradient (dQ, dK, dV of their head), so it needs no clearing.
+// qkv gradient (dQ, dK, dV of their head).
+//
+// Causal walks differ in length (a key block near the start meets every
+// query block after it, one near the end only its own), so with few blocks
+// per CU the longest walks set the time: at B=4 T=1024, 384 workgroups of
+// 4 to 32 block pairs, the busiest CUs held 44 block pairs against an
+// average of 27. With fewer than 1024 walks each walk is split in two
+// halves (split = 2), twice the workgroups, longest first; both halves add
+// their part into the gradient, zeroed first. Two additions onto zero give
+// the same bits in either order (x + y = y + x), so the result stays
+// reproducible.
 #include "common.h"
 #include "kernels.h"
 
@@ -61,18 +71,34 @@ struct BwdShape {
     static constexpr int LIT = (32 * F4 + 255) / 256;  // float4 per thread to stage 32 rows
 };
 
+// Zero n float4 (the gradient the split walks add into).
+__global__ void __launch_bounds__(256) k_zero4(f32x4* __restrict__ p, long n) {
+    const long i = (long)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) p[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+}
+
+// The [lo, hi) range of a walk of n blocks that half `part` of `split`
+// covers (the first half takes the extra block).
+__device__ __forceinline__ void walk_part(int n, int split, int part, int& lo, int& hi) {
+    const int mid = split == 2 ? (n + 1) / 2 : n;
+    lo = part == 0 ? 0 : mid;
+    hi = part == 0 ? mid : n;
+}
+
 template <int HS, int OCC>
 __global__ void __launch_bounds__(256, OCC)
     k_attn_bwd_kv(const float* __restrict__ qkv, const float* __restrict__ dout,
                   const float* __restrict__ lse, const float* __restrict__ Dv,
-                  float* __restrict__ dqkv, int B, int T, int C, int H, int nkb, float scale) {
+                  float* __restrict__ dqkv, int B, int T, int C, int H, int nkb, float scale,
+                  int split) {
     using S_ = BwdShape<HS>;
     constexpr int HALF = S_::HALF, ROW = S_::ROW, NDB = S_::NDB, F4 = S_::F4, LIT = S_::LIT;
     __shared__ float Qs[2][32 * ROW], Os[2][32 * ROW];
     __shared__ float Ls[2][32], Ds[2][32];
 
     const int BH = B * H;
-    const int kb = (int)(blockIdx.x / BH);  // key block of 128: the longest walks first
+    const int w = (int)(blockIdx.x / BH);  // walk part: the longest walks first
+    const int kb = w / split;              // key block of 128
     const int bh = blockIdx.x % BH;
     const int b = bh / H, h = bh % H;
     const long C3 = 3L * C;
@@ -137,15 +163,20 @@ __global__ void __launch_bounds__(256, OCC)
         for (int r = 0; r < 16; r++) dk[j][r] = dv[j][r] = 0.f;
 
     const int nqb = (T + 31) / 32;
-    const int qb0 = kb * 4;  // the first query block that meets this workgroup's keys
-    if (qb0 < nqb) {
+    // query blocks from the first that meets this workgroup's keys, or this
+    // part of them
+    int qb0, qb1;
+    walk_part(max(nqb - kb * 4, 0), split, w % split, qb0, qb1);
+    qb0 += kb * 4;
+    qb1 += kb * 4;
+    if (qb0 < qb1) {
         gload(qb0);
         lstore(0);
     }
     __syncthreads();
-    for (int qb = qb0; qb < nqb; qb++) {
+    for (int qb = qb0; qb < qb1; qb++) {
         const int cur = (qb - qb0) & 1;
-        if (qb + 1 < nqb) gload(qb + 1);
+        if (qb + 1 < qb1) gload(qb + 1);
         // wave-uniform: the block holds a query at or after this wavefront's first key
         if (key0 < T && qb * 32 + 31 >= key0) {
             const float* qs = Qs[cur];
@@ -190,7 +221,7 @@ __global__ void __launch_bounds__(256, OCC)
                 }
             }
         }
-        if (qb + 1 < nqb) lstore(cur ^ 1);
+        if (qb + 1 < qb1) lstore(cur ^ 1);
         __syncthreads();
     }
 
@@ -204,8 +235,13 @@ __global__ void __launch_bounds__(256, OCC)
         for (int j = 0; j < NDB; j++) {
             const int dd = 32 * j + lr;
             if (HS >= 32 || dd < HS) {
-                row[C + dd] = dk[j][r] * scale;
-                row[2 * C + dd] = dv[j][r];
+                if (split == 1) {
+                    row[C + dd] = dk[j][r] * scale;
+                    row[2 * C + dd] = dv[j][r];
+                } else {
+                    unsafeAtomicAdd(row + C + dd, dk[j][r] * scale);
+                    unsafeAtomicAdd(row + 2 * C + dd, dv[j][r]);
+                }
             }
         }
     }
@@ -215,13 +251,19 @@ template <int HS, int OCC>
 __global__ void __launch_bounds__(256, OCC)
     k_attn_bwd_q(const float* __restrict__ qkv, const float* __restrict__ dout,
                  const float* __restrict__ lse, const float* __restrict__ Dv,
-                 float* __restrict__ dqkv, int B, int T, int C, int H, int nqb, float scale) {
+                 float* __restrict__ dqkv, int B, int T, int C, int H, int nqb, float scale,
+                 int split) {
     using S_ = BwdShape<HS>;
     constexpr int HALF = S_::HALF, ROW = S_::ROW, NDB = S_::NDB, F4 = S_::F4, LIT = S_::LIT;
-    __shared__ float Ks[2][32 * ROW], Vs[2][32 * ROW];
+    // K and V stages; after the walk, each wavefront's dQ rows (32 x HS + 1)
+    __shared__ float kvs[4 * 32 * ROW];
+    float (*Ks)[32 * ROW] = (float (*)[32 * ROW])kvs;
+    float (*Vs)[32 * ROW] = (float (*)[32 * ROW])(kvs + 2 * 32 * ROW);
+    static_assert(4 * 32 * (HS + 1) <= 4 * 32 * ROW, "dQ rows fit the stages");
 
     const int BH = B * H;
-    const int qbk = nqb - 1 - (int)(blockIdx.x / BH);  // query block of 128, longest first
+    const int w = (int)(blockIdx.x / BH);  // walk part: the longest walks first
+    const int qbk = nqb - 1 - w / split;   // query block of 128
     const int bh = blockIdx.x % BH;
     const int b = bh / H, h = bh % H;
     const long C3 = 3L * C;
@@ -280,13 +322,17 @@ __global__ void __launch_bounds__(256, OCC)
 #pragma unroll
         for (int r = 0; r < 16; r++) dqa[j][r] = 0.f;
 
-    const int nkb = min(qbk * 128 + 127, T - 1) / 32 + 1;  // key blocks up to the diagonal
-    gload(0);
-    lstore(0);
+    // key blocks up to the diagonal, or this part of them
+    int kb0, kb1;
+    walk_part(min(qbk * 128 + 127, T - 1) / 32 + 1, split, w % split, kb0, kb1);
+    if (kb0 < kb1) {
+        gload(kb0);
+        lstore(0);
+    }
     __syncthreads();
-    for (int kb = 0; kb < nkb; kb++) {
-        const int cur = kb & 1;
-        if (kb + 1 < nkb) gload(kb + 1);
+    for (int kb = kb0; kb < kb1; kb++) {
+        const int cur = (kb - kb0) & 1;
+        if (kb + 1 < kb1) gload(kb + 1);
         if (q0 < T && kb * 32 <= q0 + 31) {
             const float* ks = Ks[cur];
             const float* vs = Vs[cur];
@@ -325,23 +371,44 @@ __global__ void __launch_bounds__(256, OCC)
                 }
             }
         }
-        if (kb + 1 < nkb) lstore(cur ^ 1);
+        if (kb + 1 < kb1) lstore(cur ^ 1);
         __syncthreads();
     }
 
     // dqa[j][r]: d = 32 j + 8 (r/4) + 4 lh + r%4, query qi
-    if (qi < T) {
-        float* row = dqkv + ((long)b * T + qi) * C3 + h * HS;
+    if (split == 1) {
+        if (qi < T) {
+            float* row = dqkv + ((long)b * T + qi) * C3 + h * HS;
 #pragma unroll
-        for (int j = 0; j < NDB; j++)
+            for (int j = 0; j < NDB; j++)
 #pragma unroll
-            for (int g = 0; g < 4; g++) {
-                const int dd = 32 * j + 8 * g + 4 * lh;
-                if (dd < HS)
-                    *(f32x4*)(row + dd) = f32x4{dqa[j][4 * g] * scale, dqa[j][4 * g + 1] * scale,
-                                                dqa[j][4 * g + 2] * scale, dqa[j][4 * g + 3] * scale};
-            }
+                for (int g = 0; g < 4; g++) {
+                    const int dd = 32 * j + 8 * g + 4 * lh;
+                    if (dd < HS)
+                        *(f32x4*)(row + dd) =
+                            f32x4{dqa[j][4 * g] * scale, dqa[j][4 * g + 1] * scale,
+                                  dqa[j][4 * g + 2] * scale, dqa[j][4 * g + 3] * scale};
+                }
+        }
+        return;
     }
+    // A half walk adds its part. A lane holds one query's d values, so the
+    // rows go through LDS first (the stages are free after the walk's last
+    // barrier): each addition instruction then covers one row's contiguous
+    // d instead of 64 rows.
+    constexpr int P = HS + 1;
+    float* tq = kvs + wave * 32 * P;
+#pragma unroll
+    for (int j = 0; j < NDB; j++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int dd = 32 * j + 8 * (r >> 2) + 4 * lh + (r & 3);
+            if (dd < HS) tq[lr * P + dd] = dqa[j][r] * scale;
+        }
+    __builtin_amdgcn_wave_barrier();
+    for (int d = lane; d < HS; d += 64)
+        for (int q = 0; q < 32 && q0 + q < T; q++)
+            unsafeAtomicAdd(dqkv + ((long)b * T + q0 + q) * C3 + h * HS + d, tq[q * P + d]);
 }
 
 template <int HS, int OCC>
@@ -353,12 +420,20 @@ hipError_t bwd_hs(const float* qkv, const float* out, const float* dout, const f
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int nb = (T + 127) / 128;
-    k_attn_bwd_kv<HS, OCC><<<nb * B * H, 256, 0, s>>>(qkv, dout, lse, D, dqkv, B, T, C, H, nb,
-                                                      scale);
+    const int split = (long)nb * B * H < 1024 ? 2 : 1;
+    if (split == 2) {
+        // the halves add into the gradient rows of every (sequence, position)
+        const long n4 = (long)B * T * 3 * C / 4;
+        k_zero4<<<(unsigned)((n4 + 255) / 256), 256, 0, s>>>((f32x4*)dqkv, n4);
+        e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    k_attn_bwd_kv<HS, OCC><<<split * nb * B * H, 256, 0, s>>>(qkv, dout, lse, D, dqkv, B, T, C,
+                                                              H, nb, scale, split);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
-    k_attn_bwd_q<HS, OCC><<<nb * B * H, 256, 0, s>>>(qkv, dout, lse, D, dqkv, B, T, C, H, nb,
-                                                     scale);
+    k_attn_bwd_q<HS, OCC><<<split * nb * B * H, 256, 0, s>>>(qkv, dout, lse, D, dqkv, B, T, C, H,
+                                                             nb, scale, split);
     return hipGetLastError();
 }
 
