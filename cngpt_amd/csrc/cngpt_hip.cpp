@@ -152,7 +152,8 @@ struct cngpt_hip_ctx {
     // CNGPT_HIP_PERSIST=0 in the environment at create time selects _KERNELS)
     int decode_path = CNGPT_DECODE_AUTO;
     int last_path = 0;           // path of the last decode step
-    int persist_G = -1;          // workgroups of the persistent launch (-1: not queried)
+    int persist_G = -1;          // workgroups of the persistent launch (-1: not queried,
+                                 // 0: unavailable, e.g. a refused cooperative launch)
 
     // the decode step as a replayable graph (kernels only); CNGPT_HIP_GRAPH=0
     // in the environment at create time selects direct launches instead
@@ -363,8 +364,18 @@ int run_attn_row_proj(cngpt_hip_ctx* h, const float* qkv, long seq_stride, int B
     a.q_pos = q_pos; a.pos_dev = pos_dev;
     a.scale = 1.0f / sqrtf((float)hs);
     a.part = h->attn_part; a.max_splits = h->attn_splits;
+    const double keys = pos_dev ? 0.5 * max_keys : q_pos + 1.0;
+    if (B > SKINNY && attention_dec_one_pass(B, c.n_head)) {
+        // many (sequence, head) pairs: one pass, rows straight to c_proj's input
+        {
+            Timed t(h, CNGPT_K_ATTN_ROW, 4.0 * C * keys * B,
+                    4.0 * ((double)B * keys * 2 * C + (double)B * C));
+            HIP_TRY(launch_attention_dec_rows(a, B, h->aoutc, C, h->stream));
+        }
+        return run_gemm(h, h->aoutc, w.proj_w, w.proj_b, xres, B, C, C, EPI_RESID, 0, 0, -1, 0,
+                        nullptr, lnw, lnb, lnout);
+    }
     {
-        const double keys = pos_dev ? 0.5 * max_keys : q_pos + 1.0;
         Timed t(h, CNGPT_K_ATTN_ROW, 4.0 * C * keys * B,
                 4.0 * ((double)B * keys * 2 * C + (double)B * C));
         HIP_TRY(launch_attention_dec(a, B, max_keys, h->stream));
@@ -707,6 +718,12 @@ int persist_refused(cngpt_hip_ctx* h) {
                 "cache capacity", h->kvB);
 }
 
+// run_persist's result when the cooperative launch itself was refused (no
+// step ran, nothing changed on the device): another process on the GPU can
+// hold what a cooperative launch needs. The handle then takes the
+// kernel-per-stage path for the rest of its life.
+constexpr int PERSIST_REFUSED = 1;
+
 // n greedy decode steps of the single cached sequence as one launch.
 // n persistent steps; with top_k > 0 each step samples its token with
 // draws[step] inside the launch. *done (when set) receives the steps that
@@ -745,7 +762,14 @@ int run_persist(cngpt_hip_ctx* h, int n, float temp = 0.f, int top_k = 0,
     }
     {
         Timed tm(h, CNGPT_K_STEP, flops, bytes);
-        HIP_TRY(launch_decode_persist(a, h->persist_G, h->stream));
+        const hipError_t e = launch_decode_persist(a, h->persist_G, h->stream);
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            h->persist_G = 0;
+            if (h->decode_path == CNGPT_DECODE_PERSISTENT)
+                return fail("persistent decode launch refused: %s", hipGetErrorString(e));
+            return PERSIST_REFUSED;
+        }
     }
     if (done) {
         HIP_TRY(hipMemcpyAsync(done, h->dev_err + 2, sizeof(int), hipMemcpyDeviceToHost,
@@ -1387,9 +1411,14 @@ int cngpt_hip_decode_step(cngpt_hip_ctx* h, const int* tokens, float* logits_out
         // the caller's buffer may be reused as soon as this returns
         HIP_TRY(hipStreamSynchronize(h->stream));
     }
-    const bool persist = persist_usable(h);
+    bool persist = persist_usable(h);
     if (!persist && h->decode_path == CNGPT_DECODE_PERSISTENT) return persist_refused(h);
-    if (persist ? run_persist(h, 1) : run_decode_step(h)) return -1;
+    if (persist) {
+        const int rc = run_persist(h, 1);
+        if (rc < 0) return -1;
+        persist = rc == 0;
+    }
+    if (!persist && run_decode_step(h)) return -1;
     if (logits_out) {
         HIP_TRY(hipMemcpyAsync(logits_out, h->logits, (size_t)B * h->cfg.vocab_size * sizeof(float),
                                hipMemcpyDeviceToHost, h->stream));
@@ -1416,17 +1445,27 @@ int cngpt_hip_generate(cngpt_hip_ctx* h, int n_new, float temperature, int top_k
     if (draws && run_sample(h, h->draws, temperature, top_k)) return -1;
     const bool persist = persist_usable(h);
     if (!persist && h->decode_path == CNGPT_DECODE_PERSISTENT) return persist_refused(h);
+    // i: tokens of this call already in next_tok / the history (the first
+    // comes from decode_begin or the previous step); a refused persistent
+    // launch leaves i where it was and the step kernels take the rest
+    int i = 1;
     if (persist && !draws) {
         // greedy: every step in one launch, the argmax fed back on the device
-        if (n_new > 1 && run_persist(h, n_new - 1)) return -1;
+        if (n_new > 1) {
+            const int rc = run_persist(h, n_new - 1);
+            if (rc < 0) return -1;
+            if (rc == 0) i = n_new;
+        }
     } else if (persist && persist_sampling_supported(h->cfg.vocab_size, h->persist_G, top_k)) {
         // sampled inside the launch: step i draws token i with draws[i];
         // a step whose candidates overflow ends the launch, and its token
         // is drawn here before the next launch continues
-        for (int i = 1; i < n_new;) {
+        while (i < n_new) {
             int done = 0;
-            if (run_persist(h, n_new - i, temperature, top_k, h->draws + (size_t)i * B, &done))
-                return -1;
+            const int rc =
+                run_persist(h, n_new - i, temperature, top_k, h->draws + (size_t)i * B, &done);
+            if (rc < 0) return -1;
+            if (rc > 0) break;
             i += done;
             int next = 0;
             HIP_TRY(hipMemcpyAsync(&next, h->next_tok, sizeof(int), hipMemcpyDeviceToHost,
@@ -1438,15 +1477,16 @@ int cngpt_hip_generate(cngpt_hip_ctx* h, int n_new, float temperature, int top_k
     } else if (persist) {
         // sampled: one persistent step per launch, then the sampler replaces
         // the step's argmax by the sampled token the next launch embeds
-        for (int i = 1; i < n_new; i++) {
-            if (run_persist(h, 1)) return -1;
+        for (; i < n_new; i++) {
+            const int rc = run_persist(h, 1);
+            if (rc < 0) return -1;
+            if (rc > 0) break;
             if (run_sample(h, h->draws + (size_t)i * B, temperature, top_k)) return -1;
         }
-    } else {
-        for (int i = 1; i < n_new; i++) {
-            if (run_decode_step(h)) return -1;
-            if (draws && run_sample(h, h->draws + (size_t)i * B, temperature, top_k)) return -1;
-        }
+    }
+    for (; i < n_new; i++) {
+        if (run_decode_step(h)) return -1;
+        if (draws && run_sample(h, h->draws + (size_t)i * B, temperature, top_k)) return -1;
     }
     // tokens fed at positions start.. are the first n_new - 1; the last is in next_tok
     if (n_new > 1)

@@ -136,6 +136,12 @@ struct AttnDecArgs {
 int attn_dec_keys_per_split(int hs);
 // max_keys bounds t + 1 over every launch of a captured graph (sizes the grid).
 hipError_t launch_attention_dec(const AttnDecArgs& a, int B, int max_keys, hipStream_t s);
+// With many (sequence, head) pairs (attention_dec_one_pass): the same
+// attention in one launch with no partials, normalised rows [B, C] (row
+// stride ldo, a multiple of 4) straight to out.
+bool attention_dec_one_pass(int B, int H);
+hipError_t launch_attention_dec_rows(const AttnDecArgs& a, int B, float* out, long ldo,
+                                     hipStream_t s);
 // Merged attention rows [B, C] (row stride ldo) from the partials.
 hipError_t launch_attention_merge(const MergeArgs& g, int B, float* out, long ldo, hipStream_t s);
 // out[r] = argmax of logits row r (first index on ties); then *pos_inc += 1.
