@@ -158,13 +158,16 @@ def test_decode_layernorm_formed_by_the_residual_products(C, H, B):
     compare(np.stack(logits, 1), ref, what=f"C={C} B={B} decode")
 
 
-@pytest.mark.parametrize("C,H,B", [(256, 4, 5), (256, 8, 20), (256, 2, 3), (384, 6, 33)])
+@pytest.mark.parametrize("C,H,B", [(256, 4, 5), (256, 8, 20), (256, 2, 3), (384, 6, 33),
+                                   (256, 2, 64), (128, 16, 8), (256, 16, 24)])
 def test_decode_split_products_widths(C, H, B):
     """Batched decode over widths whose products split K two or three ways
     (the in-order reduce of each split product writes row t of the cache,
-    which every later step reads back), 3 to 33 sequences (one and two
-    16-row blocks of the few-row products, then three), head sizes 64, 32
-    and 128."""
+    which every later step reads back), 3 to 64 sequences (one to four
+    16-row blocks of the few-row products), head sizes 8 to 128; with at
+    least 128 (sequence, head) pairs the attention runs in one pass (16
+    wavefronts per pair, 8 from 384 pairs), below that split by keys and
+    merged."""
     cfg = cngpt_amd.Config(2, H, C, 300, 48)
     params = randomize(cfg, cngpt_amd.init_weights(cfg, 31), 32)
     prompt = np.random.default_rng(17).integers(0, cfg.vocab_size, size=(B, 9), dtype=np.int32)

@@ -85,6 +85,27 @@ def test_forward_backward_vs_oracle(name):
     ref.close()
 
 
+def test_attention_backward_whole_walks():
+    """With at least 1024 causal walks (here 8 x 32 heads x 4 key blocks of
+    128) the attention backward keeps each walk in one workgroup and stores
+    the gradient; below that (every other case here) the walks are split in
+    halves that add into a zeroed gradient."""
+    cfg, B, T = cngpt_amd.Config(1, 32, 256, 97, 512), 8, 512
+    params = randomize(cfg, cngpt_amd.init_weights(cfg, 71), 72)
+    tok, tgt = batch(cfg, B, T, 73)
+    ref = oracle.Trainer(ocfg(cfg), params, B, T)
+    ref.zero_grad()
+    ref_loss = ref.forward(tok, tgt)
+    ref.backward()
+    with cngpt_amd.Model(cfg, params) as m, cngpt_amd.Trainer(m, B, T) as tr:
+        loss = tr.forward(tok, tgt)
+        tr.backward()
+        grads = tr.grads
+    assert abs(loss - ref_loss) <= 1e-5 * abs(ref_loss)
+    compare_grads(cfg, grads, ref.grads, what="whole walks (hs 8)")
+    ref.close()
+
+
 def test_gpt2_small_full_depth_step():
     """GPT-2 small at full depth and width (the bench's training model),
     B=2 T=128, seeded weights with LayerNorm gains and biases randomised:
