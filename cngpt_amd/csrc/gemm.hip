@@ -899,16 +899,20 @@ int sk_workgroups(const GemmArgs& a, int tiles) {
     return tiles < G ? cus : G;
 }
 
-// Both operands K-major (a.km == 3), the residual epilogue: whole 128 x 128
-// tiles, or K split over the CUs when the tiles are too few (no stream-K).
+// K-major operands: both (a.km == 3, the residual epilogue of the dW
+// products) or W only (a.km == 2, the stored epilogue of the dX products,
+// W the weight matrix as stored: row k = output k of the forward product):
+// whole 128 x 128 tiles, or K split over the CUs when the tiles are too few
+// (no stream-K).
+template <int EPI, int KM>
 hipError_t gemm_km(const GemmArgs& a, hipStream_t s) {
     const int tiles_m = (a.M + BM - 1) / BM, tiles_n = (a.N + BN - 1) / BN;
     const int tiles = tiles_m * tiles_n;
     int KR;
     const int KS = tile_splits(a, tiles, &KR);
-    k_gemm_dl<EPI_RESID, 32, 2, 2, 3><<<tiles * KS, NTHREADS, 0, s>>>(a, tiles_m, tiles_n, KS > 1 ? KR : a.K, KS);
+    k_gemm_dl<EPI, 32, 2, 2, KM><<<tiles * KS, NTHREADS, 0, s>>>(a, tiles_m, tiles_n, KS > 1 ? KR : a.K, KS);
     const hipError_t e = hipGetLastError();
-    return e != hipSuccess || KS == 1 ? e : reduce_splits<EPI_RESID>(a, KS, s);
+    return e != hipSuccess || KS == 1 ? e : reduce_splits<EPI>(a, KS, s);
 }
 
 template <int EPI>
@@ -963,14 +967,16 @@ hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
                      (a.ldy & 3) || a.N > 2048 || !a.ln_w || !a.ln_b))
         return hipErrorInvalidValue;
     if (a.km) {
-        // K-major operands: the residual (accumulating) epilogue of the dW
-        // products, plain row-major output, K whole steps, rows of whole
+        // K-major operands: both with the residual (accumulating) epilogue
+        // of the dW products, or W only with the stored epilogue of the dX
+        // products; plain row-major output, K whole steps, rows of whole
         // granules (ld a multiple of 4 covering the tile's rows rounded to 4)
-        if (a.km != 3 || a.epi != EPI_RESID || a.M <= SKINNY_MAX_M || a.K % 32 || a.seg ||
-            a.row_off || a.row_off_dev || a.ln_out || (a.ldx & 3) || (a.ldw & 3) ||
-            a.ldx < ((a.M + 3) & ~3) || a.ldw < ((a.N + 3) & ~3))
+        const bool both = a.km == 3 && a.epi == EPI_RESID, w_only = a.km == 2 && a.epi == EPI_STORE;
+        if ((!both && !w_only) || a.M <= SKINNY_MAX_M || a.K % 32 || a.seg || a.row_off ||
+            a.row_off_dev || a.ln_out || (a.ldw & 3) || a.ldw < ((a.N + 3) & ~3) ||
+            (both && ((a.ldx & 3) || a.ldx < ((a.M + 3) & ~3))))
             return hipErrorInvalidValue;
-        return gemm_km(a, s);
+        return both ? gemm_km<EPI_RESID, 3>(a, s) : gemm_km<EPI_STORE, 2>(a, s);
     }
     if (a.M <= SKINNY_MAX_M) {
         switch (a.epi) {

@@ -40,9 +40,10 @@ struct GemmArgs {
     const float* ln_w;
     const float* ln_b;
     float* ln_out;
-    // Optional K-major operands (km = 3: both; the residual epilogue, M >
-    // SKINNY_MAX_M, K a multiple of 32): X is [K][ldx] (row k holds the M
-    // rows' k-th values), W is [K][ldw]; ldx and ldw multiples of 4, at
+    // Optional K-major operands (M > SKINNY_MAX_M, K a multiple of 32):
+    // km = 3, both, with the residual epilogue: X is [K][ldx] (row k holds
+    // the M rows' k-th values), W is [K][ldw]; km = 2, W only, with the
+    // stored epilogue (X rows of K floats). ldx and ldw multiples of 4, at
     // least M and N rounded up to 4. 0: both K-contiguous, rows of K floats.
     int km;
     long ldx, ldw;

@@ -120,9 +120,23 @@ int gemm(cngpt_hip_train* t, hipStream_t s, const float* X, const float* W, cons
     return 0;
 }
 
-// dX [rows, in] = dY [rows, out] . W [out, in] (overwrites dX).
+// dX [rows, in] = dY [rows, out] . W [out, in] (overwrites dX). Over more
+// than SKINNY_MAX_M rows with out a multiple of 32, the product reads W as
+// stored, K-major (row k = output k); otherwise through a transposed copy.
 int linear_dx(cngpt_hip_train* t, hipStream_t s, const float* dY, const float* W, float* dX,
               long out, long in) {
+    if (t->N > SKINNY_MAX_M && out % 32 == 0 && in % 4 == 0) {
+        GemmArgs a{};
+        a.X = dY; a.W = W; a.ldw = in; a.km = 2;
+        a.Y = dX;
+        a.M = (int)t->N; a.N = (int)in; a.K = (int)out;
+        a.ldy = in;
+        a.epi = EPI_STORE;
+        a.part = t->part;
+        a.part_cap = PART_FLOATS;
+        TRY(launch_gemm(a, s));
+        return 0;
+    }
     TRY(launch_transpose(W, in, (int)out, (int)in, t->tW, out, (int)out, (int)in, s));
     return gemm(t, s, dY, t->tW, nullptr, dX, t->N, in, out, EPI_STORE);
 }
