@@ -32,6 +32,7 @@
 // K split over workgroups when the column tiles are few. Products over
 // M <= 2 rows (single-sequence decode) are k_dgemv in decode.hip.
 #include <algorithm>
+#include <type_traits>
 
 #include "common.h"
 #include "kernels.h"
@@ -550,89 +551,141 @@ __global__ void __launch_bounds__(NTHREADS, OCC) k_gemm(GemmArgs a, int tiles_m,
 // M rows only (at M = 32, 2 * 32 FLOP per 4-byte weight = 16 FLOP/B, near
 // the fp32 ridge of 157.3 / 8 = 19.7), so each weight is read once and the
 // input rows are shared out of LDS. A workgroup of ST_NW wavefronts owns
-// ST_NT = 16 * ST_NW output columns over a K range [kb, ke): each wavefront
-// streams its 16 weight rows with ST_PF 16-byte loads in flight per lane
-// (k-steps of 16: lane l holds column l%16, k = 4*(l/16)..+3), while the
-// input rows of the range pass through LDS in chunks of ST_KC k, the next
-// chunk loaded into registers during the current one. Products are
-// v_mfma_f32_16x16x4f32 (16 rows x 16 columns x 4 k), MB row blocks of 16.
+// ST_NT = 16 * ST_NW output columns over a K range [kb, ke), in steps of 16
+// k: for its 16 columns a wavefront's lane l holds column l % 16, k = 4 (l /
+// 16) .. +3 of a step, and the input rows of the range pass through LDS in
+// chunks of ST_KC k. Products are v_mfma_f32_16x16x4f32 (16 rows x 16
+// columns x 4 k), MB row blocks of 16.
+//
+// Both operands go from global memory straight into LDS (lds_dma16, no
+// registers on the way), so the compiler neither waits for them nor moves
+// them: input chunk c + 1 is issued when chunk c starts (double
+// buffer, granules XOR-swizzled by row so the 16 rows a read instruction
+// touches fall in different banks), and each wavefront streams its
+// weights through a ring of ST_PF steps (1 KB each, one load instruction),
+// the load of step s + ST_PF issued right after step s's products. The
+// issue order is the same in every chunk but the last (which issues
+// nothing), so each wait is a constant count of the loads issued after the
+// one needed: the weights stay ST_PF steps in flight across chunk
+// boundaries (a register ring loses that: the compiler waits for every load
+// in flight at the top of each loop trip), and no load is in flight past
+// the range.
 // When the column tiles alone would leave CUs idle, K is split over KS
 // workgroups that write partial tiles; k_stream_reduce then sums them in
 // order and applies the epilogue (no atomics: the result is reproducible).
 constexpr int ST_NW = 4;
 constexpr int ST_NT = 16 * ST_NW;
 constexpr int ST_KC = 128;
-constexpr int ST_PF = ST_KC / 16;   // weight steps in flight = steps per chunk
-constexpr int ST_XP = ST_KC + 4;    // padded LDS row (floats)
+constexpr int ST_PF = ST_KC / 16;   // weight steps in flight = steps per chunk (<= 8)
+constexpr int ST_GPR = ST_KC / 4;   // input granules (16 bytes) per row of a chunk
 
+// 16 bytes per lane from global memory into LDS at lds + 16 * lane
+// (global_load_lds_dwordx4, lds wavefront-uniform), issued as assembly so
+// that the compiler tracks neither the load nor the LDS it writes: it would
+// otherwise wait for every such load in flight before the first LDS read
+// that it cannot prove disjoint (the first read of each input chunk). The
+// caller's explicit vmcnt waits cover them. M0 (the LDS base) is restored
+// for the compiler's own use.
+__device__ __forceinline__ void lds_dma16(const void* g, const float* lds) {
+    const unsigned la = (unsigned)(size_t)(const __attribute__((address_space(3))) float*)lds;
+    int m0s;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "global_load_lds_dwordx4 %2, off\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(m0s)
+        : "s"(la), "v"(g)
+        : "memory");
+}
 
 template <int EPI, int MB>
 __global__ void __launch_bounds__(ST_NW * 64) k_stream(GemmArgs a, int tiles_n, int KR, int KS) {
-    constexpr int R = 16 * MB;                                  // rows held (M <= R)
-    constexpr int XF4 = R * ST_KC / 4;                          // float4 per X chunk
-    constexpr int XPT = (XF4 + ST_NW * 64 - 1) / (ST_NW * 64);  // per thread
-    __shared__ float xs[2][R * ST_XP];
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    constexpr int R = 16 * MB;                       // rows held (M <= R)
+    constexpr int XI = R * ST_GPR / (ST_NW * 64);    // input load instructions per wavefront per chunk
+    static_assert(XI * ST_NW * 64 == R * ST_GPR, "whole instructions");
+    __shared__ __attribute__((aligned(1024))) float xs[2][R * ST_KC];
+    __shared__ __attribute__((aligned(1024))) float ws[ST_NW][ST_PF][256];
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int lc = lane & 15, g4 = (lane >> 4) * 4;
     const int tn = blockIdx.x % tiles_n, ks = blockIdx.x / tiles_n;
     const int K = a.K, M = a.M, N = a.N;
     const int kb = ks * KR, ke = min(K, kb + KR);
     const int nchunks = (ke - kb + ST_KC - 1) / ST_KC;
-    const int nsteps = nchunks * ST_PF;
     const int col = tn * ST_NT + 16 * wave + lc;
-    const float* wrow = a.W + (long)min(col, N - 1) * K;
+    const float* wrow = a.W + (long)min(col, N - 1) * K + g4;
 
-    // input chunk c -> registers (zero past M or ke); clamped addresses
-    auto xload = [&](f32x4 (&xr)[XPT], int c) {
+    // input chunk c into buffer b: granule g = (i * ST_NW + wave) * 64 +
+    // lane of the chunk sits at row g / ST_GPR, slot g % ST_GPR and holds k
+    // quad slot ^ (row % 16); rows past M read row M - 1 and k past K reads
+    // K - 4 (finite values whose products are discarded or multiply zeroed
+    // weights)
+    const float* xsrc[XI];
+    int xslot[XI];
 #pragma unroll
-        for (int i = 0; i < XPT; i++) {
-            const int f = tid + i * ST_NW * 64;
-            const int row = f / (ST_KC / 4), k = kb + c * ST_KC + (f % (ST_KC / 4)) * 4;
-            const bool ok = f < XF4 && row < M && k < ke;
-            const f32x4 v = *(const f32x4*)(a.X + (long)min(row, M - 1) * K + min(k, K - 4));
-            xr[i] = ok ? v : f32x4{0.f, 0.f, 0.f, 0.f};
-        }
-    };
-    auto xstore = [&](const f32x4 (&xr)[XPT], int buf) {
+    for (int i = 0; i < XI; i++) {
+        const int g = (i * ST_NW + wave) * 64 + lane;
+        const int row = g / ST_GPR, slot = g % ST_GPR;
+        xsrc[i] = a.X + (long)min(row, M - 1) * K;
+        xslot[i] = 4 * (slot ^ (row & 15));
+    }
+    auto issue_x = [&](int c, const float* xd) {
+        const int k0 = kb + c * ST_KC;
 #pragma unroll
-        for (int i = 0; i < XPT; i++) {
-            const int f = tid + i * ST_NW * 64;
-            if (f < XF4) {
-                const int row = f / (ST_KC / 4), k4 = f % (ST_KC / 4);
-                *(f32x4*)&xs[buf][row * ST_XP + k4 * 4] = xr[i];
-            }
-        }
+        for (int i = 0; i < XI; i++)
+            lds_dma16(xsrc[i] + min(k0 + xslot[i], K - 4), &xd[(i * ST_NW + wave) * 256]);
     };
-    // weight step s: this lane's column at k = kb + 16 s + g4 .. +3 (steps
-    // past the range re-read the last one; their product is masked)
-    auto wload = [&](int s) {
-        const int k = kb + 16 * min(s, nsteps - 1) + g4;
-        return *(const f32x4*)(wrow + min(k, K - 4));
+    // weight step s (k = kb + 16 s + g4 .. +3 of this lane's column; steps
+    // past the range re-read K - 4 and are zeroed at use) into ring slot
+    // s % ST_PF
+    auto issue_w = [&](int s) {
+        lds_dma16(wrow + min(kb + 16 * s, K - 4 - g4), &ws[wave][s % ST_PF][0]);
     };
 
     f32x4 acc[MB];
 #pragma unroll
     for (int mb = 0; mb < MB; mb++) acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
-    f32x4 wr[ST_PF];
-#pragma unroll
-    for (int j = 0; j < ST_PF; j++) wr[j] = wload(j);
-    f32x4 xr[XPT];
-    xload(xr, 0);
-    xstore(xr, 0);
-    __syncthreads();
-    for (int c = 0; c < nchunks; c++) {
-        if (c + 1 < nchunks) xload(xr, c + 1);
+    // chunk c (LAST: the final one, which issues no loads: nothing is left
+    // in flight past the range, so none has to be waited for at the end)
+    auto chunk = [&](int c, auto last_c) {
+        constexpr bool LAST = decltype(last_c)::value;
+        // chunk c has landed once at most the ST_PF weight loads issued
+        // after it are in flight; the barrier then also frees the other
+        // buffer (read in chunk c - 1) for chunk c + 1
+        wait_vmcnt<ST_PF>();
+        asm volatile("s_barrier" ::: "memory");
+        if (!LAST) issue_x(c + 1, xs[(c + 1) & 1]);
         const float* xb = xs[c & 1];
 #pragma unroll
         for (int j = 0; j < ST_PF; j++) {
             const int s = c * ST_PF + j;
+            // step s has landed once at most the later ring loads and the
+            // next chunk are in flight (in the last chunk: the later ring
+            // loads only)
+            if (LAST) {
+                // (j is a constant once the loop is unrolled)
+                switch (ST_PF - 1 - j) {
+                    case 0: wait_vmcnt<0>(); break;
+                    case 1: wait_vmcnt<1>(); break;
+                    case 2: wait_vmcnt<2>(); break;
+                    case 3: wait_vmcnt<3>(); break;
+                    case 4: wait_vmcnt<4>(); break;
+                    case 5: wait_vmcnt<5>(); break;
+                    case 6: wait_vmcnt<6>(); break;
+                    default: wait_vmcnt<7>(); break;
+                }
+            } else {
+                wait_vmcnt<ST_PF - 1 + XI>();
+            }
+            asm volatile("" ::: "memory");
             const bool kok = kb + 16 * s + g4 < ke;
+            const f32x4 w = *(const f32x4*)&ws[wave][j][4 * lane];
             f32x4 xf[MB];
 #pragma unroll
-            for (int mb = 0; mb < MB; mb++)
-                xf[mb] = *(const f32x4*)&xb[(16 * mb + lc) * ST_XP + 16 * j + g4];
-            const f32x4 w = wr[j];
-            wr[j] = wload(s + ST_PF);
+            for (int mb = 0; mb < MB; mb++) {
+                const int r = 16 * mb + lc, q = 4 * j + (lane >> 4);
+                xf[mb] = *(const f32x4*)&xb[r * ST_KC + 4 * (q ^ (r & 15))];
+            }
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 const float we = kok ? w[e] : 0.f;
@@ -640,11 +693,18 @@ __global__ void __launch_bounds__(ST_NW * 64) k_stream(GemmArgs a, int tiles_n, 
                 for (int mb = 0; mb < MB; mb++)
                     acc[mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(xf[mb][e], we, acc[mb], 0, 0, 0);
             }
+            if (!LAST) {
+                // the slot is refilled only after its values are in registers
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                issue_w(s + ST_PF);
+            }
         }
-        // the other buffer was last read in chunk c - 1, before the barrier
-        if (c + 1 < nchunks) xstore(xr, (c + 1) & 1);
-        __syncthreads();
-    }
+    };
+    issue_x(0, xs[0]);
+#pragma unroll
+    for (int j = 0; j < ST_PF; j++) issue_w(j);
+    for (int c = 0; c + 1 < nchunks; c++) chunk(c, std::false_type{});
+    chunk(nchunks - 1, std::true_type{});
 
     // acc[mb][r]: row 16 mb + 4 (lane / 16) + r, column col
     if (col >= N) return;

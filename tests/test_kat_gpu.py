@@ -237,7 +237,12 @@ def test_softmax_error_bound_dense_grid(kat, kind):
     (0, 130, 81, 1600, 1),    # MFMA tiles, ragged edges, K = 1600 (XL)
     (0, 200, 333, 36, 2),     # register-staged tiles (K not a multiple of 16), GELU
     (0, 257, 129, 768, 3),    # direct-to-LDS BK = 32, residual
-    (0, 128, 2304, 768, 1),   # tiles with K split 12 ways (M = 128), in-order reduce
+    (0, 128, 2304, 768, 1),   # tiles with K split (M = 128), in-order reduce
+    (0, 100, 3072, 768, 2),   # tiles with K split, ragged rows, GELU
+    (0, 128, 768, 3072, 3),   # tiles with K split, residual reduce
+    (0, 256, 771, 768, 3),    # two row tiles, ragged columns, K split
+    (0, 65, 50, 36, 1),       # register-staged tiles, K = 36, one tile
+    (0, 2048, 768, 768, 3),   # tiles with K split (M = 2048), residual reduce
     (0, 2048, 768, 3072, 3),  # tiles with K split 5 ways (M = 2048), residual reduce
     (0, 2048, 2304, 768, 1),  # stream-K: 288 tiles over 512 workgroups, fixup
     (0, 1100, 4000, 1600, 3), # stream-K: 9 x 32 ragged tiles, residual
