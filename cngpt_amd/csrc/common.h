@@ -56,6 +56,27 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (7 << 4) | (0xF << 8));
 }
 
+// 16 bytes per lane from global memory into LDS at lds + 16 * lane
+// (global_load_lds_dwordx4, lds wavefront-uniform), issued as assembly so
+// that the compiler tracks neither the load nor the LDS it writes: it would
+// otherwise wait for every such load in flight before the first LDS read
+// that it cannot prove disjoint, and a ring of such loads carried across
+// loop trips in registers would lose its prefetch to a wait for every load
+// at the top of each trip. The caller's explicit vmcnt waits cover them.
+// M0 (the LDS base) is restored for the compiler's own use.
+__device__ __forceinline__ void lds_dma16(const void* g, const float* lds) {
+    const unsigned la = (unsigned)(size_t)(const __attribute__((address_space(3))) float*)lds;
+    int m0s;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "global_load_lds_dwordx4 %2, off\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(m0s)
+        : "s"(la), "v"(g)
+        : "memory");
+}
+
 __device__ __forceinline__ float lane_f(float v, int l) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
 }

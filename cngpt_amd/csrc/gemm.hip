@@ -579,26 +579,6 @@ constexpr int ST_KC = 128;
 constexpr int ST_PF = ST_KC / 16;   // weight steps in flight = steps per chunk (<= 8)
 constexpr int ST_GPR = ST_KC / 4;   // input granules (16 bytes) per row of a chunk
 
-// 16 bytes per lane from global memory into LDS at lds + 16 * lane
-// (global_load_lds_dwordx4, lds wavefront-uniform), issued as assembly so
-// that the compiler tracks neither the load nor the LDS it writes: it would
-// otherwise wait for every such load in flight before the first LDS read
-// that it cannot prove disjoint (the first read of each input chunk). The
-// caller's explicit vmcnt waits cover them. M0 (the LDS base) is restored
-// for the compiler's own use.
-__device__ __forceinline__ void lds_dma16(const void* g, const float* lds) {
-    const unsigned la = (unsigned)(size_t)(const __attribute__((address_space(3))) float*)lds;
-    int m0s;
-    asm volatile(
-        "s_mov_b32 %0, m0\n\t"
-        "s_mov_b32 m0, %1\n\t"
-        "global_load_lds_dwordx4 %2, off\n\t"
-        "s_mov_b32 m0, %0"
-        : "=&s"(m0s)
-        : "s"(la), "v"(g)
-        : "memory");
-}
-
 template <int EPI, int MB>
 __global__ void __launch_bounds__(ST_NW * 64) k_stream(GemmArgs a, int tiles_n, int KR, int KS) {
     constexpr int R = 16 * MB;                       // rows held (M <= R)
