@@ -32,6 +32,7 @@
 // K split over workgroups when the column tiles are few. Products over
 // M <= 2 rows (single-sequence decode) are k_dgemv in decode.hip.
 #include <algorithm>
+#include <cstdlib>
 #include <type_traits>
 
 #include "common.h"
@@ -575,12 +576,19 @@ __global__ void __launch_bounds__(NTHREADS, OCC) k_gemm(GemmArgs a, int tiles_m,
 // order and applies the epilogue (no atomics: the result is reproducible).
 constexpr int ST_NW = 4;
 constexpr int ST_NT = 16 * ST_NW;
-constexpr int ST_KC = 128;
-constexpr int ST_PF = ST_KC / 16;   // weight steps in flight = steps per chunk (<= 8)
-constexpr int ST_GPR = ST_KC / 4;   // input granules (16 bytes) per row of a chunk
+constexpr int ST_MAX_M = 128;  // rows of the largest row-block count (MB = 8)
+// Chunk length by row blocks: 128 k up to 64 rows, 64 k above (the input
+// double buffer of 128 rows x 64 k plus the weight rings is 80 KB, two
+// workgroups per CU).
+constexpr int st_kc(int MB) { return MB > 4 ? 64 : 128; }
+constexpr int st_mb(int M) { return M <= 16 ? 1 : M <= 32 ? 2 : M <= 48 ? 3 : M <= 64 ? 4 : 8; }
 
 template <int EPI, int MB>
 __global__ void __launch_bounds__(ST_NW * 64) k_stream(GemmArgs a, int tiles_n, int KR, int KS) {
+    constexpr int ST_KC = st_kc(MB);     // k per input chunk
+    constexpr int ST_PF = ST_KC / 16;    // weight steps in flight = steps per chunk (<= 8)
+    constexpr int ST_GPR = ST_KC / 4;    // input granules (16 bytes) per row of a chunk
+    static_assert(ST_GPR >= 16 && ST_PF <= 8, "swizzle over 16 rows; waits of at most 7 + XI");
     constexpr int R = 16 * MB;                       // rows held (M <= R)
     constexpr int XI = R * ST_GPR / (ST_NW * 64);    // input load instructions per wavefront per chunk
     static_assert(XI * ST_NW * 64 == R * ST_GPR, "whole instructions");
@@ -824,11 +832,19 @@ hipError_t ln_after(const GemmArgs& a, hipStream_t s) {
 // CU (the partials must fit a.part_cap floats; ranges are whole chunks):
 // returns the splits, *KR the k per split.
 int stream_splits(const GemmArgs& a, int* KR) {
+    const int kc = st_kc(st_mb(a.M));
     const int tiles_n = (a.N + ST_NT - 1) / ST_NT;
-    const int kchunks = (a.K + ST_KC - 1) / ST_KC;
-    int KS = a.part ? std::max(1, std::min((512 + tiles_n - 1) / tiles_n, kchunks)) : 1;
+    const int kchunks = (a.K + kc - 1) / kc;
+    // Enough splits for about one workgroup per CU, never more: a
+    // workgroup's fixed cost (launch, first loads, partial store) repays
+    // longer ranges better than a second workgroup sharing its CU. Measured
+    // per product (ordered sum included): GPT-2 medium B=8 proj 9.53 ->
+    // 7.91 us at 256 workgroups instead of 512, fc 8.57 -> 7.41; XL B=32
+    // proj 18.29 -> 15.04, fc 17.92 -> 17.55 at 200 instead of 500; GPT-2
+    // small M = 128 QKV 18.6 -> 14.7, fc 20.6 -> 16.4.
+    int KS = a.part ? std::max(1, std::min(256 / tiles_n, kchunks)) : 1;
     while (KS > 1 && (long)KS * a.M * a.N > a.part_cap) KS--;
-    *KR = ((kchunks + KS - 1) / KS) * ST_KC;
+    *KR = ((kchunks + KS - 1) / KS) * kc;
     return (a.K + *KR - 1) / *KR;
 }
 
@@ -848,7 +864,24 @@ hipError_t skinny_epi(const GemmArgs& a, hipStream_t s) {
     if (a.M <= 16) return stream_mb<EPI, 1>(a, s);
     if (a.M <= 32) return stream_mb<EPI, 2>(a, s);
     if (a.M <= 48) return stream_mb<EPI, 3>(a, s);
-    return stream_mb<EPI, 4>(a, s);
+    if (a.M <= 64) return stream_mb<EPI, 4>(a, s);
+    return stream_mb<EPI, 8>(a, s);
+}
+
+// The few-row products take M <= SKINNY_MAX_M rows, and up to ST_MAX_M rows
+// of products whose 128 x 128 tiles would be too few for the CUs (the
+// reference's own B=1 T=128 forward: 6-24 tiles per product), with
+// row-major operands. CNGPT_HIP_STREAM128=0 / 1 forces the choice for
+// 64 < M <= 128 (A/B timing of the two paths).
+bool use_stream(const GemmArgs& a) {
+    if (a.M <= SKINNY_MAX_M) return true;
+    if (a.M > ST_MAX_M || a.km) return false;
+    static const int force = [] {
+        const char* e = getenv("CNGPT_HIP_STREAM128");
+        return e && (e[0] == '0' || e[0] == '1') ? e[0] - '0' : -1;
+    }();
+    if (force >= 0) return force == 1;
+    return (long)((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN) < 256;
 }
 
 // Share of the tile slots the last round of a launch fills when `res`
@@ -995,7 +1028,7 @@ hipError_t gemm_epi(const GemmArgs& a, hipStream_t s) {
 int launch_gemm_splits(const GemmArgs& a) {
     if (a.M <= 0 || a.N <= 0 || a.K <= 0 || (a.K & 3)) return 1;
     int KR;
-    if (a.M <= SKINNY_MAX_M) return stream_splits(a, &KR);
+    if (use_stream(a)) return stream_splits(a, &KR);
     return tile_splits(a, ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN), &KR);
 }
 
@@ -1018,7 +1051,7 @@ hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
             return hipErrorInvalidValue;
         return both ? gemm_km<EPI_RESID, 3>(a, s) : gemm_km<EPI_STORE, 2>(a, s);
     }
-    if (a.M <= SKINNY_MAX_M) {
+    if (use_stream(a)) {
         switch (a.epi) {
             case EPI_STORE: return skinny_epi<EPI_STORE>(a, s);
             case EPI_BIAS: return skinny_epi<EPI_BIAS>(a, s);
