@@ -409,6 +409,11 @@ int run_attn_row_proj(cngpt_hip_ctx* h, const float* qkv, long seq_stride, int B
 }
 
 void drop_graph(cngpt_hip_ctx* h) {
+    // the last launch of the executable graph may still be queued on the
+    // stream (a re-capture for a new batch follows the previous sequence's
+    // steps without a synchronisation): it must finish before the graph's
+    // resources are released
+    if (h->step_exec) (void)hipStreamSynchronize(h->stream);
     if (h->step_exec) (void)hipGraphExecDestroy(h->step_exec);
     h->step_exec = nullptr;
     h->graph_B = h->graph_cap = 0;
