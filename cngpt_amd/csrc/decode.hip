@@ -500,8 +500,24 @@ __global__ void __launch_bounds__(1024) k_argmax_part(const float* __restrict__ 
     const int* pi = part_i + (long)blockIdx.x * nparts;
     float best = -INFINITY;
     int bi = 0x7fffffff;
-    for (int g = threadIdx.x; g < nparts; g += 1024)
-        if (better(pv[g], pi[g], best, bi)) { best = pv[g]; bi = pi[g]; }
+    // 16 partials in flight per thread (as k_argmax_rows)
+    constexpr int U = 16;
+    for (int g0 = threadIdx.x; g0 < nparts; g0 += 1024 * U) {
+        float xv[U];
+        int xi[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int g = min(g0 + 1024 * u, nparts - 1);
+            xv[u] = pv[g];
+            xi[u] = pi[g];
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++)
+            if (g0 + 1024 * u < nparts && better(xv[u], xi[u], best, bi)) {
+                best = xv[u];
+                bi = xi[u];
+            }
+    }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
         const float ob = __shfl_xor(best, o, 64);
@@ -528,9 +544,20 @@ __global__ void __launch_bounds__(1024) k_argmax_rows(const float* __restrict__ 
     const float* row = logits + (long)blockIdx.x * V;
     float best = -INFINITY;
     int bi = 0x7fffffff;
-    for (int v = threadIdx.x; v < V; v += 1024) {
-        const float x = row[v];
-        if (x > best) { best = x; bi = v; }
+    // 16 loads in flight per thread, then compared in index order (one load
+    // at a time waited for each in turn: 49 memory round trips for a
+    // 50257-wide row)
+    constexpr int U = 16;
+    for (int v0 = threadIdx.x; v0 < V; v0 += 1024 * U) {
+        float x[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) x[u] = row[min(v0 + 1024 * u, V - 1)];
+#pragma unroll
+        for (int u = 0; u < U; u++)
+            if (v0 + 1024 * u < V && x[u] > best) {
+                best = x[u];
+                bi = v0 + 1024 * u;
+            }
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
