@@ -145,6 +145,8 @@ struct cngpt_hip_ctx {
     long loss_rows = 0;          // rows of the last cross-entropy (0: none)
     long ldp = 0;
     int pos_host = 0;            // staging for the position upload
+    unsigned long long* dtag = nullptr;  // tagged halves of the split one-pass decode attention
+    unsigned* dcnt = nullptr;            // and its per-(sequence, head) counters
     unsigned long long* ptag = nullptr;  // exchange words of the persistent decode
     unsigned ptag_next = 0;      // next unused tag (tags only grow until the words are cleared)
 
@@ -364,6 +366,7 @@ int run_attn_row_proj(cngpt_hip_ctx* h, const float* qkv, long seq_stride, int B
     a.q_pos = q_pos; a.pos_dev = pos_dev;
     a.scale = 1.0f / sqrtf((float)hs);
     a.part = h->attn_part; a.max_splits = h->attn_splits;
+    a.tag_part = h->dtag; a.tag_cnt = h->dcnt;
     const double keys = pos_dev ? 0.5 * max_keys : q_pos + 1.0;
     if (B > SKINNY && attention_dec_one_pass(B, c.n_head)) {
         // many (sequence, head) pairs: one pass, rows straight to c_proj's input
@@ -463,6 +466,7 @@ int ensure_arena(cngpt_hip_ctx* h, int B, int T, int all, int kv) {
     sz[n++] = nB * C * 4;                     // aoutc
     sz[n++] = nB * 4 * C * 4;                 // hidc
     sz[n++] = (size_t)persist_tagged_words(c.n_embd, c.n_head) * 8;  // ptag
+    sz[n++] = attn_dec1_tag_words(nB * (int)H, (int)(C / H)) * 8 + (size_t)nB * H * 4;  // dtag, dcnt
     sz[n++] = rows * sizeof(int);             // tgt
     sz[n++] = rows * sizeof(float);           // row_loss
     sz[n++] = sizeof(float);                  // loss
@@ -515,6 +519,9 @@ int ensure_arena(cngpt_hip_ctx* h, int B, int T, int all, int kv) {
     h->ptag = (unsigned long long*)take(sz[n++]);
     h->ptag_next = 0;
     HIP_TRY(hipMemsetAsync(h->ptag, 0, sz[n - 1], h->stream));
+    h->dtag = (unsigned long long*)take(sz[n++]);
+    h->dcnt = (unsigned*)(h->dtag + attn_dec1_tag_words(nB * (int)H, (int)(C / H)));
+    HIP_TRY(hipMemsetAsync(h->dtag, 0, sz[n - 1], h->stream));
     h->tgt = (int*)take(sz[n++]);
     h->row_loss = (float*)take(sz[n++]);
     h->loss = (float*)take(sz[n++]);

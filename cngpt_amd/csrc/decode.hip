@@ -383,15 +383,30 @@ __global__ void __launch_bounds__(256) k_attn_dec(AttnDecArgs a) {
 // 12.3 us, medium B=8 t=300 10.6 -> 7.8 us, medium B=8 t=1000 19.8 -> 19.8
 // us; with fewer pairs (small B=4 t=1000: 12.1 -> 15.4 us) the split form
 // keeps more loads in flight.
+//
+// With fewer pairs than CUs (SPL = 2: B * H < 256, e.g. GPT-2 medium B=8's
+// 128 pairs, whose workgroups leave half the CUs idle) the keys of a pair
+// are split over two workgroups. Each writes its unnormalised (m, l, o) as
+// tagged 64-bit words (the tag in the high half, agent-scope atomics: the
+// L2 of one XCD is not coherent with another's), and the second to count
+// itself in on the pair's counter merges both halves, half 0 first whatever
+// the arrival order (reproducible), and writes the row. Tags come from the
+// counter (each use adds 2), so both halves of a use agree on theirs and no
+// use can match an earlier use's words; the first to count has written its
+// words before counting, so the second never waits on a workgroup that has
+// not run.
 constexpr int DEC1_MIN_PAIRS = 128;
-template <int HS, int NW, int PD>
+constexpr int DEC1_SPLIT_BELOW = 256;
+typedef unsigned long long u64;
+template <int HS, int NW, int PD, int SPL>
 __global__ void __launch_bounds__(NW * 64) k_attn_dec1(AttnDecArgs a, float* __restrict__ out,
                                                        long ldo) {
     constexpr int LPK = HS / 4;    // lanes per key
     constexpr int KPW = 64 / LPK;  // keys per wavefront pass
+    static_assert(LPK <= 64, "the merged row is held by wavefront 0");
     __shared__ float wm[NW], wl[NW];
     __shared__ f32x4 wo[NW][LPK];
-    const int bh = blockIdx.x;
+    const int bh = blockIdx.x / SPL, half = blockIdx.x % SPL;
     const int b = bh / a.H, h = bh % a.H;
     const int t = a.pos_dev ? *a.pos_dev : a.q_pos;
     const int nk = t + 1;
@@ -399,7 +414,9 @@ __global__ void __launch_bounds__(NW * 64) k_attn_dec1(AttnDecArgs a, float* __r
     const float* base = a.qkv + (long)b * a.seq_stride * C3 + h * HS;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int kl = lane / LPK, d4 = lane % LPK;
-    const int k0 = (int)((long)wave * nk / NW), k1 = (int)((long)(wave + 1) * nk / NW);
+    // this workgroup's keys [kb, ke), split over its wavefronts
+    const int kb = (int)((long)half * nk / SPL), nks = (int)((long)(half + 1) * nk / SPL) - kb;
+    const int k0 = kb + (int)((long)wave * nks / NW), k1 = kb + (int)((long)(wave + 1) * nks / NW);
     const int npass = (k1 - k0 + KPW - 1) / KPW;
     const f32x4 q =
         *(const f32x4*)(base + (long)t * C3 + d4 * 4) * (a.scale * 1.4426950408889634f);
@@ -456,19 +473,91 @@ __global__ void __launch_bounds__(NW * 64) k_attn_dec1(AttnDecArgs a, float* __r
         wl[wave] = l;
     }
     __syncthreads();
-    // then the wavefronts, in order (key 0 is in every row, so L > 0)
+    // then the wavefronts, in order (key 0 is in every row, so L > 0 once
+    // the halves of a split pair are merged)
+    float M = -INFINITY, L = 0.f;
+    f32x4 O = {0.f, 0.f, 0.f, 0.f};
     if (tid < LPK) {
-        float M = -INFINITY;
         for (int w = 0; w < NW; w++) M = fmaxf(M, wm[w]);
-        float L = 0.f;
-        f32x4 O = {0.f, 0.f, 0.f, 0.f};
         for (int w = 0; w < NW; w++) {
             const float f = wm[w] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(wm[w] - M);
             L += wl[w] * f;
             O += wo[w][tid] * f;
         }
-        *(f32x4*)(out + (long)b * ldo + h * HS + tid * 4) = O * (1.0f / L);
     }
+    if (SPL == 1) {
+        if (tid < LPK) *(f32x4*)(out + (long)b * ldo + h * HS + tid * 4) = O * (1.0f / L);
+        return;
+    }
+    if (wave != 0) return;
+    // words of half s of this pair: m, l, o[HS]
+    constexpr int NWD = HS + 2;
+    unsigned* cnt = a.tag_cnt + bh;
+    const unsigned tag = (unsigned)__builtin_amdgcn_readfirstlane(
+                             (int)__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) /
+                             2u + 1u;
+    auto word = [&](float v) { return ((u64)tag << 32) | (u64)__float_as_uint(v); };
+    u64* mine = a.tag_part + ((long)bh * 2 + half) * NWD;
+    if (lane < LPK)
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+            __hip_atomic_store(mine + 2 + 4 * lane + c, word(O[c]), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    if (lane == 0) {
+        __hip_atomic_store(mine, word(M), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(mine + 1, word(L), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    // the words are written before the count
+    wait_vmcnt<0>();
+    unsigned old = 0;
+    if (lane == 0) old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    old = (unsigned)__builtin_amdgcn_readfirstlane((int)old);
+    if ((old & 1u) == 0) return;  // first in: the other half merges
+    // second in: the other half's words, until each carries this use's tag
+    const u64* other = a.tag_part + ((long)bh * 2 + (1 - half)) * NWD;
+    u64 w[6];
+    auto fetch_other = [&]() {
+        const int e = 2 + 4 * min(lane, LPK - 1);
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+            w[c] = __hip_atomic_load(other + e + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        w[4] = __hip_atomic_load(other, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        w[5] = __hip_atomic_load(other + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    };
+    auto current = [&]() {
+        bool ok = true;
+#pragma unroll
+        for (int c = 0; c < 6; c++) ok = ok && (unsigned)(w[c] >> 32) == tag;
+        return ok;
+    };
+    fetch_other();
+    bool ok = current();
+    // the other half counted itself in after its words' stores completed, so
+    // they become visible within a few round trips; the limit only guards
+    // against a fault, and then the row is poisoned (NaN) rather than hung
+    for (long it = 0; __builtin_amdgcn_ballot_w64(!ok) != 0 && it < (1L << 20); it++) {
+        __builtin_amdgcn_s_sleep(1);
+        if (!ok) {
+            fetch_other();
+            ok = current();
+        }
+    }
+    const float Mo = __uint_as_float((unsigned)w[4]), Lo = __uint_as_float((unsigned)w[5]);
+    const f32x4 Oo = {__uint_as_float((unsigned)w[0]), __uint_as_float((unsigned)w[1]),
+                      __uint_as_float((unsigned)w[2]), __uint_as_float((unsigned)w[3])};
+    // half 0 first, then half 1
+    const float M0 = half == 0 ? M : Mo, L0 = half == 0 ? L : Lo;
+    const float M1 = half == 0 ? Mo : M, L1 = half == 0 ? Lo : L;
+    const f32x4 O0 = half == 0 ? O : Oo, O1 = half == 0 ? Oo : O;
+    const float Mx = fmaxf(M0, M1);
+    const float f0 = M0 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M0 - Mx);
+    const float f1 = M1 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M1 - Mx);
+    const float Ls = L0 * f0 + L1 * f1;
+    const f32x4 Os = O0 * f0 + O1 * f1;
+    const bool all_ok = __builtin_amdgcn_ballot_w64(!ok) == 0;
+    if (lane < LPK)
+        *(f32x4*)(out + (long)b * ldo + h * HS + lane * 4) =
+            all_ok ? Os * (1.0f / Ls) : f32x4{NAN, NAN, NAN, NAN};
 }
 
 // Rows of merged attention for the consumers that are not k_dgemv (M > 8).
@@ -625,14 +714,19 @@ hipError_t attn_dec_hs(const AttnDecArgs& a, int B, int max_keys, hipStream_t s)
 
 template <int HS>
 hipError_t attn_dec1_hs(const AttnDecArgs& a, int B, float* out, long ldo, hipStream_t s) {
-    if (B * a.H < 384) k_attn_dec1<HS, 16, 4><<<B * a.H, 16 * 64, 0, s>>>(a, out, ldo);
-    else k_attn_dec1<HS, 8, 4><<<B * a.H, 8 * 64, 0, s>>>(a, out, ldo);
+    const int pairs = B * a.H;
+    if (pairs < DEC1_SPLIT_BELOW && a.tag_part && a.tag_cnt)
+        k_attn_dec1<HS, 16, 4, 2><<<2 * pairs, 16 * 64, 0, s>>>(a, out, ldo);
+    else if (pairs < 384) k_attn_dec1<HS, 16, 4, 1><<<pairs, 16 * 64, 0, s>>>(a, out, ldo);
+    else k_attn_dec1<HS, 8, 4, 1><<<pairs, 8 * 64, 0, s>>>(a, out, ldo);
     return hipGetLastError();
 }
 
 }  // namespace
 
 bool attention_dec_one_pass(int B, int H) { return (long)B * H >= DEC1_MIN_PAIRS; }
+
+size_t attn_dec1_tag_words(int pairs, int hs) { return (size_t)pairs * 2 * (hs + 2); }
 
 hipError_t launch_attention_dec_rows(const AttnDecArgs& a, int B, float* out, long ldo,
                                      hipStream_t s) {

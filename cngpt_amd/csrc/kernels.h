@@ -133,7 +133,15 @@ struct AttnDecArgs {
     float scale;
     float* part;
     int max_splits;
+    // Optional, for the one-pass attention with its keys split over two
+    // workgroups per (sequence, head) (too few pairs for one per CU): per
+    // pair a counter and 2 * (hs + 2) tagged words, zeroed once and then
+    // used only by that attention (attn_dec1_tag_words 64-bit words and one
+    // 32-bit counter per pair, for B * H pairs).
+    unsigned long long* tag_part;
+    unsigned* tag_cnt;
 };
+size_t attn_dec1_tag_words(int pairs, int hs);
 int attn_dec_keys_per_split(int hs);
 // max_keys bounds t + 1 over every launch of a captured graph (sizes the grid).
 hipError_t launch_attention_dec(const AttnDecArgs& a, int B, int max_keys, hipStream_t s);
