@@ -14,7 +14,10 @@
  * logits); without it the pass produces the logits of every position, which
  * is what the reference's gpt_forward computes. The parity line compares
  * the final-position logits of the two modes on the LCG tokens of
- * src/cngpt.c:338-342.
+ * src/cngpt.c:338-342, and the fast path with an independent route to
+ * the same final-position logits (prefill of the first T - 1 tokens, then
+ * one KV-cache decode step), as the reference compares gpt_forward_fast
+ * with gpt_forward (src/cngpt.c:334-356).
  *
  * sample follows gpt_sample (src/model.c:991-1016) and sample_top_k
  * (src/model.c:927-989): prompt token ids, one rand() draw per new token,
@@ -126,7 +129,37 @@ static int cmd_bench(int argc, char **argv)
             for (int v = 0; v < V; v++) maxd = fmaxf(maxd, fabsf(fl[v] - last[v]));
             printf("  max |logit diff| final position, fast vs all-positions : %.3e\n",
                    (double)maxd);
+            memcpy(last, fl, (size_t)V * sizeof(float));
         }
+    }
+    if (!rc && T >= 2) {
+        /* The reference checks its fast path against the straightforward
+         * gpt_forward (src/cngpt.c:334-356). Here the independent route to
+         * the same logits is the KV-cache decode: the first T - 1 tokens
+         * prefilled, then one decode step for token T - 1, whose row goes
+         * through every layer on the decode kernels (products over one row,
+         * attention of one query against the cache) instead of the prefill
+         * tiles. */
+        cngpt_hip_ctx *h = NULL;
+        const cngpt_hip_config c = {m.cfg.n_layer, m.cfg.n_head, m.cfg.n_embd, m.cfg.vocab_size,
+                                    m.cfg.block_size};
+        float *dl = malloc((size_t)V * sizeof(float));
+        const char *dev = getenv("CNGPT_HIP_DEVICE");
+        int drc = dl ? cngpt_hip_create(dev && *dev ? atoi(dev) : 0, &h) : 1;
+        if (!drc) drc = cngpt_hip_load_params(h, &c, m.param_buf, m.n_params);
+        if (!drc) drc = cngpt_hip_decode_begin(h, tk, 1, T - 1, T, NULL);
+        if (!drc) drc = cngpt_hip_decode_step(h, tk + T - 1, dl);
+        if (drc) {
+            fprintf(stderr, "bench: decode check failed: %s\n", cngpt_hip_last_error());
+            rc = 1;
+        } else {
+            float maxd = 0.0f;
+            for (int v = 0; v < V; v++) maxd = fmaxf(maxd, fabsf(dl[v] - last[v]));
+            printf("  max |logit diff| final position, fast vs KV-cache decode : %.3e\n",
+                   (double)maxd);
+        }
+        if (h) cngpt_hip_destroy(h);
+        free(dl);
     }
     if (!rc) {
         memset(tk, 0, (size_t)B * T * sizeof(int));   /* src/cngpt.c:283 */
