@@ -23,6 +23,7 @@
 #include <cstring>
 #include <mutex>
 #include <thread>
+#include <unordered_map>
 #include <vector>
 
 #include "../../include/cngpt_hip.h"
@@ -118,6 +119,20 @@ struct cngpt_hip_ctx {
     std::vector<LayerW> layers;
     LayerW* d_layers = nullptr;  // device copy of layers (persistent decode), at the
                                  // end of the parameter allocation
+    // Packed copies (launch_pack_w) of the weight matrices, after the layer
+    // table in the same allocation, read by the few-row products.
+    // CNGPT_HIP_PACK=0 in the environment at create time leaves them out.
+    // A training view may change the parameters: it marks the copies stale,
+    // and the next forward or decode entry point packs them again.
+    struct Packed {
+        const float* W;
+        float* Wp;
+        int N, K;
+    };
+    bool use_packed = true;
+    bool packed_fresh = false;
+    std::vector<Packed> packs;
+    std::unordered_map<const float*, const float*> packed_of;
 
     // activation arena: one allocation, carved below
     char* d_act = nullptr;
@@ -254,6 +269,10 @@ int run_gemm(cngpt_hip_ctx* h, const float* X, const float* W, const float* bias
     }
     GemmArgs a{};
     a.X = X; a.W = W; a.bias = bias; a.Y = Y;
+    if (h->use_packed) {
+        const auto it = h->packed_of.find(W);
+        if (it != h->packed_of.end()) a.Wp = it->second;
+    }
     a.M = M; a.N = N; a.K = K;
     a.ldy = ldy < 0 ? N : ldy;
     a.seg = seg; a.seg_stride = seg_stride;
@@ -845,6 +864,27 @@ long params_of(const cngpt_hip_config* c) {
 // Make h->d_params hold the parameters of shape cfg: reuse the allocation
 // when the shape is unchanged, else free it (and the activations, which
 // depend on the shape) and allocate anew.
+// Bytes of the packed weight copies: the token embedding (the lm_head's
+// weights) and each layer's four matrices.
+size_t packed_bytes(const cngpt_hip_config* cfg) {
+    const int C = cfg->n_embd;
+    const size_t layer = align_up(packed_w_floats(3 * C, C) * sizeof(float)) +
+                         align_up(packed_w_floats(C, C) * sizeof(float)) +
+                         align_up(packed_w_floats(4 * C, C) * sizeof(float)) +
+                         align_up(packed_w_floats(C, 4 * C) * sizeof(float));
+    return align_up(packed_w_floats(cfg->vocab_size, C) * sizeof(float)) + layer * cfg->n_layer;
+}
+
+// Packs the weight matrices again when a training view may have changed
+// them (kernels on the handle's stream, ordered before what follows).
+int fresh_packed(cngpt_hip_ctx* h) {
+    if (!h->use_packed || h->packed_fresh) return 0;
+    HIP_TRY(hipSetDevice(h->device));
+    for (const cngpt_hip_ctx::Packed& p : h->packs) HIP_TRY(launch_pack_w(p.W, p.Wp, p.N, p.K, h->stream));
+    h->packed_fresh = true;
+    return 0;
+}
+
 int params_prepare(cngpt_hip_ctx* h, const cngpt_hip_config* cfg) {
     HIP_TRY(hipSetDevice(h->device));
     if (h->d_params && memcmp(&h->cfg, cfg, sizeof(*cfg)) == 0) return 0;
@@ -862,10 +902,12 @@ int params_prepare(cngpt_hip_ctx* h, const cngpt_hip_config* cfg) {
     }
     h->have_params = false;
     h->d_layers = nullptr;
-    // one allocation: the parameters, then the table of per-layer pointers
-    // into them that the persistent decode reads
+    // one allocation: the parameters, the table of per-layer pointers into
+    // them that the persistent decode reads, the packed weight copies
     const long want = params_of(cfg);
-    const size_t bytes = align_up((size_t)want * sizeof(float)) + (size_t)cfg->n_layer * sizeof(LayerW);
+    const size_t bytes = align_up((size_t)want * sizeof(float)) +
+                         align_up((size_t)cfg->n_layer * sizeof(LayerW)) +
+                         (h->use_packed ? packed_bytes(cfg) : 0);
     if (hipMalloc(&h->d_params, bytes) != hipSuccess) {
         (void)hipGetLastError();
         h->d_params = nullptr;
@@ -905,6 +947,26 @@ int params_commit(cngpt_hip_ctx* h, const cngpt_hip_config* cfg) {
     h->lnf_b = p;
     HIP_TRY(hipMemcpy(h->d_layers, h->layers.data(), (size_t)cfg->n_layer * sizeof(LayerW),
                       hipMemcpyHostToDevice));
+    h->packs.clear();
+    h->packed_of.clear();
+    h->packed_fresh = false;
+    if (h->use_packed) {
+        char* q = (char*)h->d_layers + align_up((size_t)cfg->n_layer * sizeof(LayerW));
+        auto add = [&](const float* W, int N, int K) {
+            h->packs.push_back({W, (float*)q, N, K});
+            h->packed_of[W] = (const float*)q;
+            q += align_up(packed_w_floats(N, K) * sizeof(float));
+        };
+        const int c = (int)C;
+        add(h->wte, (int)V, c);
+        for (const LayerW& w : h->layers) {
+            add(w.attn_w, 3 * c, c);
+            add(w.proj_w, c, c);
+            add(w.fc_w, 4 * c, c);
+            add(w.mlp_w, c, 4 * c);
+        }
+        if (fresh_packed(h)) return -1;
+    }
     h->have_params = true;
     return 0;
 }
@@ -1121,6 +1183,7 @@ int ctx_view(cngpt_hip_ctx* h, CtxView* v) {
     v->lnf_w = h->lnf_w;
     v->lnf_b = h->lnf_b;
     v->layers = h->layers.data();
+    h->packed_fresh = false;  // the view can write the parameters
     return 0;
 }
 
@@ -1157,6 +1220,8 @@ int cngpt_hip_create(int device, cngpt_hip_ctx** out) {
     h->use_graph = !(g && g[0] == '0');
     const char* pp = getenv("CNGPT_HIP_PERSIST");
     if (pp && pp[0] == '0') h->decode_path = CNGPT_DECODE_KERNELS;
+    const char* pk = getenv("CNGPT_HIP_PACK");
+    h->use_packed = !(pk && pk[0] == '0');
     if (hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking) != hipSuccess) {
         delete h;
         return fail("hipStreamCreate failed");
@@ -1240,7 +1305,7 @@ int cngpt_hip_upload_tokens(cngpt_hip_ctx* h, const int* tokens, int B, int T) {
 }
 
 int cngpt_hip_forward_resident(cngpt_hip_ctx* h, int B, int T, int mode) {
-    if (need_params(h)) return -1;
+    if (need_params(h) || fresh_packed(h)) return -1;
     if (mode != CNGPT_LAST && mode != CNGPT_ALL) return fail("bad mode %d", mode);
     if (B > h->capB || T > h->capT || (mode == CNGPT_ALL && !h->capAll))
         return fail("forward_resident: arena not reserved for B=%d T=%d mode=%d", B, T, mode);
@@ -1251,7 +1316,7 @@ int cngpt_hip_forward_resident(cngpt_hip_ctx* h, int B, int T, int mode) {
 
 int cngpt_hip_forward_noalloc(cngpt_hip_ctx* h, const int* tokens, int B, int T, int mode,
                               float* logits, int* err) {
-    if (need_params(h)) return -1;
+    if (need_params(h) || fresh_packed(h)) return -1;
     if (mode != CNGPT_LAST && mode != CNGPT_ALL) return fail("bad mode %d", mode);
     if (!tokens || !logits) return fail("forward_noalloc: null device pointer");
     if (B <= 0 || T <= 0) return fail("B=%d T=%d must be positive", B, T);
@@ -1281,7 +1346,7 @@ int cngpt_hip_forward_noalloc(cngpt_hip_ctx* h, const int* tokens, int B, int T,
 
 int cngpt_hip_forward(cngpt_hip_ctx* h, const int* tokens, int B, int T, int mode,
                       float* logits_out) {
-    if (need_params(h)) return -1;
+    if (need_params(h) || fresh_packed(h)) return -1;
     if (mode != CNGPT_LAST && mode != CNGPT_ALL) return fail("bad mode %d", mode);
     if (!tokens) return fail("null tokens");
     if (B <= 0 || T <= 0) return fail("B=%d T=%d must be positive", B, T);
@@ -1381,7 +1446,7 @@ int cngpt_hip_cross_entropy(cngpt_hip_ctx* h, const int* targets, int B, int T, 
 
 int cngpt_hip_decode_begin(cngpt_hip_ctx* h, const int* prompt, int B, int T, int capacity,
                            float* logits_out) {
-    if (need_params(h)) return -1;
+    if (need_params(h) || fresh_packed(h)) return -1;
     if (!prompt) return fail("null prompt");
     if (B <= 0 || T <= 0) return fail("B=%d T=%d must be positive", B, T);
     if (capacity <= T || capacity > h->cfg.block_size)
@@ -1410,7 +1475,7 @@ int cngpt_hip_decode_begin(cngpt_hip_ctx* h, const int* prompt, int B, int T, in
 }
 
 int cngpt_hip_decode_step(cngpt_hip_ctx* h, const int* tokens, float* logits_out) {
-    if (need_params(h)) return -1;
+    if (need_params(h) || fresh_packed(h)) return -1;
     if (h->kvB == 0) return fail("decode_step before decode_begin");
     if (h->kvLen >= h->capKV)
         return fail("KV cache full (%d positions)", h->capKV);
@@ -1441,7 +1506,7 @@ int cngpt_hip_decode_step(cngpt_hip_ctx* h, const int* tokens, float* logits_out
 
 int cngpt_hip_generate(cngpt_hip_ctx* h, int n_new, float temperature, int top_k,
                        const float* draws, int* out_tokens) {
-    if (need_params(h)) return -1;
+    if (need_params(h) || fresh_packed(h)) return -1;
     if (h->kvB == 0) return fail("generate before decode_begin");
     if (!out_tokens) return fail("null output");
     if (n_new <= 0) return fail("n_new=%d must be positive", n_new);

@@ -571,6 +571,10 @@ __global__ void __launch_bounds__(NTHREADS, OCC) k_gemm(GemmArgs a, int tiles_m,
 // boundaries (a register ring loses that: the compiler waits for every load
 // in flight at the top of each loop trip), and no load is in flight past
 // the range.
+// With PK the weights come from their packed copy (k_pack_w): the 1 KB of a
+// wavefront's step is contiguous there instead of 16 rows x 64 bytes, each
+// 128-byte line of W split over two steps (measured on a bare stream of the
+// GPT-2 XL MLP weights, 1 KB units: 4.9 TB/s packed, 3.6 TB/s row-major).
 // When the column tiles alone would leave CUs idle, K is split over KS
 // workgroups that write partial tiles; k_stream_reduce then sums them in
 // order and applies the epilogue (no atomics: the result is reproducible).
@@ -583,7 +587,7 @@ constexpr int ST_MAX_M = 128;  // rows of the largest row-block count (MB = 8)
 constexpr int st_kc(int MB) { return MB > 4 ? 64 : 128; }
 constexpr int st_mb(int M) { return M <= 16 ? 1 : M <= 32 ? 2 : M <= 48 ? 3 : M <= 64 ? 4 : 8; }
 
-template <int EPI, int MB>
+template <int EPI, int MB, bool PK>
 __global__ void __launch_bounds__(ST_NW * 64) k_stream(GemmArgs a, int tiles_n, int KR, int KS) {
     constexpr int ST_KC = st_kc(MB);     // k per input chunk
     constexpr int ST_PF = ST_KC / 16;    // weight steps in flight = steps per chunk (<= 8)
@@ -602,6 +606,10 @@ __global__ void __launch_bounds__(ST_NW * 64) k_stream(GemmArgs a, int tiles_n, 
     const int nchunks = (ke - kb + ST_KC - 1) / ST_KC;
     const int col = tn * ST_NT + 16 * wave + lc;
     const float* wrow = a.W + (long)min(col, N - 1) * K + g4;
+    // packed: column block col / 16 (the last one for columns past N), its
+    // k steps of 256 floats each, this lane's 16 bytes at 4 * lane
+    const int KQ = (K + 15) >> 4;
+    const float* wpk = PK ? a.Wp + (long)min(col >> 4, (N - 1) >> 4) * KQ * 256 + 4 * lane : nullptr;
 
     // input chunk c into buffer b: granule g = (i * ST_NW + wave) * 64 +
     // lane of the chunk sits at row g / ST_GPR, slot g % ST_GPR and holds k
@@ -627,7 +635,10 @@ __global__ void __launch_bounds__(ST_NW * 64) k_stream(GemmArgs a, int tiles_n, 
     // past the range re-read K - 4 and are zeroed at use) into ring slot
     // s % ST_PF
     auto issue_w = [&](int s) {
-        lds_dma16(wrow + min(kb + 16 * s, K - 4 - g4), &ws[wave][s % ST_PF][0]);
+        if (PK)
+            lds_dma16(wpk + (long)min((kb >> 4) + s, KQ - 1) * 256, &ws[wave][s % ST_PF][0]);
+        else
+            lds_dma16(wrow + min(kb + 16 * s, K - 4 - g4), &ws[wave][s % ST_PF][0]);
     };
 
     f32x4 acc[MB];
@@ -853,7 +864,10 @@ hipError_t stream_mb(const GemmArgs& a, hipStream_t s) {
     const int tiles_n = (a.N + ST_NT - 1) / ST_NT;
     int KR;
     const int KS = stream_splits(a, &KR);
-    k_stream<EPI, MB><<<tiles_n * KS, ST_NW * 64, 0, s>>>(a, tiles_n, KR, KS);
+    if (a.Wp)
+        k_stream<EPI, MB, true><<<tiles_n * KS, ST_NW * 64, 0, s>>>(a, tiles_n, KR, KS);
+    else
+        k_stream<EPI, MB, false><<<tiles_n * KS, ST_NW * 64, 0, s>>>(a, tiles_n, KR, KS);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     return KS == 1 ? ln_after(a, s) : reduce_splits<EPI>(a, KS, s);
@@ -1023,7 +1037,33 @@ hipError_t gemm_epi(const GemmArgs& a, hipStream_t s) {
     return e != hipSuccess ? e : ln_after(a, s);
 }
 
+// Packed copy of W [N][K] (row-major, K a multiple of 4) for k_stream:
+// column block b (columns 16 b .. 16 b + 15) holds ceil(K / 16) steps of 256
+// floats, and floats 4 l .. 4 l + 3 of step q are W[16 b + l % 16][16 q +
+// 4 (l / 16) .. +3], zero past N or K. One thread per 16 bytes written.
+__global__ void __launch_bounds__(256) k_pack_w(const float* __restrict__ W, float* __restrict__ Wp,
+                                                int N, int K, long n4) {
+    const long i = (long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n4) return;
+    const int l = (int)(i & 63), KQ = (K + 15) >> 4;
+    const long bq = i >> 6;
+    const long n = bq / KQ * 16 + (l & 15);
+    const int k = (int)(bq % KQ) * 16 + 4 * (l >> 4);
+    f32x4 v = {0.f, 0.f, 0.f, 0.f};
+    if (n < N && k < K) v = *(const f32x4*)&W[n * K + k];
+    *(f32x4*)&Wp[4 * i] = v;
+}
+
 }  // namespace
+
+size_t packed_w_floats(int N, int K) { return (size_t)((N + 15) / 16) * ((K + 15) / 16) * 256; }
+
+hipError_t launch_pack_w(const float* W, float* Wp, int N, int K, hipStream_t s) {
+    if (N <= 0 || K <= 0 || (K & 3)) return hipErrorInvalidValue;
+    const long n4 = (long)(packed_w_floats(N, K) / 4);
+    k_pack_w<<<(unsigned)((n4 + 255) / 256), 256, 0, s>>>(W, Wp, N, K, n4);
+    return hipGetLastError();
+}
 
 int launch_gemm_splits(const GemmArgs& a) {
     if (a.M <= 0 || a.N <= 0 || a.K <= 0 || (a.K & 3)) return 1;

@@ -21,6 +21,9 @@ hipError_t launch_gather_rows(const float* src, long src_stride, float* dst, int
 struct GemmArgs {
     const float* X;
     const float* W;
+    // Optional packed copy of W (launch_pack_w), read instead of W by the
+    // few-row products; the other paths read W.
+    const float* Wp;
     const float* bias;
     float* Y;
     int M, N, K;
@@ -55,6 +58,10 @@ hipError_t launch_gemm(const GemmArgs& a, hipStream_t s);
 // Number of K splits launch_gemm uses for a (1: none; then a LayerNorm
 // asked for with ln_out is a launch of its own after the product).
 int launch_gemm_splits(const GemmArgs& a);
+// Floats of the packed copy of an [N][K] weight matrix, and the launch
+// that writes it (K a multiple of 4).
+size_t packed_w_floats(int N, int K);
+hipError_t launch_pack_w(const float* W, float* Wp, int N, int K, hipStream_t s);
 
 // decode.hip
 // Partials of the split one-query attention, merged by their consumer:

@@ -65,7 +65,8 @@ const char* kat_error(void) { return g_err; }
 // GELU, 3 Y += . + bias (Y is read). path 0: launch_gemm (M <= 64 the
 // weight-streaming k_stream, split over K when its column tiles are few;
 // larger M the 128 x 128 MFMA tiles); path 1: launch_dgemv (M <= 8, the
-// decode products).
+// decode products); path 2: launch_gemm with the packed copy of W
+// (launch_pack_w), which k_stream reads instead of W.
 int kat_gemm(const float* X, const float* W, const float* bias, float* Y, int M, int N, int K,
              int epi, int path) {
     if (M <= 0 || N <= 0 || K <= 0 || epi < 0 || epi > 3) return fail("bad shape or epilogue");
@@ -75,11 +76,16 @@ int kat_gemm(const float* X, const float* W, const float* bias, float* Y, int M,
     float* dw = d.put(W, (size_t)N * K);
     float* db = d.put(bias, bias ? (size_t)N : 0);
     float* dy = d.put(epi == EPI_RESID ? Y : nullptr, (size_t)M * N);
-    float* part = path == 0 ? d.put<float>(nullptr, 1 << 24) : nullptr;
-    if (!dx || !dw || !db || !dy || (path == 0 && !part)) return fail("device allocation failed");
-    if (path == 0) {
+    if (path < 0 || path > 2) return fail("bad path");
+    const bool pk = path == 2;
+    float* part = path != 1 ? d.put<float>(nullptr, 1 << 24) : nullptr;
+    float* dwp = pk ? d.put<float>(nullptr, packed_w_floats(N, K)) : nullptr;
+    if (!dx || !dw || !db || !dy || (path != 1 && !part) || (pk && !dwp))
+        return fail("device allocation failed");
+    if (pk) TRY(launch_pack_w(dw, dwp, N, K, nullptr));
+    if (path != 1) {
         GemmArgs a{};
-        a.X = dx; a.W = dw; a.bias = db; a.Y = dy;
+        a.X = dx; a.W = dw; a.Wp = dwp; a.bias = db; a.Y = dy;
         a.M = M; a.N = N; a.K = K; a.ldy = N;
         a.epi = epi;
         a.part = part; a.part_cap = 1 << 24;  // the forward's 64 MB
@@ -94,6 +100,39 @@ int kat_gemm(const float* X, const float* W, const float* bias, float* Y, int M,
     TRY(hipDeviceSynchronize());
     TRY(hipMemcpy(Y, dy, (size_t)M * N * sizeof(float), hipMemcpyDeviceToHost));
     return 0;
+}
+
+// Y[M,N] += X . W^T + bias (launch_gemm), and lnout = LayerNorm(Y rows)
+// with gains lnw and biases lnb, formed by the split sum when K is split;
+// returns the splits (> 1: the sum formed the LayerNorm), -1 on failure.
+int kat_gemm_ln(const float* X, const float* W, const float* bias, float* Y, const float* lnw,
+                const float* lnb, float* lnout, int M, int N, int K) {
+    if (M <= 0 || N <= 0 || K <= 0) return fail("bad shape");
+    Dev d;
+    float* dx = d.put(X, (size_t)M * K);
+    float* dw = d.put(W, (size_t)N * K);
+    float* db = d.put(bias, (size_t)N);
+    float* dy = d.put(Y, (size_t)M * N);
+    float* dlw = d.put(lnw, (size_t)N);
+    float* dlb = d.put(lnb, (size_t)N);
+    float* dln = d.put<float>(nullptr, (size_t)M * N);
+    float* part = d.put<float>(nullptr, 1 << 24);
+    if (!dx || !dw || !db || !dy || !dlw || !dlb || !dln || !part)
+        return fail("device allocation failed");
+    GemmArgs a{};
+    a.X = dx; a.W = dw; a.bias = db; a.Y = dy;
+    a.M = M; a.N = N; a.K = K; a.ldy = N;
+    a.epi = EPI_RESID;
+    a.part = part; a.part_cap = 1 << 24;
+    const int splits = launch_gemm_splits(a);
+    if (splits > 1) {
+        a.ln_w = dlw; a.ln_b = dlb; a.ln_out = dln;
+    }
+    TRY(launch_gemm(a, nullptr));
+    TRY(hipDeviceSynchronize());
+    TRY(hipMemcpy(Y, dy, (size_t)M * N * sizeof(float), hipMemcpyDeviceToHost));
+    TRY(hipMemcpy(lnout, dln, (size_t)M * N * sizeof(float), hipMemcpyDeviceToHost));
+    return splits;
 }
 
 // out[rows, C] = LayerNorm(x) with gains w and biases b.

@@ -57,7 +57,7 @@ def kat():
     assert os.path.exists(LIB), "tests/kat/libcngpt_kat.so not built (run __graft_entry__.build())"
     lib = ctypes.CDLL(LIB)
     lib.kat_error.restype = ctypes.c_char_p
-    for name in ("kat_gemm", "kat_layernorm", "kat_attention", "kat_attention_row"):
+    for name in ("kat_gemm", "kat_gemm_ln", "kat_layernorm", "kat_attention", "kat_attention_row"):
         getattr(lib, name).restype = ctypes.c_int
     return lib
 
@@ -248,6 +248,10 @@ def test_softmax_error_bound_dense_grid(kat, kind):
     (0, 1100, 4000, 1600, 3), # stream-K: 9 x 32 ragged tiles, residual
     (0, 37, 100, 3072, 3),    # weight-streaming product, split over K
     (0, 5, 2304, 768, 1),     # weight-streaming, QKV width
+    (2, 37, 100, 3072, 3),    # weight-streaming from packed weights, split over K
+    (2, 20, 771, 1600, 2),    # packed weights, ragged last column block, GELU
+    (2, 100, 333, 36, 1),     # packed, K = 36 (zero-padded last step), 128-row tiles
+    (2, 128, 2304, 768, 1),   # packed, 128 rows, split over K
     (1, 2, 771, 1024, 3),     # decode product
 ])
 def test_gemm_error_bound_float64(kat, path, M, N, K, epi):
@@ -279,6 +283,53 @@ def test_gemm_error_bound_float64(kat, path, M, N, K, epi):
     print(f"gemm path {path} {M}x{N}x{K} epi {epi}: max err/bound "
           f"{float((err / bound).max()):.3f}", flush=True)
     assert np.all(err <= bound)
+
+
+@pytest.mark.parametrize("M,N,K,epi", [
+    (3, 2304, 768, 1), (24, 3200, 800, 2), (40, 1600, 6400, 3), (64, 50257, 64, 0),
+    (100, 333, 36, 3), (128, 771, 1280, 1),
+])
+def test_gemm_packed_weights_bitwise(kat, M, N, K, epi):
+    """The packed copy of W only moves where each weight is read from: the
+    few-row product gives bit-identical results from it and from W."""
+    rng = np.random.default_rng(7 * M + N + K)
+    X = rng.standard_normal((M, K)).astype(np.float32)
+    W = (0.02 * rng.standard_normal((N, K))).astype(np.float32)
+    b = rng.standard_normal(N).astype(np.float32)
+    Y0 = rng.standard_normal((M, N)).astype(np.float32)
+    Yr = gemm(kat, X, W, b, M, N, K, epi, 0, Y0.copy())
+    Yp = gemm(kat, X, W, b, M, N, K, epi, 2, Y0.copy())
+    assert np.isfinite(Yr).all()
+    assert np.array_equal(Yr.view(np.uint32), Yp.view(np.uint32))
+
+
+@pytest.mark.parametrize("M,N,K", [
+    (8, 1024, 1024), (32, 1600, 6400), (5, 1280, 5120), (40, 768, 3072), (64, 2048, 2048),
+    (17, 1600, 1600), (128, 768, 3072),
+])
+def test_gemm_layernorm_in_split_sum(kat, M, N, K):
+    """The residual product whose split sum also forms the next LayerNorm
+    (the sum launch over whole rows): the residual stream within the float64
+    error bound, and the LayerNorm within 1e-5 of a float64 LayerNorm of the
+    float32 rows."""
+    rng = np.random.default_rng(13 * M + N + K)
+    X = rng.standard_normal((M, K)).astype(np.float32)
+    W = (0.02 * rng.standard_normal((N, K))).astype(np.float32)
+    b = rng.standard_normal(N).astype(np.float32)
+    Y0 = rng.standard_normal((M, N)).astype(np.float32)
+    lw = (1 + 0.1 * rng.standard_normal(N)).astype(np.float32)
+    lb = (0.1 * rng.standard_normal(N)).astype(np.float32)
+    Y = Y0.copy()
+    ln = np.zeros((M, N), np.float32)
+    splits = kat.kat_gemm_ln(fp(X), fp(W), fp(b), fp(Y), fp(lw), fp(lb), fp(ln), M, N, K)
+    assert splits > 1, kat.kat_error().decode()
+    acc = X.astype(np.float64) @ W.astype(np.float64).T
+    mag = np.abs(X.astype(np.float64)) @ np.abs(W.astype(np.float64)).T + np.abs(b) + np.abs(Y0)
+    assert np.all(np.abs(Y - ((Y0 + acc) + b)) <= (K + 4) * U * mag + TINY)
+    y = Y.astype(np.float64)
+    mu = y.mean(1, keepdims=True)
+    ref = (y - mu) / np.sqrt(((y - mu) ** 2).mean(1, keepdims=True) + 1e-5) * lw + lb
+    assert np.abs(ln - ref).max() < 1e-5
 
 
 @pytest.mark.parametrize("C", [4, 64, 768, 1024, 1600])

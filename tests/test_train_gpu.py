@@ -213,6 +213,8 @@ def test_training_steps_vs_oracle():
             assert err <= 2 * 1e-3 * (step + 1)
             assert np.mean(np.abs(p - ref.params) > 1e-5) < 1e-2
         # the updated weights serve the inference path of the same handle
+        # (its 16-row products read the packed weight copies, which the
+        # updates marked stale and the forward packs again)
         tok, _ = batch(cfg, 1, 16, 7)
         got = m.forward(tok, cngpt_amd.ALL)
     np.testing.assert_allclose(losses, ref_losses, rtol=1e-4)
