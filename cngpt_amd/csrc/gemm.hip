@@ -406,7 +406,10 @@ __global__ void __launch_bounds__(256) k_sk_fixup(GemmArgs a, int tiles_m, int t
     // float4 c4 = tid + 256 i of this workgroup's SK_RPW rows: row
     // rb * SK_RPW + c4 / 32, columns 4 (c4 % 32) ..
     constexpr int NI = SK_RPW * BN / 4 / 256;
-    f32x4 p[NI][SK_SEGS], old[NI];
+    // the residual and bias are loaded with the partials: a load after the
+    // first store would wait for that store too (the vector-memory counter
+    // counts both), one round trip per element
+    f32x4 p[NI][SK_SEGS], old[NI], bb[NI];
     int row[NI], col[NI];
     long yo[NI];
 #pragma unroll
@@ -425,6 +428,9 @@ __global__ void __launch_bounds__(256) k_sk_fixup(GemmArgs a, int tiles_m, int t
         if (EPI == EPI_RESID)
 #pragma unroll
             for (int e = 0; e < 4; e++) old[i][e] = a.Y[yo[i] + min(col[i] + e, a.N - 1)];
+        if (EPI != EPI_STORE)
+#pragma unroll
+            for (int e = 0; e < 4; e++) bb[i][e] = a.bias[min(col[i] + e, a.N - 1)];
     }
 #pragma unroll
     for (int i = 0; i < NI; i++) {
@@ -444,9 +450,9 @@ __global__ void __launch_bounds__(256) k_sk_fixup(GemmArgs a, int tiles_m, int t
             const int c = col[i] + e;
             if (c < a.N) {
                 float y = v[e];
-                if (EPI == EPI_BIAS) y += a.bias[c];
-                else if (EPI == EPI_BIAS_GELU) y = gelu_tanh(y + a.bias[c]);
-                else if (EPI == EPI_RESID) y = (old[i][e] + y) + a.bias[c];
+                if (EPI == EPI_BIAS) y += bb[i][e];
+                else if (EPI == EPI_BIAS_GELU) y = gelu_tanh(y + bb[i][e]);
+                else if (EPI == EPI_RESID) y = (old[i][e] + y) + bb[i][e];
                 a.Y[yo[i] + c] = y;
             }
         }
@@ -733,6 +739,15 @@ __global__ void __launch_bounds__(256) k_stream_reduce(GemmArgs a, int KS) {
     const long i = (long)blockIdx.x * 256 + threadIdx.x;
     const long MN = (long)a.M * a.N;
     if (i >= MN) return;
+    const int row = (int)(i / a.N), col = (int)(i % a.N);
+    long orow = a.seg ? (long)(row / a.seg) * a.seg_stride + row % a.seg : row;
+    orow += a.row_off + (a.row_off_dev ? *a.row_off_dev : 0);
+    float* y = a.Y + orow * a.ldy + col;
+    // the epilogue's bias and residual are loaded with the first partials
+    // (one memory round trip rather than one after the sum; the values and
+    // the arithmetic are store_out's)
+    const float b = EPI != EPI_STORE ? a.bias[col] : 0.f;
+    const float old = EPI == EPI_RESID ? *y : 0.f;
     // partials in batches of 8 loads in flight, summed in split order
     float v = 0.f;
     for (int q0 = 0; q0 < KS; q0 += 8) {
@@ -743,8 +758,7 @@ __global__ void __launch_bounds__(256) k_stream_reduce(GemmArgs a, int KS) {
         for (int j = 0; j < 8; j++)
             if (q0 + j < KS) v += p[j];
     }
-    const long roff = a.row_off + (a.row_off_dev ? *a.row_off_dev : 0);
-    store_out<EPI>(a, roff, (int)(i / a.N), (int)(i % a.N), v);
+    *y = epi_value<EPI>(v, b, old);
 }
 
 // The same sum for one row per workgroup (float4 columns tid + 256 i),
@@ -762,6 +776,18 @@ __global__ void __launch_bounds__(256) k_stream_reduce_ln(GemmArgs a, int KS) {
     const f32x4* p = (const f32x4*)(a.part + (long)r * a.N);
     float* yrow = a.Y + (long)r * a.ldy;
     f32x4 y[NCH], v[NCH];
+    // the residual row, bias and LayerNorm gains of this thread's columns
+    // are loaded with the first partials (one memory round trip, not three
+    // after the sum)
+    f32x4 yo[NCH], bb[NCH], lw[NCH], lb[NCH];
+#pragma unroll
+    for (int i = 0; i < NCH; i++) {
+        const int cc = min(tid + 256 * i, N4 - 1);
+        yo[i] = *(const f32x4*)(yrow + 4 * cc);
+        bb[i] = *(const f32x4*)(a.bias + 4 * cc);
+        lw[i] = *(const f32x4*)(a.ln_w + 4 * cc);
+        lb[i] = *(const f32x4*)(a.ln_b + 4 * cc);
+    }
 #pragma unroll
     for (int i = 0; i < NCH; i++) v[i] = f32x4{0.f, 0.f, 0.f, 0.f};
     // batches of 8 partials of every column of this thread in flight together
@@ -784,7 +810,7 @@ __global__ void __launch_bounds__(256) k_stream_reduce_ln(GemmArgs a, int KS) {
     for (int i = 0; i < NCH; i++) {
         const int c4 = tid + 256 * i, cc = min(c4, N4 - 1);
 #pragma unroll
-        for (int k = 0; k < 4; k++) y[i][k] = apply_epi<EPI>(v[i][k], a.bias, 4 * cc + k, yrow + 4 * cc + k);
+        for (int k = 0; k < 4; k++) y[i][k] = epi_value<EPI>(v[i][k], bb[i][k], yo[i][k]);
         if (c4 < N4) {
             *(f32x4*)(yrow + 4 * c4) = y[i];
             s += (y[i].x + y[i].y) + (y[i].z + y[i].w);
@@ -811,8 +837,7 @@ __global__ void __launch_bounds__(256) k_stream_reduce_ln(GemmArgs a, int KS) {
     for (int i = 0; i < NCH; i++) {
         const int c4 = tid + 256 * i;
         if (c4 < N4)
-            *(f32x4*)(orow + 4 * c4) = (y[i] - mean) * rstd * *(const f32x4*)(a.ln_w + 4 * c4) +
-                                       *(const f32x4*)(a.ln_b + 4 * c4);
+            *(f32x4*)(orow + 4 * c4) = (y[i] - mean) * rstd * lw[i] + lb[i];
     }
 }
 
