@@ -372,9 +372,9 @@ __global__ void __launch_bounds__(256) k_attn_dec(AttnDecArgs a) {
 
 // The same attention in one pass when the (sequence, head) pairs alone
 // occupy the CUs (batched decode, B * H >= 128): one workgroup per pair, its
-// NW wavefronts split keys 0..t into contiguous ranges and walk them with
-// PD passes of K/V loads in flight (a pass: 64 / (hs/4) keys, hs/4 lanes
-// per key, one float4 each); each lane group keeps a running max, sum and
+// NW wavefronts split keys 0..t into contiguous ranges and walk them in
+// rounds of PD passes of K/V loads issued together (a pass: 64 / (hs/4)
+// keys, hs/4 lanes per key, one float4 each); each lane group keeps a running max, sum and
 // o (online softmax in base 2, q pre-scaled by scale * log2(e)); the groups
 // of a wavefront merge by shuffles, the wavefronts through LDS in order,
 // and the workgroup writes the normalised row: no partials, no merge
@@ -398,6 +398,21 @@ __global__ void __launch_bounds__(256) k_attn_dec(AttnDecArgs a) {
 constexpr int DEC1_MIN_PAIRS = 128;
 constexpr int DEC1_SPLIT_BELOW = 256;
 typedef unsigned long long u64;
+// Sum over each group of G consecutive lanes (G a power of two <= 64),
+// every lane of a group receiving it: the xor butterfly over 1, 2, 4, ...
+// (the same additions in the same order), within 16 lanes by DPP row
+// operations instead of LDS permutes.
+template <int G>
+__device__ __forceinline__ float lane_group_sum(float d) {
+    if (G >= 2) d += CNGPT_DPP(d, 0xB1);   // quad_perm [1,0,3,2]: lane ^ 1
+    if (G >= 4) d += CNGPT_DPP(d, 0x4E);   // quad_perm [2,3,0,1]: lane ^ 2
+    if (G >= 8) d += CNGPT_DPP(d, 0x141);  // row_half_mirror: the other quad of 8
+    if (G >= 16) d += CNGPT_DPP(d, 0x140); // row_mirror: the other half of 16
+    if (G >= 32) d += __shfl_xor(d, 16, 64);
+    if (G >= 64) d += __shfl_xor(d, 32, 64);
+    return d;
+}
+
 template <int HS, int NW, int PD, int SPL>
 __global__ void __launch_bounds__(NW * 64) k_attn_dec1(AttnDecArgs a, float* __restrict__ out,
                                                        long ldo) {
@@ -421,37 +436,39 @@ __global__ void __launch_bounds__(NW * 64) k_attn_dec1(AttnDecArgs a, float* __r
     const f32x4 q =
         *(const f32x4*)(base + (long)t * C3 + d4 * 4) * (a.scale * 1.4426950408889634f);
 
-    // keys past the range re-read its last one (an empty range loads nothing)
-    f32x4 kr[PD], vr[PD];
-    auto load = [&](int p, int slot) {
-        const float* rp = base + (long)min(k0 + p * KPW + kl, k1 - 1) * C3 + d4 * 4;
-        kr[slot] = *(const f32x4*)(rp + a.C);
-        vr[slot] = *(const f32x4*)(rp + 2 * a.C);
-    };
-#pragma unroll
-    for (int j = 0; j < PD; j++)
-        if (j < npass) load(j, j);
+    // Rounds of PD passes: every load of a round is issued first (keys
+    // past the range re-read its last one; an empty range runs no round),
+    // then the passes are consumed in order. No load register is carried
+    // from one loop trip to the next: a ring carried that way got a wait
+    // for every load in flight after each pass, one memory latency per pass.
     float m = -INFINITY, l = 0.f;
     f32x4 o = {0.f, 0.f, 0.f, 0.f};
     for (int p0 = 0; p0 < npass; p0 += PD) {
+        f32x4 kr[PD], vr[PD];
 #pragma unroll
         for (int j = 0; j < PD; j++) {
-            const int p = p0 + j;
-            if (p < npass) {
-                const f32x4 kk = kr[j], vv = vr[j];
-                if (p + PD < npass) load(p + PD, j);
-                float d = dot4(q, kk);
+            const float* rp = base + (long)min(k0 + (p0 + j) * KPW + kl, k1 - 1) * C3 + d4 * 4;
+            kr[j] = *(const f32x4*)(rp + a.C);
+            vr[j] = *(const f32x4*)(rp + 2 * a.C);
+        }
+        // all of them before the first use (the scheduler would otherwise
+        // spread them out to save registers)
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                for (int sh = 1; sh < LPK; sh <<= 1) d += __shfl_xor(d, sh, 64);
-                if (k0 + p * KPW + kl < k1) {
-                    const float mn = fmaxf(m, d);
-                    const float al = __builtin_amdgcn_exp2f(m - mn);
-                    const float e = __builtin_amdgcn_exp2f(d - mn);
-                    l = l * al + e;
-                    o = o * al + e * vv;
-                    m = mn;
-                }
-            }
+        for (int j = 0; j < PD; j++) {
+            // formed for every lane and kept for keys in the range (a branch
+            // around the use would draw the V load into it, behind a wait
+            // for every load of the round)
+            const float d = lane_group_sum<LPK>(dot4(q, kr[j]));
+            const bool in = k0 + (p0 + j) * KPW + kl < k1;
+            const float mn = fmaxf(m, d);
+            const float al = __builtin_amdgcn_exp2f(m - mn);
+            const float e = __builtin_amdgcn_exp2f(d - mn);
+            const float ln = l * al + e;
+            const f32x4 on = o * al + e * vr[j];
+            l = in ? ln : l;
+            o = in ? on : o;
+            m = in ? mn : m;
         }
     }
     // merge the key groups of a wavefront (a group with no key has m = -inf)
