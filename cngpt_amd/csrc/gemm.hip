@@ -593,10 +593,18 @@ constexpr int ST_MAX_M = 128;  // rows of the largest row-block count (MB = 8)
 constexpr int st_kc(int MB) { return MB > 4 ? 64 : 128; }
 constexpr int st_mb(int M) { return M <= 16 ? 1 : M <= 32 ? 2 : M <= 48 ? 3 : M <= 64 ? 4 : 8; }
 
-template <int EPI, int MB, bool PK>
+// WPB > 1 (at most 32 rows): WPB wavefronts share each 16-column block,
+// the workgroup owns 16 * ST_NW / WPB columns, the input chunk is WPB times
+// longer and wavefront phase ph takes its steps ph, ph + WPB, ... (in
+// packed weights the block's steps stay contiguous across the phases); at
+// the end the phases' sums are added in phase order through LDS. Enough
+// column tiles then fill the CUs without a K split, so no partial tiles and
+// no sum launch.
+template <int EPI, int MB, bool PK, int WPB>
 __global__ void __launch_bounds__(ST_NW * 64) k_stream(GemmArgs a, int tiles_n, int KR, int KS) {
-    constexpr int ST_KC = st_kc(MB);     // k per input chunk
-    constexpr int ST_PF = ST_KC / 16;    // weight steps in flight = steps per chunk (<= 8)
+    constexpr int CBW = ST_NW / WPB;           // column blocks per workgroup
+    constexpr int ST_KC = st_kc(MB) * WPB;     // k per input chunk
+    constexpr int ST_PF = ST_KC / 16 / WPB;    // weight steps in flight = steps per chunk per wavefront (<= 8)
     constexpr int ST_GPR = ST_KC / 4;    // input granules (16 bytes) per row of a chunk
     static_assert(ST_GPR >= 16 && ST_PF <= 8, "swizzle over 16 rows; waits of at most 7 + XI");
     constexpr int R = 16 * MB;                       // rows held (M <= R)
@@ -610,7 +618,8 @@ __global__ void __launch_bounds__(ST_NW * 64) k_stream(GemmArgs a, int tiles_n, 
     const int K = a.K, M = a.M, N = a.N;
     const int kb = ks * KR, ke = min(K, kb + KR);
     const int nchunks = (ke - kb + ST_KC - 1) / ST_KC;
-    const int col = tn * ST_NT + 16 * wave + lc;
+    const int blk = wave % CBW, ph = wave / CBW;
+    const int col = tn * 16 * CBW + 16 * blk + lc;
     const float* wrow = a.W + (long)min(col, N - 1) * K + g4;
     // packed: column block col / 16 (the last one for columns past N), its
     // k steps of 256 floats each, this lane's 16 bytes at 4 * lane
@@ -637,14 +646,15 @@ __global__ void __launch_bounds__(ST_NW * 64) k_stream(GemmArgs a, int tiles_n, 
         for (int i = 0; i < XI; i++)
             lds_dma16(xsrc[i] + min(k0 + xslot[i], K - 4), &xd[(i * ST_NW + wave) * 256]);
     };
-    // weight step s (k = kb + 16 s + g4 .. +3 of this lane's column; steps
-    // past the range re-read K - 4 and are zeroed at use) into ring slot
-    // s % ST_PF
+    // this wavefront's weight step s (k = kb + 16 (s WPB + ph) + g4 .. +3
+    // of this lane's column; steps past the range re-read K - 4 and are
+    // zeroed at use) into ring slot s % ST_PF
     auto issue_w = [&](int s) {
+        const int st = s * WPB + ph;
         if (PK)
-            lds_dma16(wpk + (long)min((kb >> 4) + s, KQ - 1) * 256, &ws[wave][s % ST_PF][0]);
+            lds_dma16(wpk + (long)min((kb >> 4) + st, KQ - 1) * 256, &ws[wave][s % ST_PF][0]);
         else
-            lds_dma16(wrow + min(kb + 16 * s, K - 4 - g4), &ws[wave][s % ST_PF][0]);
+            lds_dma16(wrow + min(kb + 16 * st, K - 4 - g4), &ws[wave][s % ST_PF][0]);
     };
 
     f32x4 acc[MB];
@@ -683,12 +693,12 @@ __global__ void __launch_bounds__(ST_NW * 64) k_stream(GemmArgs a, int tiles_n, 
                 wait_vmcnt<ST_PF - 1 + XI>();
             }
             asm volatile("" ::: "memory");
-            const bool kok = kb + 16 * s + g4 < ke;
+            const bool kok = kb + 16 * (s * WPB + ph) + g4 < ke;
             const f32x4 w = *(const f32x4*)&ws[wave][j][4 * lane];
             f32x4 xf[MB];
 #pragma unroll
             for (int mb = 0; mb < MB; mb++) {
-                const int r = 16 * mb + lc, q = 4 * j + (lane >> 4);
+                const int r = 16 * mb + lc, q = 4 * (j * WPB + ph) + (lane >> 4);
                 xf[mb] = *(const f32x4*)&xb[r * ST_KC + 4 * (q ^ (r & 15))];
             }
 #pragma unroll
@@ -710,6 +720,24 @@ __global__ void __launch_bounds__(ST_NW * 64) k_stream(GemmArgs a, int tiles_n, 
     for (int j = 0; j < ST_PF; j++) issue_w(j);
     for (int c = 0; c + 1 < nchunks; c++) chunk(c, std::false_type{});
     chunk(nchunks - 1, std::true_type{});
+
+    if constexpr (WPB > 1) {
+        // phases 1.. hand their sums to phase 0 through the (now unused)
+        // input buffers, which adds them in phase order
+        __syncthreads();
+        float* red = &xs[0][0];
+        if (ph > 0)
+#pragma unroll
+            for (int mb = 0; mb < MB; mb++)
+                *(f32x4*)&red[(((ph - 1) * CBW + blk) * MB + mb) * 256 + 4 * lane] = acc[mb];
+        __syncthreads();
+        if (ph > 0) return;
+#pragma unroll
+        for (int p = 1; p < WPB; p++)
+#pragma unroll
+            for (int mb = 0; mb < MB; mb++)
+                acc[mb] += *(const f32x4*)&red[(((p - 1) * CBW + blk) * MB + mb) * 256 + 4 * lane];
+    }
 
     // acc[mb][r]: row 16 mb + 4 (lane / 16) + r, column col
     if (col >= N) return;
@@ -867,7 +895,21 @@ hipError_t ln_after(const GemmArgs& a, hipStream_t s) {
 // Split K until the column tiles times the splits reach two workgroups per
 // CU (the partials must fit a.part_cap floats; ranges are whole chunks):
 // returns the splits, *KR the k per split.
+// Wavefronts per 16-column block: the narrowest tiles (up to 4 per block
+// at 16 rows, 2 at 32: the longer input chunks' LDS) that make at least 192
+// column tiles, which then run without a K split; else 1, split as below.
+int stream_wpb(const GemmArgs& a) {
+    const int MB = st_mb(a.M);
+    for (int wpb = 1; wpb <= (MB == 1 ? 4 : MB == 2 ? 2 : 1); wpb *= 2)
+        if ((a.N + 16 * ST_NW / wpb - 1) / (16 * ST_NW / wpb) >= 192) return wpb;
+    return 1;
+}
+
 int stream_splits(const GemmArgs& a, int* KR) {
+    if (const int wpb = stream_wpb(a); wpb > 1) {
+        *KR = (a.K + 16 * 8 * wpb - 1) / (16 * 8 * wpb) * (16 * 8 * wpb);
+        return 1;
+    }
     const int kc = st_kc(st_mb(a.M));
     const int tiles_n = (a.N + ST_NT - 1) / ST_NT;
     const int kchunks = (a.K + kc - 1) / kc;
@@ -884,15 +926,25 @@ int stream_splits(const GemmArgs& a, int* KR) {
     return (a.K + *KR - 1) / *KR;
 }
 
+template <int EPI, int MB, int WPB>
+void stream_launch(const GemmArgs& a, int tiles_n, int KR, int KS, hipStream_t s) {
+    if (a.Wp)
+        k_stream<EPI, MB, true, WPB><<<tiles_n * KS, ST_NW * 64, 0, s>>>(a, tiles_n, KR, KS);
+    else
+        k_stream<EPI, MB, false, WPB><<<tiles_n * KS, ST_NW * 64, 0, s>>>(a, tiles_n, KR, KS);
+}
+
 template <int EPI, int MB>
 hipError_t stream_mb(const GemmArgs& a, hipStream_t s) {
-    const int tiles_n = (a.N + ST_NT - 1) / ST_NT;
+    const int wpb = stream_wpb(a);
+    const int tiles_n = (a.N + 16 * ST_NW / wpb - 1) / (16 * ST_NW / wpb);
     int KR;
     const int KS = stream_splits(a, &KR);
-    if (a.Wp)
-        k_stream<EPI, MB, true><<<tiles_n * KS, ST_NW * 64, 0, s>>>(a, tiles_n, KR, KS);
-    else
-        k_stream<EPI, MB, false><<<tiles_n * KS, ST_NW * 64, 0, s>>>(a, tiles_n, KR, KS);
+    if constexpr (MB <= 2) {
+        if (wpb == 2) stream_launch<EPI, MB, 2>(a, tiles_n, KR, KS, s);
+        if (MB == 1 && wpb == 4) stream_launch<EPI, MB, MB == 1 ? 4 : 2>(a, tiles_n, KR, KS, s);
+    }
+    if (wpb == 1) stream_launch<EPI, MB, 1>(a, tiles_n, KR, KS, s);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     return KS == 1 ? ln_after(a, s) : reduce_splits<EPI>(a, KS, s);

@@ -248,6 +248,11 @@ def test_softmax_error_bound_dense_grid(kat, kind):
     (0, 1100, 4000, 1600, 3), # stream-K: 9 x 32 ragged tiles, residual
     (0, 37, 100, 3072, 3),    # weight-streaming product, split over K
     (0, 5, 2304, 768, 1),     # weight-streaming, QKV width
+    (0, 8, 3072, 1024, 1),    # weight-streaming, four wavefronts per column block, no K split
+    (0, 13, 4100, 1000, 2),   # two phases per block, ragged columns and K, GELU
+    (0, 30, 6400, 1600, 3),   # two phases per block at 30 rows, residual
+    (0, 16, 3200, 36, 1),     # four phases per block, K = 36 (one step, three phases empty)
+    (2, 8, 4096, 1024, 2),    # packed weights, four phases per block
     (2, 37, 100, 3072, 3),    # weight-streaming from packed weights, split over K
     (2, 20, 771, 1600, 2),    # packed weights, ragged last column block, GELU
     (2, 100, 333, 36, 1),     # packed, K = 36 (zero-padded last step), 128-row tiles
@@ -287,7 +292,7 @@ def test_gemm_error_bound_float64(kat, path, M, N, K, epi):
 
 @pytest.mark.parametrize("M,N,K,epi", [
     (3, 2304, 768, 1), (24, 3200, 800, 2), (40, 1600, 6400, 3), (64, 50257, 64, 0),
-    (100, 333, 36, 3), (128, 771, 1280, 1),
+    (100, 333, 36, 3), (128, 771, 1280, 1), (8, 3072, 1024, 1), (32, 6400, 1600, 2),
 ])
 def test_gemm_packed_weights_bitwise(kat, M, N, K, epi):
     """The packed copy of W only moves where each weight is read from: the
