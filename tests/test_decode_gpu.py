@@ -352,3 +352,26 @@ def test_generate_sampling_gpt2_small_rand_stream():
             say(f"  diverged at a CDF boundary at token {i}")
             break
     say(f"generate sampled small: {n} tokens")
+
+
+def test_packed_weights_bit_identical_to_row_major(monkeypatch):
+    """A handle made with CNGPT_HIP_PACK=0 streams the row-major weights in
+    its few-row products instead of their packed copy: the same values in
+    the same order, so prefill and every batched decode step agree bit for
+    bit (B=6 and a 40-row prompt put every product on the few-row kernel)."""
+    cfg = cngpt_amd.Config(2, 4, 256, 1000, 128)
+    params = randomize(cfg, cngpt_amd.init_weights(cfg, 5), 6)
+    prompt = oracle.lcg_tokens(6 * 40, cfg.vocab_size).reshape(6, 40) % cfg.vocab_size
+    runs = []
+    for pack in ("1", "0"):
+        monkeypatch.setenv("CNGPT_HIP_PACK", pack)
+        with cngpt_amd.Model(cfg, params) as m:
+            got = [m.forward(prompt[:1, :40], cngpt_amd.ALL), m.decode_begin(prompt, capacity=60)]
+            toks = got[-1].argmax(-1).astype(np.int32)
+            for _ in range(12):
+                got.append(m.decode_step(toks))
+                toks = got[-1].argmax(-1).astype(np.int32)
+        runs.append(got)
+    for a, b in zip(*runs):
+        assert np.isfinite(a).all()
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
