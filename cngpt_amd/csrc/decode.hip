@@ -386,15 +386,15 @@ __global__ void __launch_bounds__(256) k_attn_dec(AttnDecArgs a) {
 //
 // With fewer pairs than CUs (SPL = 2: B * H < 256, e.g. GPT-2 medium B=8's
 // 128 pairs, whose workgroups leave half the CUs idle) the keys of a pair
-// are split over two workgroups. Each writes its unnormalised (m, l, o) as
-// tagged 64-bit words (the tag in the high half, agent-scope atomics: the
-// L2 of one XCD is not coherent with another's), and the second to count
-// itself in on the pair's counter merges both halves, half 0 first whatever
-// the arrival order (reproducible), and writes the row. Tags come from the
+// are split over two workgroups. Each counts itself in on the pair's
+// counter; the first in writes its unnormalised (m, l, o) as tagged 64-bit
+// words (the tag in the high half, agent-scope atomics: the L2 of one XCD
+// is not coherent with another's) and leaves, and the second in polls them,
+// merges both halves, half 0 first whatever the arrival order
+// (reproducible), writes the row and clears the words. Tags come from the
 // counter (each use adds 2), so both halves of a use agree on theirs and no
-// use can match an earlier use's words; the first to count has written its
-// words before counting, so the second never waits on a workgroup that has
-// not run.
+// use can match an earlier use's words; the second waits only on a
+// workgroup that has already counted itself in, i.e. is running.
 constexpr int DEC1_MIN_PAIRS = 128;
 constexpr int DEC1_SPLIT_BELOW = 256;
 typedef unsigned long long u64;
@@ -510,26 +510,27 @@ __global__ void __launch_bounds__(NW * 64) k_attn_dec1(AttnDecArgs a, float* __r
     // words of half s of this pair: m, l, o[HS]
     constexpr int NWD = HS + 2;
     unsigned* cnt = a.tag_cnt + bh;
-    const unsigned tag = (unsigned)__builtin_amdgcn_readfirstlane(
-                             (int)__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) /
-                             2u + 1u;
-    auto word = [&](float v) { return ((u64)tag << 32) | (u64)__float_as_uint(v); };
-    u64* mine = a.tag_part + ((long)bh * 2 + half) * NWD;
-    if (lane < LPK)
-#pragma unroll
-        for (int c = 0; c < 4; c++)
-            __hip_atomic_store(mine + 2 + 4 * lane + c, word(O[c]), __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-    if (lane == 0) {
-        __hip_atomic_store(mine, word(M), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(mine + 1, word(L), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    // the words are written before the count
-    wait_vmcnt<0>();
+    // count in first: one round trip, after which the first in publishes
+    // its words and leaves, and the second in (which has its own half in
+    // registers) merges without writing or waiting for any store
     unsigned old = 0;
     if (lane == 0) old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     old = (unsigned)__builtin_amdgcn_readfirstlane((int)old);
-    if ((old & 1u) == 0) return;  // first in: the other half merges
+    const unsigned tag = old / 2u + 1u;
+    auto word = [&](float v) { return ((u64)tag << 32) | (u64)__float_as_uint(v); };
+    if ((old & 1u) == 0) {
+        u64* mine = a.tag_part + ((long)bh * 2 + half) * NWD;
+        if (lane < LPK)
+#pragma unroll
+            for (int c = 0; c < 4; c++)
+                __hip_atomic_store(mine + 2 + 4 * lane + c, word(O[c]), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        if (lane == 0) {
+            __hip_atomic_store(mine, word(M), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(mine + 1, word(L), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        return;
+    }
     // second in: the other half's words, until each carries this use's tag
     const u64* other = a.tag_part + ((long)bh * 2 + (1 - half)) * NWD;
     u64 w[6];
@@ -549,8 +550,8 @@ __global__ void __launch_bounds__(NW * 64) k_attn_dec1(AttnDecArgs a, float* __r
     };
     fetch_other();
     bool ok = current();
-    // the other half counted itself in after its words' stores completed, so
-    // they become visible within a few round trips; the limit only guards
+    // the other half counted itself in first and is writing its words, so
+    // they become visible within a round trip or two; the limit only guards
     // against a fault, and then the row is poisoned (NaN) rather than hung
     for (long it = 0; __builtin_amdgcn_ballot_w64(!ok) != 0 && it < (1L << 20); it++) {
         __builtin_amdgcn_s_sleep(1);
@@ -575,6 +576,17 @@ __global__ void __launch_bounds__(NW * 64) k_attn_dec1(AttnDecArgs a, float* __r
     if (lane < LPK)
         *(f32x4*)(out + (long)b * ldo + h * HS + lane * 4) =
             all_ok ? Os * (1.0f / Ls) : f32x4{NAN, NAN, NAN, NAN};
+    // the words read are cleared, so that a slot never keeps an old use's
+    // words (tags repeat after 2^31 uses of a pair)
+    u64* done = const_cast<u64*>(other);
+    if (lane < LPK)
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+            __hip_atomic_store(done + 2 + 4 * lane + c, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (lane == 0) {
+        __hip_atomic_store(done, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(done + 1, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 }
 
 // Rows of merged attention for the consumers that are not k_dgemv (M > 8).
