@@ -122,8 +122,9 @@ struct cngpt_hip_ctx {
     // Packed copies (launch_pack_w) of the weight matrices, after the layer
     // table in the same allocation, read by the few-row products.
     // CNGPT_HIP_PACK=0 in the environment at create time leaves them out.
-    // A training view may change the parameters: it marks the copies stale,
-    // and the next forward or decode entry point packs them again.
+    // A training update changes the parameters in place: it marks the
+    // copies stale, and the next forward or decode entry point packs them
+    // again.
     struct Packed {
         const float* W;
         float* Wp;
@@ -1183,8 +1184,11 @@ int ctx_view(cngpt_hip_ctx* h, CtxView* v) {
     v->lnf_w = h->lnf_w;
     v->lnf_b = h->lnf_b;
     v->layers = h->layers.data();
-    h->packed_fresh = false;  // the view can write the parameters
     return 0;
+}
+
+void ctx_params_written(cngpt_hip_ctx* h) {
+    if (h) h->packed_fresh = false;
 }
 
 int ctx_fail(const char* fmt, ...) {

@@ -19,5 +19,8 @@ struct CtxView {
 
 // Fills v from h; -1 (message set) when h is null or holds no parameters.
 __attribute__((visibility("hidden"))) int ctx_view(cngpt_hip_ctx* h, CtxView* v);
+// Marks the packed weight copies stale after the parameters were updated
+// in place (the next forward or decode entry point packs them again).
+__attribute__((visibility("hidden"))) void ctx_params_written(cngpt_hip_ctx* h);
 // Sets the message cngpt_hip_last_error() returns; returns -1.
 __attribute__((visibility("hidden"))) int ctx_fail(const char* fmt, ...);

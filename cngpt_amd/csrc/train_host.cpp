@@ -479,6 +479,7 @@ int cngpt_hip_train_adamw(cngpt_hip_train* t, float lr, float beta1, float beta2
     TRY(launch_adamw(v.params, t->grads, t->m, t->v, t->decay, t->n_params, t->nparts, t->norm,
                      t->coef, lr, beta1, beta2, eps, weight_decay, grad_clip, bc1, bc2,
                      v.stream));
+    ctx_params_written(t->h);  // the packed weight copies no longer match
     if (grad_norm) {
         TRY(hipMemcpyAsync(grad_norm, t->norm, sizeof(float), hipMemcpyDeviceToHost, v.stream));
         TRY(hipStreamSynchronize(v.stream));
