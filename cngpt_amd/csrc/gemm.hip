@@ -940,9 +940,12 @@ hipError_t stream_mb(const GemmArgs& a, hipStream_t s) {
     const int tiles_n = (a.N + 16 * ST_NW / wpb - 1) / (16 * ST_NW / wpb);
     int KR;
     const int KS = stream_splits(a, &KR);
+    // (stream_wpb gives 4 for one row block only, 2 for at most two)
+    if constexpr (MB == 1) {
+        if (wpb == 4) stream_launch<EPI, MB, 4>(a, tiles_n, KR, KS, s);
+    }
     if constexpr (MB <= 2) {
         if (wpb == 2) stream_launch<EPI, MB, 2>(a, tiles_n, KR, KS, s);
-        if (MB == 1 && wpb == 4) stream_launch<EPI, MB, MB == 1 ? 4 : 2>(a, tiles_n, KR, KS, s);
     }
     if (wpb == 1) stream_launch<EPI, MB, 1>(a, tiles_n, KR, KS, s);
     hipError_t e = hipGetLastError();
