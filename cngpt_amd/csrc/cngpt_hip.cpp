@@ -862,9 +862,6 @@ long params_of(const cngpt_hip_config* c) {
     return V * C + T * C + L * (12 * C * C + 13 * C) + 2 * C;  // model.c:20-48
 }
 
-// Make h->d_params hold the parameters of shape cfg: reuse the allocation
-// when the shape is unchanged, else free it (and the activations, which
-// depend on the shape) and allocate anew.
 // Bytes of the packed weight copies: the token embedding (the lm_head's
 // weights) and each layer's four matrices.
 size_t packed_bytes(const cngpt_hip_config* cfg) {
@@ -876,16 +873,21 @@ size_t packed_bytes(const cngpt_hip_config* cfg) {
     return align_up(packed_w_floats(cfg->vocab_size, C) * sizeof(float)) + layer * cfg->n_layer;
 }
 
-// Packs the weight matrices again when a training view may have changed
-// them (kernels on the handle's stream, ordered before what follows).
+// Packs the weight matrices (again, after an AdamW update marked them
+// stale: ctx_params_written) in kernels on the handle's stream, ordered
+// before what follows.
 int fresh_packed(cngpt_hip_ctx* h) {
     if (!h->use_packed || h->packed_fresh) return 0;
     HIP_TRY(hipSetDevice(h->device));
-    for (const cngpt_hip_ctx::Packed& p : h->packs) HIP_TRY(launch_pack_w(p.W, p.Wp, p.N, p.K, h->stream));
+    for (const cngpt_hip_ctx::Packed& p : h->packs)
+        HIP_TRY(launch_pack_w(p.W, p.Wp, p.N, p.K, h->stream));
     h->packed_fresh = true;
     return 0;
 }
 
+// Make h->d_params hold the parameters of shape cfg: reuse the allocation
+// when the shape is unchanged, else free it (and the activations, which
+// depend on the shape) and allocate anew.
 int params_prepare(cngpt_hip_ctx* h, const cngpt_hip_config* cfg) {
     HIP_TRY(hipSetDevice(h->device));
     if (h->d_params && memcmp(&h->cfg, cfg, sizeof(*cfg)) == 0) return 0;

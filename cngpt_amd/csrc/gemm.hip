@@ -28,9 +28,12 @@
 // step k+1 while step k is multiplied, then into a padded LDS double buffer;
 // the last step zero-fills past K.
 //
-// k_stream: M <= 64 rows, weights streamed once, input rows through LDS,
-// K split over workgroups when the column tiles are few. Products over
-// M <= 2 rows (single-sequence decode) are k_dgemv in decode.hip.
+// k_stream: up to 128 rows (64 < M <= 128 when 128 x 128 tiles would be
+// too few), weights streamed once (from their packed copy when the caller
+// has one), input rows through LDS, K split over workgroups when the column
+// tiles are few, or over the wavefronts of narrower tiles up to 32 rows.
+// Products over M <= 2 rows (single-sequence decode) are k_dgemv in
+// decode.hip.
 #include <algorithm>
 #include <cstdlib>
 #include <type_traits>
@@ -553,11 +556,12 @@ __global__ void __launch_bounds__(NTHREADS, OCC) k_gemm(GemmArgs a, int tiles_m,
 
 // ---------------------------------------------------------------- skinny
 
-// k_stream: M <= 64 rows (batched decode, last-position passes of larger
-// batches, short prefills). Weight-bandwidth bound: every weight is used by
-// M rows only (at M = 32, 2 * 32 FLOP per 4-byte weight = 16 FLOP/B, near
-// the fp32 ridge of 157.3 / 8 = 19.7), so each weight is read once and the
-// input rows are shared out of LDS. A workgroup of ST_NW wavefronts owns
+// k_stream: up to 128 rows (batched decode, last-position passes of larger
+// batches, short prefills). Every weight is used by M rows only (at M = 32,
+// 2 * 32 FLOP per 4-byte weight = 16 FLOP/B, near the fp32 ridge of
+// 157.3 / 8 = 19.7; at decode sizes a launch's fixed cost, not its bytes,
+// dominates: cache-resident weights gain 5-10 %), so each weight is read
+// once and the input rows are shared out of LDS. A workgroup of ST_NW wavefronts owns
 // ST_NT = 16 * ST_NW output columns over a K range [kb, ke), in steps of 16
 // k: for its 16 columns a wavefront's lane l holds column l % 16, k = 4 (l /
 // 16) .. +3 of a step, and the input rows of the range pass through LDS in
@@ -604,7 +608,8 @@ template <int EPI, int MB, bool PK, int WPB>
 __global__ void __launch_bounds__(ST_NW * 64) k_stream(GemmArgs a, int tiles_n, int KR, int KS) {
     constexpr int CBW = ST_NW / WPB;           // column blocks per workgroup
     constexpr int ST_KC = st_kc(MB) * WPB;     // k per input chunk
-    constexpr int ST_PF = ST_KC / 16 / WPB;    // weight steps in flight = steps per chunk per wavefront (<= 8)
+    constexpr int ST_PF = ST_KC / 16 / WPB;    // weight steps in flight = steps per
+                                               // chunk per wavefront (<= 8)
     constexpr int ST_GPR = ST_KC / 4;    // input granules (16 bytes) per row of a chunk
     static_assert(ST_GPR >= 16 && ST_PF <= 8, "swizzle over 16 rows; waits of at most 7 + XI");
     constexpr int R = 16 * MB;                       // rows held (M <= R)
@@ -624,7 +629,8 @@ __global__ void __launch_bounds__(ST_NW * 64) k_stream(GemmArgs a, int tiles_n, 
     // packed: column block col / 16 (the last one for columns past N), its
     // k steps of 256 floats each, this lane's 16 bytes at 4 * lane
     const int KQ = (K + 15) >> 4;
-    const float* wpk = PK ? a.Wp + (long)min(col >> 4, (N - 1) >> 4) * KQ * 256 + 4 * lane : nullptr;
+    const float* wpk =
+        PK ? a.Wp + (long)min(col >> 4, (N - 1) >> 4) * KQ * 256 + 4 * lane : nullptr;
 
     // input chunk c into buffer b: granule g = (i * ST_NW + wave) * 64 +
     // lane of the chunk sits at row g / ST_GPR, slot g % ST_GPR and holds k
@@ -836,7 +842,7 @@ __global__ void __launch_bounds__(256) k_stream_reduce_ln(GemmArgs a, int KS) {
     float s = 0.f;
 #pragma unroll
     for (int i = 0; i < NCH; i++) {
-        const int c4 = tid + 256 * i, cc = min(c4, N4 - 1);
+        const int c4 = tid + 256 * i;
 #pragma unroll
         for (int k = 0; k < 4; k++) y[i][k] = epi_value<EPI>(v[i][k], bb[i][k], yo[i][k]);
         if (c4 < N4) {
