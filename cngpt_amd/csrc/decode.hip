@@ -374,8 +374,9 @@ __global__ void __launch_bounds__(256) k_attn_dec(AttnDecArgs a) {
 // occupy the CUs (batched decode, B * H >= 128): one workgroup per pair, its
 // NW wavefronts split keys 0..t into contiguous ranges and walk them in
 // rounds of PD passes of K/V loads issued together (a pass: 64 / (hs/4)
-// keys, hs/4 lanes per key, one float4 each); each lane group keeps a running max, sum and
-// o (online softmax in base 2, q pre-scaled by scale * log2(e)); the groups
+// keys, hs/4 lanes per key, one float4 each); each lane group keeps a
+// running max, sum and o (online softmax in base 2, q pre-scaled by
+// scale * log2(e)); the groups
 // of a wavefront merge by shuffles, the wavefronts through LDS in order,
 // and the workgroup writes the normalised row: no partials, no merge
 // launch. Measured against the split form + merge (probe, caches streamed
