@@ -205,15 +205,15 @@ def load_weights(path: str) -> tuple[Config, np.ndarray]:
     with open(path, "rb") as f:
         hdr = f.read(28)
     if len(hdr) < 28:
-        raise CngptError(f"{path}: short header")
+        raise CngptError(f"{path}: file ends inside its 28-byte header")
     magic, _ver, L, H, C, V, T = struct.unpack("<7i", hdr)
     if magic != MAGIC:
-        raise CngptError(f"{path}: bad magic 0x{magic & 0xFFFFFFFF:X}")
+        raise CngptError(f"{path}: not a cngpt weight file (first word 0x{magic & 0xFFFFFFFF:X})")
     cfg = Config(L, H, C, V, T)
     n = num_params(cfg)
     p = np.memmap(path, dtype=np.float32, mode="r", offset=28)
     if p.size < n:
-        raise CngptError(f"{path}: short param data ({p.size} < {n})")
+        raise CngptError(f"{path}: file ends before its parameters ({p.size} of {n} floats)")
     return cfg, np.ascontiguousarray(p[:n])
 
 

@@ -73,12 +73,30 @@ size_t align_up(size_t n) { return (n + ALIGN - 1) & ~(ALIGN - 1); }
 // hipGetSymbolAddress, once per device, in cngpt_hip_create.
 constexpr long SCRATCH_FLOATS = 32l << 20;
 __device__ __align__(256) float scratch[SCRATCH_FLOATS];
+// The first SCRATCH_TAG_FLOATS of the scratch hold the tagged words and
+// per-pair counters of the split decode attention (head sizes up to
+// SCRATCH_TAG_HS, attn_dec1_split_pairs() pairs), at fixed offsets: they
+// keep their state from one call to the next (counters grow, words are
+// cleared by the attention after use), zeroed once when the device's
+// address is looked up.
+constexpr int SCRATCH_TAG_HS = 128;
+long scratch_tag_floats() {
+    const long words = (long)attn_dec1_tag_words(attn_dec1_split_pairs(), SCRATCH_TAG_HS);
+    return (2 * words + attn_dec1_split_pairs() + 63) / 64 * 64;
+}
 
 constexpr int MAX_DEVICES = 64;
 std::mutex g_scratch_mu;
 float* g_scratch[MAX_DEVICES];  // device address of `scratch`, per device
 
-// With `device` current: look up and keep its address of the scratch array.
+// Zeroes n ints with a kernel (a memset node in a captured graph is avoided).
+__global__ void k_zero_i32(int* p, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0;
+}
+
+// With `device` current: look up and keep its address of the scratch array,
+// and zero its tag region.
 int scratch_setup(int device) {
     if (device < 0 || device >= MAX_DEVICES) return 0;  // the no-alloc entry refuses such devices
     std::lock_guard<std::mutex> lock(g_scratch_mu);
@@ -89,6 +107,13 @@ int scratch_setup(int device) {
         (void)hipGetLastError();
         return fail("scratch address on device %d: %s", device, hipGetErrorString(e));
     }
+    const int n = (int)scratch_tag_floats();
+    k_zero_i32<<<(n + 255) / 256, 256, 0, 0>>>((int*)p, n);
+    const hipError_t z = hipStreamSynchronize(0);
+    if (z != hipSuccess) {
+        (void)hipGetLastError();
+        return fail("scratch tag region on device %d: %s", device, hipGetErrorString(z));
+    }
     g_scratch[device] = (float*)p;
     return 0;
 }
@@ -97,12 +122,6 @@ float* scratch_of(int device) {
     if (device < 0 || device >= MAX_DEVICES) return nullptr;
     std::lock_guard<std::mutex> lock(g_scratch_mu);
     return g_scratch[device];
-}
-
-// Zeroes n ints with a kernel (a memset node in a captured graph is avoided).
-__global__ void k_zero_i32(int* p, int n) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) p[i] = 0;
 }
 
 }  // namespace
@@ -163,6 +182,7 @@ struct cngpt_hip_ctx {
     int pos_host = 0;            // staging for the position upload
     unsigned long long* dtag = nullptr;  // tagged halves of the split one-pass decode attention
     unsigned* dcnt = nullptr;            // and its per-(sequence, head) counters
+    int dtag_pairs = 0;                  // pairs dtag / dcnt hold
     unsigned long long* ptag = nullptr;  // exchange words of the persistent decode
     unsigned ptag_next = 0;      // next unused tag (tags only grow until the words are cleared)
 
@@ -386,7 +406,8 @@ int run_attn_row_proj(cngpt_hip_ctx* h, const float* qkv, long seq_stride, int B
     a.q_pos = q_pos; a.pos_dev = pos_dev;
     a.scale = 1.0f / sqrtf((float)hs);
     a.part = h->attn_part; a.max_splits = h->attn_splits;
-    a.tag_part = h->dtag; a.tag_cnt = h->dcnt;
+    a.tag_part = h->dtag; a.tag_cnt = h->dcnt; a.tag_pairs = h->dtag_pairs;
+    a.err = h->dev_err;
     const double keys = pos_dev ? 0.5 * max_keys : q_pos + 1.0;
     if (B > SKINNY && attention_dec_one_pass(B, c.n_head)) {
         // many (sequence, head) pairs: one pass, rows straight to c_proj's input
@@ -541,6 +562,7 @@ int ensure_arena(cngpt_hip_ctx* h, int B, int T, int all, int kv) {
     HIP_TRY(hipMemsetAsync(h->ptag, 0, sz[n - 1], h->stream));
     h->dtag = (unsigned long long*)take(sz[n++]);
     h->dcnt = (unsigned*)(h->dtag + attn_dec1_tag_words(nB * (int)H, (int)(C / H)));
+    h->dtag_pairs = nB * (int)H;
     HIP_TRY(hipMemsetAsync(h->dtag, 0, sz[n - 1], h->stream));
     h->tgt = (int*)take(sz[n++]);
     h->row_loss = (float*)take(sz[n++]);
@@ -839,6 +861,9 @@ int check_dev_err(cngpt_hip_ctx* h) {
         HIP_TRY(hipMemsetAsync(h->dev_err, 0, sizeof(int), h->stream));
         if (e & 2) return fail("persistent decode: a wait for a value of another workgroup timed out");
         if (e & 4) return fail("cross-entropy targets outside [0, %d) were clamped", h->cfg.vocab_size);
+        if (e & ATTN_DEC_TIMEOUT)
+            return fail("decode attention: a wait for the other half of a split (sequence, head) "
+                        "pair timed out; its row is NaN");
         return fail("device-resident token ids outside [0, %d) were clamped", h->cfg.vocab_size);
     }
     return 0;
@@ -1002,9 +1027,9 @@ int open_weight_file(const char* path, WeightFile* wf) {
         rc = fail("%s: %s", path, strerror(errno));
     } else if ((size_t)st.st_size < FILE_HEADER ||
                pread(fd, hdr, FILE_HEADER, 0) != (ssize_t)FILE_HEADER) {
-        rc = fail("%s: short header", path);
+        rc = fail("%s: file ends inside its %d-byte header", path, (int)FILE_HEADER);
     } else if (hdr[0] != FILE_MAGIC) {
-        rc = fail("%s: bad magic 0x%X", path, (unsigned)hdr[0]);
+        rc = fail("%s: not a cngpt weight file (first word 0x%X)", path, (unsigned)hdr[0]);
     } else if (hdr[1] != FILE_VERSION) {
         rc = fail("%s: unsupported version %d (this build reads version %d)", path, hdr[1],
                   FILE_VERSION);
@@ -1020,7 +1045,7 @@ int open_weight_file(const char* path, WeightFile* wf) {
             wf->n_params = params_of(&wf->cfg);
             const double need = (double)FILE_HEADER + 4.0 * (double)wf->n_params;
             if ((double)st.st_size < need)
-                rc = fail("%s: short param data (%lld bytes, the header's shape needs %.0f)", path,
+                rc = fail("%s: file ends before its parameters (%lld bytes, the header's shape needs %.0f)", path,
                           (long long)st.st_size, need);
         }
     }
@@ -1120,6 +1145,9 @@ struct FwdBufs {
     int *tok, *dev_err;
     float *x, *ln, *qkv, *aout, *hid, *logits, *xc, *lnc, *aoutc, *hidc, *attn_part, *gemm_part;
     int attn_splits;
+    unsigned long long* dtag;
+    unsigned* dcnt;
+    int dtag_pairs;
     int curB, curT, curMode;
     size_t logits_count;
     bool prof;
@@ -1128,7 +1156,7 @@ struct FwdBufs {
 FwdBufs fwd_bufs(const cngpt_hip_ctx* h) {
     return FwdBufs{h->tok, h->dev_err, h->x, h->ln, h->qkv, h->aout, h->hid, h->logits, h->xc,
                    h->lnc, h->aoutc, h->hidc, h->attn_part, h->gemm_part, h->attn_splits,
-                   h->curB, h->curT, h->curMode, h->logits_count, h->prof};
+                   h->dtag, h->dcnt, h->dtag_pairs, h->curB, h->curT, h->curMode, h->logits_count, h->prof};
 }
 
 void set_fwd_bufs(cngpt_hip_ctx* h, const FwdBufs& f) {
@@ -1137,6 +1165,7 @@ void set_fwd_bufs(cngpt_hip_ctx* h, const FwdBufs& f) {
     h->logits = f.logits;
     h->xc = f.xc; h->lnc = f.lnc; h->aoutc = f.aoutc; h->hidc = f.hidc;
     h->attn_part = f.attn_part; h->gemm_part = f.gemm_part; h->attn_splits = f.attn_splits;
+    h->dtag = f.dtag; h->dcnt = f.dcnt; h->dtag_pairs = f.dtag_pairs;
     h->curB = f.curB; h->curT = f.curT; h->curMode = f.curMode;
     h->logits_count = f.logits_count;
     h->prof = f.prof;
@@ -1148,7 +1177,12 @@ long carve_scratch(const cngpt_hip_config& c, int B, int T, float* base, FwdBufs
     const long C = c.n_embd, H = c.n_head, hs = C / H, rows = (long)B * T;
     const int kps = attn_dec_keys_per_split((int)hs);
     const int splits = (T + kps - 1) / kps;
-    long off = 0;
+    // the tag region first, at its fixed offset
+    const long tag_words = (long)attn_dec1_tag_words(attn_dec1_split_pairs(), SCRATCH_TAG_HS);
+    f->dtag = base ? (unsigned long long*)base : nullptr;
+    f->dcnt = base ? (unsigned*)(f->dtag + tag_words) : nullptr;
+    f->dtag_pairs = hs <= SCRATCH_TAG_HS ? attn_dec1_split_pairs() : 0;
+    long off = scratch_tag_floats();
     auto take = [&](long n) {
         float* r = base ? base + off : nullptr;
         off += (n + 63) / 64 * 64;
@@ -1224,6 +1258,18 @@ int cngpt_hip_create(int device, cngpt_hip_ctx** out) {
     h->device = device;
     const char* g = getenv("CNGPT_HIP_GRAPH");
     h->use_graph = !(g && g[0] == '0');
+    // Under rocprofv3 (which exports ROCP_TOOL_LIBRARIES and
+    // ROCPROF_OUTPUT_PATH to the program it profiles) no captured decode
+    // graph is replayed: the first replay of a freshly instantiated step
+    // graph ended in a segmentation fault inside hipGraphLaunch there, whose
+    // cause is not known. Decode steps then launch their kernels directly.
+    const char* tool = getenv("ROCP_TOOL_LIBRARIES");
+    const char* rp = getenv("ROCPROF_OUTPUT_PATH");
+    if (h->use_graph && ((tool && tool[0]) || (rp && rp[0]))) {
+        h->use_graph = false;
+        fprintf(stderr, "cngpt_hip: profiler detected (rocprofv3 environment); decode steps "
+                        "launch kernels directly instead of replaying captured graphs\n");
+    }
     const char* pp = getenv("CNGPT_HIP_PERSIST");
     if (pp && pp[0] == '0') h->decode_path = CNGPT_DECODE_KERNELS;
     const char* pk = getenv("CNGPT_HIP_PACK");

@@ -574,6 +574,7 @@ __global__ void __launch_bounds__(NW * 64) k_attn_dec1(AttnDecArgs a, float* __r
     const float Ls = L0 * f0 + L1 * f1;
     const f32x4 Os = O0 * f0 + O1 * f1;
     const bool all_ok = __builtin_amdgcn_ballot_w64(!ok) == 0;
+    if (!all_ok && lane == 0 && a.err) atomicOr(a.err, ATTN_DEC_TIMEOUT);
     if (lane < LPK)
         *(f32x4*)(out + (long)b * ldo + h * HS + lane * 4) =
             all_ok ? Os * (1.0f / Ls) : f32x4{NAN, NAN, NAN, NAN};
@@ -745,7 +746,7 @@ hipError_t attn_dec_hs(const AttnDecArgs& a, int B, int max_keys, hipStream_t s)
 template <int HS>
 hipError_t attn_dec1_hs(const AttnDecArgs& a, int B, float* out, long ldo, hipStream_t s) {
     const int pairs = B * a.H;
-    if (pairs < DEC1_SPLIT_BELOW && a.tag_part && a.tag_cnt)
+    if (pairs < DEC1_SPLIT_BELOW && a.tag_part && a.tag_cnt && pairs <= a.tag_pairs)
         k_attn_dec1<HS, 16, 4, 2><<<2 * pairs, 16 * 64, 0, s>>>(a, out, ldo);
     else if (pairs < 384) k_attn_dec1<HS, 16, 4, 1><<<pairs, 16 * 64, 0, s>>>(a, out, ldo);
     else k_attn_dec1<HS, 8, 4, 1><<<pairs, 8 * 64, 0, s>>>(a, out, ldo);
@@ -757,6 +758,8 @@ hipError_t attn_dec1_hs(const AttnDecArgs& a, int B, float* out, long ldo, hipSt
 bool attention_dec_one_pass(int B, int H) { return (long)B * H >= DEC1_MIN_PAIRS; }
 
 size_t attn_dec1_tag_words(int pairs, int hs) { return (size_t)pairs * 2 * (hs + 2); }
+
+int attn_dec1_split_pairs() { return DEC1_SPLIT_BELOW - 1; }
 
 hipError_t launch_attention_dec_rows(const AttnDecArgs& a, int B, float* out, long ldo,
                                      hipStream_t s) {

@@ -144,11 +144,19 @@ struct AttnDecArgs {
     // workgroups per (sequence, head) (too few pairs for one per CU): per
     // pair a counter and 2 * (hs + 2) tagged words, zeroed once and then
     // used only by that attention (attn_dec1_tag_words 64-bit words and one
-    // 32-bit counter per pair, for B * H pairs).
+    // 32-bit counter per pair), sized for tag_pairs pairs: a launch with more
+    // (sequence, head) pairs than that takes the unsplit form.
     unsigned long long* tag_part;
     unsigned* tag_cnt;
+    int tag_pairs;
+    // Optional: a wait of the split form that gives up (its row is then
+    // NaN) ORs ATTN_DEC_TIMEOUT into *err.
+    int* err;
 };
+constexpr int ATTN_DEC_TIMEOUT = 8;
 size_t attn_dec1_tag_words(int pairs, int hs);
+// Most (sequence, head) pairs the split form takes (more: one workgroup each).
+int attn_dec1_split_pairs();
 int attn_dec_keys_per_split(int hs);
 // max_keys bounds t + 1 over every launch of a captured graph (sizes the grid).
 hipError_t launch_attention_dec(const AttnDecArgs& a, int B, int max_keys, hipStream_t s);

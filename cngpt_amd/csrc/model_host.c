@@ -142,12 +142,12 @@ WEAK int gpt_load(GPT *m, const char *path)                /* model.c:177-211 */
     if (!f) { perror(path); return -1; }
     GPTHeader hdr;
     if (fread(&hdr, sizeof(hdr), 1, f) != 1) {
-        fprintf(stderr, "gpt_load: short header\n");
+        fprintf(stderr, "gpt_load: %s ends inside its %zu-byte header\n", path, sizeof(hdr));
         fclose(f);
         return -1;
     }
     if (hdr.magic != CNGPT_MAGIC) {
-        fprintf(stderr, "gpt_load: bad magic 0x%X\n", hdr.magic);
+        fprintf(stderr, "gpt_load: %s is not a cngpt weight file (first word 0x%X)\n", path, hdr.magic);
         fclose(f);
         return -1;
     }
@@ -157,13 +157,13 @@ WEAK int gpt_load(GPT *m, const char *path)                /* model.c:177-211 */
     } else if (m->cfg.n_layer != cfg.n_layer || m->cfg.n_head != cfg.n_head ||
                m->cfg.n_embd != cfg.n_embd || m->cfg.vocab_size != cfg.vocab_size ||
                m->cfg.block_size != cfg.block_size) {
-        fprintf(stderr, "gpt_load: file shape does not match the model\n");
+        fprintf(stderr, "gpt_load: %s holds a different shape than the model\n", path);
         fclose(f);
         return -1;
     }
     size_t n = (size_t)m->n_params;
     if (fread(m->param_buf, sizeof(float), n, f) != n) {
-        fprintf(stderr, "gpt_load: short param data\n");
+        fprintf(stderr, "gpt_load: %s ends before its %zu parameters\n", path, n);
         fclose(f);
         return -1;
     }

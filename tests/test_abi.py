@@ -62,11 +62,11 @@ def test_weight_file_roundtrip_and_errors(tmp_path):
     raw = f.read_bytes()
     bad = tmp_path / "bad.bin"
     bad.write_bytes(struct.pack("<i", 0x12345678) + raw[4:])
-    with pytest.raises(cngpt_amd.CngptError, match="magic"):
+    with pytest.raises(cngpt_amd.CngptError, match="not a cngpt weight file"):
         cngpt_amd.load_weights(str(bad))
     short = tmp_path / "short.bin"
     short.write_bytes(raw[:-8])
-    with pytest.raises(cngpt_amd.CngptError, match="short"):
+    with pytest.raises(cngpt_amd.CngptError, match="ends before its parameters"):
         cngpt_amd.load_weights(str(short))
 
 
@@ -98,15 +98,15 @@ def test_file_config_validates_header_without_gpu(tmp_path):
             h[i] = kw.get(k, h[i])
         return struct.pack("<7i", *h) + raw[28:]
 
-    bad("empty.bin", b"", "short header")
-    bad("hdr.bin", raw[:27], "short header")
-    bad("magic.bin", with_hdr(magic=0x12345678), "bad magic 0x12345678")
+    bad("empty.bin", b"", "ends inside its 28-byte header")
+    bad("hdr.bin", raw[:27], "ends inside its 28-byte header")
+    bad("magic.bin", with_hdr(magic=0x12345678), "not a cngpt weight file \\(first word 0x12345678\\)")
     bad("version.bin", with_hdr(version=2), "unsupported version 2")
     bad("heads.bin", with_hdr(H=5), "invalid shape")          # 64 % 5 != 0
     bad("zero.bin", with_hdr(L=0), "invalid shape")
     bad("huge.bin", with_hdr(C=1 << 30, H=1), "invalid shape")
-    bad("short.bin", raw[:-4], "short param data")
-    bad("bigger.bin", with_hdr(L=3), "short param data")      # header promises more
+    bad("short.bin", raw[:-4], "ends before its parameters")
+    bad("bigger.bin", with_hdr(L=3), "ends before its parameters")      # header promises more
     with pytest.raises(cngpt_amd.CngptError, match="No such file"):
         cngpt_amd.file_config(str(tmp_path / "missing.bin"))
 

@@ -46,10 +46,10 @@ def test_usage_and_errors(tmp_path):
     bad = tmp_path / "bad.bin"
     bad.write_bytes(b"\0" * 64)
     r = run("bench", f"--weights={bad}")
-    assert r.returncode == 1 and "bad magic" in r.stderr
+    assert r.returncode == 1 and "not a cngpt weight file" in r.stderr
     # sample validates the file header before it touches a device
     r = run("sample", f"--weights={bad}")
-    assert r.returncode == 1 and "bad magic" in r.stderr
+    assert r.returncode == 1 and "not a cngpt weight file" in r.stderr
     r = run("sample", f"--weights={tmp_path / 'missing.bin'}")
     assert r.returncode == 1 and "No such file" in r.stderr
 

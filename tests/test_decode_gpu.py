@@ -375,3 +375,35 @@ def test_packed_weights_bit_identical_to_row_major(monkeypatch):
     for a, b in zip(*runs):
         assert np.isfinite(a).all()
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_profiler_environment_turns_graph_replay_off(monkeypatch, capfd):
+    """In rocprofv3's environment (it exports ROCPROF_OUTPUT_PATH to the
+    program it profiles) a handle launches the batched decode step's kernels
+    directly instead of replaying the captured step graph, and says so on
+    stderr. The same kernels with the same arguments run either way, so
+    every step agrees bit for bit with a handle that replays its graph."""
+    cfg = cngpt_amd.Config(2, 4, 256, 1000, 128)
+    params = randomize(cfg, cngpt_amd.init_weights(cfg, 5), 6)
+    prompt = oracle.lcg_tokens(6 * 20, cfg.vocab_size).reshape(6, 20) % cfg.vocab_size
+    runs = []
+    for profiled in (False, True):
+        monkeypatch.delenv("ROCP_TOOL_LIBRARIES", raising=False)
+        if profiled:
+            monkeypatch.setenv("ROCPROF_OUTPUT_PATH", "/nonexistent-profile-output")
+        else:
+            monkeypatch.delenv("ROCPROF_OUTPUT_PATH", raising=False)
+        capfd.readouterr()
+        with cngpt_amd.Model(cfg, params) as m:
+            got = [m.decode_begin(prompt, capacity=40)]
+            toks = got[-1].argmax(-1).astype(np.int32)
+            for _ in range(10):
+                got.append(m.decode_step(toks))
+                toks = got[-1].argmax(-1).astype(np.int32)
+        noted = "profiler detected" in capfd.readouterr().err
+        assert noted == profiled
+        runs.append(got)
+    for a, b in zip(*runs):
+        assert np.isfinite(a).all()
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    say("decode B=6 with the profiler environment: direct launches, bit-identical")

@@ -75,7 +75,8 @@ def test_forward_noalloc_matches_forward_resident(hip):
     err_dev = DevBuf(hip, 4)
     try:
         with cngpt_amd.Model(cfg, params) as m:
-            # 2 x 800 rows of width 768 take 16.5 M of the scratch's 16.8 M floats
+            # 2 x 800 rows of width 768 take about 29.2 M of the scratch's 33.5 M
+            # floats (16.8 M of them the split-K partials)
             for mode, shapes in ((cngpt_amd.LAST, [(2, 800), (1, 37)]),
                                  (cngpt_amd.ALL, [(1, 300), (2, 5)])):
                 for B, T in shapes:  # the second call is smaller
@@ -106,4 +107,90 @@ def test_forward_noalloc_matches_forward_resident(hip):
             assert err_dev.get(1, np.int32)[0] & 1
     finally:
         for b in (tok_dev, logit_dev, err_dev):
+            b.free()
+
+
+def test_forward_noalloc_split_attention_on_a_small_handle(hip):
+    """GPT-2 small's 12 heads, final-position mode, B=16 T=64: the last
+    layer's 192 (sequence, head) pairs take the decode attention split over
+    two workgroups per pair, whose tagged words and counters the no-alloc
+    forward keeps in the scratch, while the handle's own arena is reserved
+    for two sequences only. Two calls in a row (the counters go on from the
+    first), each bitwise equal to the resident forward on a handle then
+    reserved for all 16."""
+    cfg = cngpt_amd.Config(2, 12, 768, 50257, 1024)
+    params = randomize(cfg, cngpt_amd.init_weights(cfg, 41), 42)
+    V = cfg.vocab_size
+    B, T = 16, 64
+    tokens = np.random.default_rng(43).integers(0, V, size=(B, T), dtype=np.int32)
+    tok_dev = DevBuf(hip, tokens.nbytes)
+    logit_dev = DevBuf(hip, B * V * 4)
+    err_dev = DevBuf(hip, 4)
+    try:
+        with cngpt_amd.Model(cfg, params) as m:
+            m.reserve(2, T, cngpt_amd.LAST)
+            tok_dev.put(tokens)
+            got = []
+            for _ in range(2):
+                say(f"noalloc split attention B={B} T={T} on a handle reserved for B=2")
+                m.forward_noalloc(tok_dev.ptr.value, B, T, cngpt_amd.LAST, logit_dev.ptr.value,
+                                  err_dev.ptr.value)
+                m.synchronize()
+                assert err_dev.get(1, np.int32)[0] == 0
+                got.append(logit_dev.get(B * V, np.float32))
+            ref = reference(m, tokens, cngpt_amd.LAST)
+        for g in got:
+            assert np.isfinite(g).all()
+            assert np.array_equal(g, ref), float(np.abs(g - ref).max())
+    finally:
+        for b in (tok_dev, logit_dev, err_dev):
+            b.free()
+
+
+def test_forward_noalloc_capacity_boundary(hip):
+    """The largest T the scratch takes at B=3 (found by halving the range
+    between an accepted and a refused length; a refusal enqueues nothing)
+    runs and matches the resident forward bitwise; one more position is
+    refused with a message."""
+    cfg = cngpt_amd.Config(2, 12, 768, 50257, 1024)
+    params = randomize(cfg, cngpt_amd.init_weights(cfg, 51), 52)
+    V = cfg.vocab_size
+    B = 3
+    rng = np.random.default_rng(53)
+    tok_dev = DevBuf(hip, B * 1024 * 4)
+    logit_dev = DevBuf(hip, B * V * 4)
+    try:
+        with cngpt_amd.Model(cfg, params) as m:
+            tok_dev.put(rng.integers(0, V, size=(B, 1024), dtype=np.int32))
+
+            def accepted(T):
+                try:
+                    m.forward_noalloc(tok_dev.ptr.value, B, T, cngpt_amd.LAST,
+                                      logit_dev.ptr.value, None)
+                except cngpt_amd.CngptError as e:
+                    assert "scratch" in str(e)
+                    return False
+                m.synchronize()
+                return True
+
+            lo, hi = 1, 1024
+            assert accepted(lo) and not accepted(hi)
+            while hi - lo > 1:
+                mid = (lo + hi) // 2
+                if accepted(mid):
+                    lo = mid
+                else:
+                    hi = mid
+            say(f"noalloc capacity at B={B}: T={lo} accepted, T={lo + 1} refused")
+            assert lo > 500
+            tokens = rng.integers(0, V, size=(B, lo), dtype=np.int32)
+            tok_dev.put(tokens)
+            assert accepted(lo)
+            got = logit_dev.get(B * V, np.float32)
+            assert not accepted(lo + 1)
+            ref = reference(m, tokens, cngpt_amd.LAST)
+        assert np.isfinite(got).all()
+        assert np.array_equal(got, ref), float(np.abs(got - ref).max())
+    finally:
+        for b in (tok_dev, logit_dev):
             b.free()
