@@ -331,6 +331,9 @@ def main():
                          "model (for kernel traces of one prefill shape)")
     ap.add_argument("--last", action="store_true",
                     help="with --prefill: final-position logits (gpt_forward_fast's mode)")
+    ap.add_argument("--loss", action="store_true",
+                    help="with --prefill (all positions): also the cross-entropy leg over the "
+                         "held logits (for counter runs of the loss kernels)")
     ap.add_argument("--train", type=int, nargs=2, metavar=("B", "T"), default=None,
                     help="only time training steps (zero_grad, forward with targets, backward, "
                          "AdamW) of B x T tokens of the workload's model")
@@ -352,6 +355,7 @@ def main():
         mode = cngpt_amd.LAST if args.last else cngpt_amd.ALL
         dt, prof = prefill(m, cfg, pB, pT, args.steps, args.warmup, mode)
         g = prof["gemm"]
+        loss = loss_leg(m, cfg, pB, pT, max(args.steps, 1)) if args.loss and not args.last else None
         m.close()
         calib = copy_calibration(args.copy_calibration << 20) if args.copy_calibration else None
         print(json.dumps({"workload": name, "B": pB, "T": pT,
@@ -362,6 +366,7 @@ def main():
                           "gemm_frac": round(g["flops"] / (g["ms"] * 1e-3) / PEAK_FP32_MFMA, 4),
                           "kernel_ms_per_forward": {k: round(v["ms"] / args.steps, 3)
                                                     for k, v in prof.items() if v["launches"]},
+                          "loss": loss,
                           "copy_calibration_bytes": calib}),
               flush=True)
         return
@@ -388,6 +393,7 @@ def main():
         m.profile(False)
         prof = m.profile_read()
         m.close()
+        calib = copy_calibration(args.copy_calibration << 20) if args.copy_calibration else None
         n = dsteps
         print(json.dumps({"workload": name, "B": dB, "decode_tok_s": round(n * dB / dec_dt, 1),
                           "ms_per_step": round(dec_dt * 1e3 / n, 4),
@@ -400,7 +406,9 @@ def main():
                           "kernel_us_per_step": {k: round(v["ms"] * 1e3 / n, 2)
                                                  for k, v in prof.items() if v["launches"]},
                           "launches_per_step": {k: round(v["launches"] / n, 2)
-                                                for k, v in prof.items() if v["launches"]}}),
+                                                for k, v in prof.items() if v["launches"]},
+                          "bytes_per_step": round(dec_bytes / n),
+                          "copy_calibration_bytes": calib}),
               flush=True)
         return
 
@@ -440,6 +448,15 @@ def main():
             tj = json.load(f)
         traffic = tj.get("measured_bytes_per_launch")
         tsrc = {k: tj.get(k) for k in ("source", "kernels_commit", "measured_on")}
+    # the single-sequence decode's HBM-side reads per step, likewise from a
+    # committed rocprofv3 --pmc FETCH_SIZE summary
+    dtraffic, dsrc = None, None
+    dpath = os.path.join(ROOT, "profiles", "decode_traffic.json")
+    if name == "small" and dB == 1 and dec_path == "persistent" and os.path.exists(dpath):
+        with open(dpath) as f:
+            dj = json.load(f)
+        dtraffic = dj.get("measured_fetch_bytes_per_step")
+        dsrc = {k: dj.get(k) for k in ("source", "kernel", "kernels_commit", "measured_on")}
 
     line = {
         "metric": f"forward tokens/sec + GEMM MFMA util %, {NAMES[name]} fp32 B={B} T={T}; "
@@ -478,7 +495,10 @@ def main():
                    "hbm": {"bound": "hbm", "achieved": round(dec_bytes / dec_dt / 1e9, 1),
                            "peak": PEAK_HBM / 1e9, "unit": "GB/s",
                            "frac": round(dec_bytes / dec_dt / PEAK_HBM, 4),
-                           "bytes_per_step": round(dec_bytes / dsteps)},
+                           "bytes_per_step": round(dec_bytes / dsteps),
+                           "traffic": dtraffic,
+                           "traffic_unit": "HBM-side read bytes per step (rocprofv3 FETCH_SIZE)",
+                           "traffic_source": dsrc},
                    "sampled_tok_s": round(dsteps * dB / samp_dt, 1),
                    "sampled": "temp 0.8, top-k 40, device sample_top_k"},
         "kernels": {k: {"ms_per_step": round(v["ms"] / args.steps, 3),
