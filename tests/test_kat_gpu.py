@@ -246,6 +246,8 @@ def test_softmax_error_bound_dense_grid(kat, kind):
     (0, 2048, 768, 3072, 3),  # tiles with K split 5 ways (M = 2048), residual reduce
     (0, 2048, 2304, 768, 1),  # stream-K: 288 tiles over 512 workgroups, fixup
     (0, 1100, 4000, 1600, 3), # stream-K: 9 x 32 ragged tiles, residual
+    (0, 1280, 7680, 256, 3),  # 600 tiles over 256 workgroups: a whole-tile round, then stream-K
+    (0, 1000, 19400, 64, 2),  # 8 x 152 ragged tiles over 512 workgroups: whole-tile round, GELU
     (0, 37, 100, 3072, 3),    # weight-streaming product, split over K
     (0, 5, 2304, 768, 1),     # weight-streaming, QKV width
     (0, 8, 3072, 1024, 1),    # weight-streaming, four wavefronts per column block, no K split
