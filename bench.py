@@ -234,13 +234,15 @@ def decode(m: cngpt_amd.Model, cfg, B: int, prompt_len: int, steps: int, draws=N
     return time.perf_counter() - t0, PATHS.get(m.decode_path(), "none")
 
 
-def reference_shape(m: cngpt_amd.Model, iters: int = 20):
+def reference_shape(m: cngpt_amd.Model, iters: int = 100, warmup: int = 10):
     """The shape the reference publishes its fast-path numbers at (B=1,
     T=128, final-position logits, README.md:410-416), through the whole
     host API (tokens H2D, logits D2H, synchronise) as `cngpt bench --fast`
-    does."""
+    does; `warmup` untimed forwards first (the first captures the forward's
+    graph)."""
     tk = np.zeros((1, 128), np.int32)
-    m.forward(tk, cngpt_amd.LAST)
+    for _ in range(warmup):
+        m.forward(tk, cngpt_amd.LAST)
     t0 = time.perf_counter()
     for _ in range(iters):
         m.forward(tk, cngpt_amd.LAST)

@@ -199,6 +199,12 @@ struct cngpt_hip_ctx {
     hipGraphExec_t step_exec = nullptr;
     int graph_B = 0, graph_cap = 0;
     const void *graph_act = nullptr, *graph_par = nullptr;
+    // the forward of one shape likewise (cngpt_hip_forward and
+    // cngpt_hip_forward_resident replay it; captured on the first call of a
+    // shape, again after the arena or the parameters moved)
+    hipGraphExec_t fwd_exec = nullptr;
+    int fwd_B = 0, fwd_T = 0, fwd_mode = -1;
+    const void *fwd_act = nullptr, *fwd_par = nullptr;
 
     // state of the last forward / decode
     int curB = 0, curT = 0, curMode = CNGPT_LAST;
@@ -452,6 +458,16 @@ int run_attn_row_proj(cngpt_hip_ctx* h, const float* qkv, long seq_stride, int B
                     nullptr, lnw, lnb, lnout);
 }
 
+void drop_fwd_graph(cngpt_hip_ctx* h) {
+    // (as for the step graph: its last launch may still be queued)
+    if (h->fwd_exec) (void)hipStreamSynchronize(h->stream);
+    if (h->fwd_exec) (void)hipGraphExecDestroy(h->fwd_exec);
+    h->fwd_exec = nullptr;
+    h->fwd_B = h->fwd_T = 0;
+    h->fwd_mode = -1;
+    h->fwd_act = h->fwd_par = nullptr;
+}
+
 void drop_graph(cngpt_hip_ctx* h) {
     // the last launch of the executable graph may still be queued on the
     // stream (a re-capture for a new batch follows the previous sequence's
@@ -516,6 +532,7 @@ int ensure_arena(cngpt_hip_ctx* h, int B, int T, int all, int kv) {
     if (h->d_act) {
         HIP_TRY(hipStreamSynchronize(h->stream));
         drop_graph(h);
+        drop_fwd_graph(h);
         HIP_TRY(hipFree(h->d_act));
         h->d_act = nullptr;
         h->act_bytes = 0;
@@ -646,6 +663,40 @@ int enqueue_forward(cngpt_hip_ctx* h, int B, int T, int mode, bool kv, bool want
         if (run_lm_head(h, h->xc, B, want_tok, nullptr)) return -1;
     }
     h->curB = B; h->curT = T; h->curMode = mode;
+    return 0;
+}
+
+// A forward of B x T tokens already in h->tok (no KV cache, no token
+// feed): the captured graph of this shape replayed, or with timing events
+// or graphs off, its kernels launched directly. A forward is ~8 launches
+// per layer; at B=1 T=128 their host-side enqueueing (about 10 us each)
+// outlasts the kernels, one graph launch does not.
+int run_forward(cngpt_hip_ctx* h, int B, int T, int mode) {
+    if (h->prof || !h->use_graph) return enqueue_forward(h, B, T, mode, false, false);
+    if (!h->fwd_exec || h->fwd_B != B || h->fwd_T != T || h->fwd_mode != mode ||
+        h->fwd_act != h->d_act || h->fwd_par != h->d_params) {
+        drop_fwd_graph(h);
+        hipGraph_t g = nullptr;
+        HIP_TRY(hipStreamBeginCapture(h->stream, hipStreamCaptureModeThreadLocal));
+        const int rc = enqueue_forward(h, B, T, mode, false, false);
+        const hipError_t e = hipStreamEndCapture(h->stream, &g);
+        if (rc || e != hipSuccess) {
+            if (g) (void)hipGraphDestroy(g);
+            (void)hipGetLastError();
+            return rc ? -1 : fail("forward graph capture failed: %s", hipGetErrorString(e));
+        }
+        hipGraphExec_t ex = nullptr;
+        const hipError_t ei = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(g);
+        if (ei != hipSuccess) return fail("forward graph instantiate: %s", hipGetErrorString(ei));
+        h->fwd_exec = ex;
+        h->fwd_B = B; h->fwd_T = T; h->fwd_mode = mode;
+        h->fwd_act = h->d_act;
+        h->fwd_par = h->d_params;
+    }
+    HIP_TRY(hipGraphLaunch(h->fwd_exec, h->stream));
+    h->curB = B; h->curT = T; h->curMode = mode;
+    h->logits_count = (size_t)(mode == CNGPT_ALL ? (long)B * T : B) * h->cfg.vocab_size;
     return 0;
 }
 
@@ -918,6 +969,7 @@ int params_prepare(cngpt_hip_ctx* h, const cngpt_hip_config* cfg) {
     if (h->d_params && memcmp(&h->cfg, cfg, sizeof(*cfg)) == 0) return 0;
     if (h->d_params) {
         HIP_TRY(hipStreamSynchronize(h->stream));
+        drop_fwd_graph(h);
         HIP_TRY(hipFree(h->d_params));
         h->d_params = nullptr;
     }
@@ -1287,6 +1339,7 @@ void cngpt_hip_destroy(cngpt_hip_ctx* h) {
     (void)hipSetDevice(h->device);
     if (h->stream) (void)hipStreamSynchronize(h->stream);
     drop_graph(h);
+    drop_fwd_graph(h);
     for (hipEvent_t e : h->pool) (void)hipEventDestroy(e);
     if (h->d_act) (void)hipFree(h->d_act);
     if (h->d_params) (void)hipFree(h->d_params);
@@ -1363,7 +1416,7 @@ int cngpt_hip_forward_resident(cngpt_hip_ctx* h, int B, int T, int mode) {
         return fail("forward_resident: arena not reserved for B=%d T=%d mode=%d", B, T, mode);
     HIP_TRY(hipSetDevice(h->device));
     h->kvB = h->kvLen = 0;
-    return enqueue_forward(h, B, T, mode, false, false);
+    return run_forward(h, B, T, mode);
 }
 
 int cngpt_hip_forward_noalloc(cngpt_hip_ctx* h, const int* tokens, int B, int T, int mode,
@@ -1409,7 +1462,7 @@ int cngpt_hip_forward(cngpt_hip_ctx* h, const int* tokens, int B, int T, int mod
     h->kvB = h->kvLen = 0;
     HIP_TRY(hipMemcpyAsync(h->tok, tokens, (size_t)B * T * sizeof(int), hipMemcpyHostToDevice,
                            h->stream));
-    if (enqueue_forward(h, B, T, mode, false, false)) return -1;
+    if (run_forward(h, B, T, mode)) return -1;
     if (logits_out)
         HIP_TRY(hipMemcpyAsync(logits_out, h->logits, h->logits_count * sizeof(float),
                                hipMemcpyDeviceToHost, h->stream));

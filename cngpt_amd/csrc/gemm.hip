@@ -781,6 +781,115 @@ __global__ void __launch_bounds__(ST_NW * 64) k_stream(GemmArgs a, int tiles_n, 
 }
 
 // Y = epi(sum over the KS partial tiles, in order); one thread per output.
+// k_rows: products over 64 < M <= 128 rows whose 128 x 128 tiles would
+// leave most CUs idle (the B=1 T=128 forward: 6-24 such tiles per product).
+// A workgroup of four wavefronts owns a 32-row x 32-column tile; each
+// wavefront one 16 x 16 block of it (v_mfma_f32_16x16x4f32) over the whole
+// K range of the workgroup, so QKV and fc (288 / 384 tiles at M = 128)
+// need no K split and no sum launch. Both operands go global -> LDS
+// (lds_dma16) through a ring of RW_S stages of RW_BK k: the loads of
+// RW_S - 1 stages are in flight while one is multiplied, one wait and one
+// barrier per stage. A stage row is 16 granules of 16 bytes, the granule
+// order XOR-swizzled by the row, so the 16 rows a read instruction touches
+// at one k quad fall in 16 different granules of the 256-byte bank line.
+// K is split over KS workgroups only when the tiles are fewer than the
+// CUs (partials, then the ordered sum of reduce_splits).
+constexpr int RW_BK = 64, RW_S = 5, RW_T = 32;
+constexpr int RW_TILE = RW_T * RW_BK;  // floats per operand per stage
+
+template <int EPI>
+__global__ void __launch_bounds__(256, 2) k_rows(GemmArgs a, int tiles_m, int tiles_n, int KR,
+                                                 int KS) {
+    __shared__ __attribute__((aligned(1024))) float sm[RW_S * 2 * RW_TILE];
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    // work id: row tiles fastest, then column tiles, then K splits; ids
+    // XCD-contiguous, so the row tiles of a column tile share its W rows in
+    // one XCD's L2
+    const int p = xcd_order(blockIdx.x, tiles_m * tiles_n * KS);
+    const int tm = p % tiles_m, tn = (p / tiles_m) % tiles_n, ks = p / (tiles_m * tiles_n);
+    const int m0 = tm * RW_T, n0 = tn * RW_T;
+    const int K = a.K, M = a.M, N = a.N;
+    const int kb = ks * KR, nk = (min(K, kb + KR) - kb) / RW_BK;
+    // load instruction i (0, 1) of wavefront w covers stage rows 4 (4 i +
+    // w) .. +3 of each operand: lane -> row 4 (4 i + w) + lane / 16, slot
+    // lane % 16, holding k quad slot ^ (row % 16); rows past M or N read
+    // the last one (finite values; their results are not stored)
+    const float* xs[2];
+    const float* ws[2];
+    int lo[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int row = 4 * (4 * i + wave) + (lane >> 4), slot = lane & 15;
+        const int kq = slot ^ (row & 15);
+        xs[i] = a.X + (long)min(m0 + row, M - 1) * K + kb + 4 * kq;
+        ws[i] = a.W + (long)min(n0 + row, N - 1) * K + kb + 4 * kq;
+        lo[i] = (4 * i + wave) * 64 * 4;  // this instruction's 64 granules in the stage
+    }
+    auto issue = [&](int kt, int st) {
+        float* base = sm + st * 2 * RW_TILE;
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            lds_dma16(xs[i] + kt * RW_BK, base + lo[i]);
+            lds_dma16(ws[i] + kt * RW_BK, base + RW_TILE + lo[i]);
+        }
+    };
+    // this wavefront's block: rows 16 (w / 2) .., columns 16 (w % 2) ..;
+    // lane reads row (or column) 16 b + lane % 16, k quad 4 s + lane / 16 of
+    // sub-step s
+    const int lc = lane & 15, g = lane >> 4;
+    const int ra = 16 * (wave >> 1) + lc, rb = 16 * (wave & 1) + lc;
+    int ao[4], bo[4];
+#pragma unroll
+    for (int s4 = 0; s4 < 4; s4++) {
+        const int q = 4 * s4 + g;
+        ao[s4] = ra * RW_BK + 4 * (q ^ (ra & 15));
+        bo[s4] = RW_TILE + rb * RW_BK + 4 * (q ^ (rb & 15));
+    }
+    // four accumulators (k = 4 j + e of each 16-k sub-step goes to acc[e]),
+    // so consecutive products do not wait for each other's results; added
+    // in a fixed order at the end
+    f32x4 acc4[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) acc4[e] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int st = 0; st < RW_S - 1; st++)
+        if (st < nk) issue(st, st);
+    for (int kt = 0; kt < nk; kt++) {
+        // stage kt has landed once at most the later stages' loads (4
+        // instructions each) are in flight
+        if (kt + RW_S - 2 < nk) wait_vmcnt<4 * (RW_S - 2)>();
+        else wait_vmcnt<0>();
+        // every wavefront's granules of this stage have landed, and every
+        // wavefront is done with the stage the next issue overwrites
+        asm volatile("s_barrier" ::: "memory");
+        if (kt + RW_S - 1 < nk) issue(kt + RW_S - 1, (kt + RW_S - 1) % RW_S);
+        const float* base = sm + (kt % RW_S) * 2 * RW_TILE;
+#pragma unroll
+        for (int s4 = 0; s4 < 4; s4++) {
+            const f32x4 av = *(const f32x4*)&base[ao[s4]];
+            const f32x4 bv = *(const f32x4*)&base[bo[s4]];
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                acc4[e] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[e], bv[e], acc4[e], 0, 0, 0);
+        }
+    }
+    const f32x4 acc = (acc4[0] + acc4[1]) + (acc4[2] + acc4[3]);
+    // acc[r]: row m0 + 16 (w / 2) + 4 (lane / 16) + r, column n0 + 16 (w % 2) + lane % 16
+    const int col = n0 + 16 * (wave & 1) + lc;
+    if (col >= N) return;
+    const int r0 = m0 + 16 * (wave >> 1) + 4 * g;
+    if (KS == 1) {
+        const long roff = a.row_off + (a.row_off_dev ? *a.row_off_dev : 0);
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+            if (r0 + r < M) store_out<EPI>(a, roff, r0 + r, col, acc[r]);
+        return;
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+        if (r0 + r < M) a.part[((long)ks * M + r0 + r) * N + col] = acc[r];
+}
+
 template <int EPI>
 __global__ void __launch_bounds__(256) k_stream_reduce(GemmArgs a, int KS) {
     const long i = (long)blockIdx.x * 256 + threadIdx.x;
@@ -981,6 +1090,29 @@ hipError_t skinny_epi(const GemmArgs& a, hipStream_t s) {
     return stream_mb<EPI, 8>(a, s);
 }
 
+// k_rows for 64 < M <= 128: K split only while the 32 x 32 tiles are
+// fewer than the CUs, each range at least 4 stages (256 k), the partials
+// within a.part_cap.
+int rows_splits(const GemmArgs& a, int* KR) {
+    const int tiles = ((a.M + RW_T - 1) / RW_T) * ((a.N + RW_T - 1) / RW_T);
+    const int steps = a.K / RW_BK;
+    int KS = a.part && tiles < 256 ? std::min((256 + tiles - 1) / tiles, std::max(1, a.K / 256)) : 1;
+    while (KS > 1 && (long)KS * a.M * a.N > a.part_cap) KS--;
+    *KR = (steps + KS - 1) / KS * RW_BK;
+    return (a.K + *KR - 1) / *KR;
+}
+
+template <int EPI>
+hipError_t rows_epi(const GemmArgs& a, hipStream_t s) {
+    const int tiles_m = (a.M + RW_T - 1) / RW_T, tiles_n = (a.N + RW_T - 1) / RW_T;
+    int KR;
+    const int KS = rows_splits(a, &KR);
+    k_rows<EPI><<<tiles_m * tiles_n * KS, 256, 0, s>>>(a, tiles_m, tiles_n, KR, KS);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    return KS == 1 ? ln_after(a, s) : reduce_splits<EPI>(a, KS, s);
+}
+
 // The few-row products take M <= SKINNY_MAX_M rows, and up to ST_MAX_M rows
 // of products whose 128 x 128 tiles would be too few for the CUs (the
 // reference's own B=1 T=128 forward: 6-24 tiles per product), with
@@ -995,6 +1127,12 @@ bool use_stream(const GemmArgs& a) {
     }();
     if (force >= 0) return force == 1;
     return (long)((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN) < 256;
+}
+
+// Of those, the ones over more than SKINNY_MAX_M rows with K in whole
+// k_rows stages take k_rows instead of k_stream.
+bool use_rows(const GemmArgs& a) {
+    return a.M > SKINNY_MAX_M && a.K % RW_BK == 0 && use_stream(a);
 }
 
 // Share of the tile slots the last round of a launch fills when `res`
@@ -1179,6 +1317,7 @@ hipError_t launch_pack_w(const float* W, float* Wp, int N, int K, hipStream_t s)
 int launch_gemm_splits(const GemmArgs& a) {
     if (a.M <= 0 || a.N <= 0 || a.K <= 0 || (a.K & 3)) return 1;
     int KR;
+    if (use_rows(a)) return rows_splits(a, &KR);
     if (use_stream(a)) return stream_splits(a, &KR);
     return tile_splits(a, ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN), &KR);
 }
@@ -1201,6 +1340,15 @@ hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
             (both && ((a.ldx & 3) || a.ldx < ((a.M + 3) & ~3))))
             return hipErrorInvalidValue;
         return both ? gemm_km<EPI_RESID, 3>(a, s) : gemm_km<EPI_STORE, 2>(a, s);
+    }
+    if (use_rows(a)) {
+        switch (a.epi) {
+            case EPI_STORE: return rows_epi<EPI_STORE>(a, s);
+            case EPI_BIAS: return rows_epi<EPI_BIAS>(a, s);
+            case EPI_BIAS_GELU: return rows_epi<EPI_BIAS_GELU>(a, s);
+            case EPI_RESID: return rows_epi<EPI_RESID>(a, s);
+        }
+        return hipErrorInvalidValue;
     }
     if (use_stream(a)) {
         switch (a.epi) {

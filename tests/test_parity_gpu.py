@@ -237,3 +237,43 @@ def test_errors_are_reported(small):
     # the handle still works after the errors
     tk = np.zeros((1, 4), np.int32)
     compare(m.forward(tk), oracle.forward(ocfg(cfg), params, tk), what="after errors")
+
+
+def test_forward_graph_replays_match_direct_launches(monkeypatch):
+    """cngpt_hip_forward and cngpt_hip_forward_resident replay a captured
+    graph per shape; a handle made with CNGPT_HIP_GRAPH=0 launches the same
+    kernels directly. Every call agrees bit for bit: repeated shapes with new
+    tokens (the replay reads the uploaded tokens), shape changes (a new
+    capture), an arena growth, and a decode (eager launches) in between."""
+    cfg = cngpt_amd.Config(2, 12, 768, 50257, 1024)
+    params = randomize(cfg, cngpt_amd.init_weights(cfg, 61), 62)
+    rng = np.random.default_rng(63)
+    monkeypatch.setenv("CNGPT_HIP_GRAPH", "1")
+    g = cngpt_amd.Model(cfg, params)
+    monkeypatch.setenv("CNGPT_HIP_GRAPH", "0")
+    d = cngpt_amd.Model(cfg, params)
+    try:
+        calls = [(1, 128, cngpt_amd.LAST), (1, 128, cngpt_amd.LAST), (2, 64, cngpt_amd.ALL),
+                 (1, 128, cngpt_amd.LAST), (5, 200, cngpt_amd.LAST), (1, 128, cngpt_amd.LAST)]
+        for i, (B, T, mode) in enumerate(calls):
+            say(f"forward graph replay {i}: B={B} T={T} mode={mode}")
+            tokens = rng.integers(0, cfg.vocab_size, size=(B, T), dtype=np.int32)
+            a = g.forward(tokens, mode)
+            b = d.forward(tokens, mode)
+            assert np.isfinite(a).all()
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), i
+            # the resident entry point replays the same graph
+            g.upload_tokens(tokens)
+            g.forward_resident(B, T, mode)
+            g.synchronize()
+            n = B * cfg.vocab_size if mode == cngpt_amd.LAST else B * T * cfg.vocab_size
+            c = g.read_logits(0, n)
+            assert np.array_equal(c.view(np.uint32), b.reshape(-1).view(np.uint32)), i
+            if i == 2:
+                # eager work between replays: a few decode steps
+                prompt = rng.integers(0, cfg.vocab_size, size=(2, 9), dtype=np.int32)
+                l0 = g.decode_begin(prompt, capacity=20)
+                g.decode_step(l0.argmax(-1).astype(np.int32))
+    finally:
+        g.close()
+        d.close()
