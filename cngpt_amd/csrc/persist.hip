@@ -303,14 +303,20 @@ __device__ __forceinline__ void col_dots(float (&acc)[UPW], const f32x4 (&w)[NW]
     cw = opaque_s(cw);
     lane = opaque_v(lane);
     const int K4 = K >> 2;
+    // the activation float4s of this lane, read once and unconditionally
+    // (at clamped indices): reads under a lane-dependent condition make the
+    // compiler branch around each one and wait for it inside the branch
+    f32x4 xv[NI];
+#pragma unroll
+    for (int i = 0; i < NI; i++) xv[i] = act[min(i * 64 + lane, K4 - 1)];
 #pragma unroll
     for (int j = 0; j < UPW; j++) {
         float s = 0.f;
         if (j < NJ && cw + CW * j < N) {
 #pragma unroll
             for (int i = 0; i < NI; i++) {
-                const int f = i * 64 + lane;
-                if (f < K4) s += dot4(w[j * NI + i], act[f]);
+                const float d = dot4(w[j * NI + i], xv[i]);
+                s += i * 64 + lane < K4 ? d : 0.f;
             }
         }
         acc[j] = s;
@@ -612,23 +618,36 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
                 if (!ctrl) {
                     const int kk = kw0 + (lane >> 2), dq = lane & 3;
                     const bool valid = kk < kw1;
+                    // q, the new key and the new value read from LDS once,
+                    // unconditionally; the new key and value then replace
+                    // the cached ones by register selects (a read under the
+                    // per-key condition was a branch and an LDS wait per key)
                     const f32x4* qn = (const f32x4*)&sm.qkv_new[0][dq * 16];
                     const f32x4* kn = (const f32x4*)&sm.qkv_new[1][dq * 16];
+                    f32x4 qv[4], kv4[4];
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        qv[i] = qn[i];
+                        kv4[i] = kn[i];
+                    }
+                    const float vnew = sm.qkv_new[2][lane];
+                    const bool isnew = kk == t;
                     float d = 0.f;
 #pragma unroll
-                    for (int i = 0; i < 4; i++) d += dot4(qn[i], kk == t ? kn[i] : kq[i]);
+                    for (int i = 0; i < 4; i++) d += dot4(qv[i], isnew ? kv4[i] : kq[i]);
                     d += CNGPT_DPP(d, 0xB1);  // the 4 lanes of a key: xor 1, xor 2
                     d += CNGPT_DPP(d, 0x4E);
                     const float sc = valid ? d * a.scale : -INFINITY;
                     const float m = wave_max_dpp(sc);
                     const float e = valid ? expf(sc - m) : 0.f;
                     const float ls = wave_sum_dpp(dq == 0 ? e : 0.f);
+                    // keys past kw1 have e = 0 (and finite cached values), so
+                    // they add exact zeros
                     float o = 0.f;
 #pragma unroll
                     for (int jj = 0; jj < KPW; jj++) {
                         const float pj = lane_f(e, 4 * jj);
-                        const int kj = kw0 + jj;
-                        if (kj < kw1) o += pj * (kj == t ? sm.qkv_new[2][lane] : vr[jj]);
+                        o += pj * (kw0 + jj == t ? vnew : vr[jj]);
                     }
                     if (lane == 0) {
                         sm.attn[wave][0] = m;
@@ -638,16 +657,23 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
                 }
                 __syncthreads();
                 if (ctrl) {
+                    // every wavefront's m, l and o read before any is used
+                    float mv[PW], lv[PW], ov[PW];
+#pragma unroll
+                    for (int v = 0; v < PW; v++) {
+                        mv[v] = sm.attn[v][0];
+                        lv[v] = sm.attn[v][1];
+                        ov[v] = sm.attn[v][4 + lane];
+                    }
                     float M = -INFINITY;
 #pragma unroll
-                    for (int v = 0; v < PW; v++) M = fmaxf(M, sm.attn[v][0]);
+                    for (int v = 0; v < PW; v++) M = fmaxf(M, mv[v]);
                     float Ls = 0.f, O = 0.f;
 #pragma unroll
                     for (int v = 0; v < PW; v++) {
-                        const float mv = sm.attn[v][0];
-                        const float f = mv == -INFINITY ? 0.f : expf(mv - M);
-                        Ls += sm.attn[v][1] * f;
-                        O += sm.attn[v][4 + lane] * f;
+                        const float f = mv[v] == -INFINITY ? 0.f : expf(mv[v] - M);
+                        Ls += lv[v] * f;
+                        O += ov[v] * f;
                     }
                     u64* part = tp + ((long)ih * PMAXS + isp) * 68;
                     put_all(part + 4 + lane, tl.ps, O, TB);
@@ -714,18 +740,27 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
                     }
                 }
                 if (!settle(ok)) return;
+                // merge: each head's split weights exp(m_s - M) / L, formed
+                // once (in place of the m values) by one thread per head,
+                // then every channel the weighted sum of its head's splits
+                if (tid < H) {
+                    float* mh = &sm.ml[0][tid * ns];
+                    const float* lh = &sm.ml[1][tid * ns];
+                    float M = -INFINITY;
+                    for (int sp = 0; sp < ns; sp++) M = fmaxf(M, mh[sp]);
+                    float Ls = 0.f;
+                    for (int sp = 0; sp < ns; sp++)
+                        Ls += lh[sp] * (mh[sp] == -INFINITY ? 0.f : expf(mh[sp] - M));
+                    const float inv = 1.0f / Ls;
+                    for (int sp = 0; sp < ns; sp++)
+                        mh[sp] = (mh[sp] == -INFINITY ? 0.f : expf(mh[sp] - M)) * inv;
+                }
+                __syncthreads();
                 for (int e = tid; e < C; e += PT) {
-                    const int h = e >> 6;
-                    float mx = -INFINITY, Ls = 0.f, acc = 0.f;
-                    for (int sp = 0; sp < ns; sp++) {
-                        const float ms = sm.ml[0][h * ns + sp], lsum = sm.ml[1][h * ns + sp];
-                        const float mn = fmaxf(mx, ms);
-                        const float fa = expf(mx - mn), fb = expf(ms - mn);
-                        acc = acc * fa + sm.obuf[sp * C + e] * fb;
-                        Ls = Ls * fa + lsum * fb;
-                        mx = mn;
-                    }
-                    actf[e] = acc * (1.0f / Ls);
+                    const float* wh = &sm.ml[0][(e >> 6) * ns];
+                    float acc = 0.f;
+                    for (int sp = 0; sp < ns; sp++) acc += wh[sp] * sm.obuf[sp * C + e];
+                    actf[e] = acc;
                 }
                 __syncthreads();
                 if (!ctrl) {
@@ -806,10 +841,13 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
                     const int ln = opaque_v(lane);
                     float acc[UPW] = {0.f, 0.f, 0.f, 0.f};
                     if (cw < C) {
+                        // (unconditional reads at clamped indices, as in col_dots)
 #pragma unroll
                         for (int i = 0; i < 4 * U; i++) {
                             const int f = i * 64 + ln;
-                            if (f < C) acc[0] += dot4(i < 2 * U ? wa[2 * U + i] : wb[i - U], sm.act[f]);
+                            const float d = dot4(i < 2 * U ? wa[2 * U + i] : wb[i - U],
+                                                 sm.act[min(f, C - 1)]);
+                            acc[0] += f < C ? d : 0.f;
                         }
                     }
                     acc[0] = wave_sum_dpp(acc[0]);
@@ -857,7 +895,8 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
 #pragma unroll
                         for (int i = 0; i < U; i++) {
                             const int f = i * 64 + ln;
-                            if (f < K4) s += dot4(wa[k * U + i], sm.act[f]);
+                            const float d = dot4(wa[k * U + i], sm.act[min(f, K4 - 1)]);
+                            s += f < K4 ? d : 0.f;
                         }
                         const int nc = col + CW * UPW;
                         if (nc < V) {
