@@ -783,111 +783,148 @@ __global__ void __launch_bounds__(ST_NW * 64) k_stream(GemmArgs a, int tiles_n, 
 // Y = epi(sum over the KS partial tiles, in order); one thread per output.
 // k_rows: products over 64 < M <= 128 rows whose 128 x 128 tiles would
 // leave most CUs idle (the B=1 T=128 forward: 6-24 such tiles per product).
-// A workgroup of four wavefronts owns a 32-row x 32-column tile; each
-// wavefront one 16 x 16 block of it (v_mfma_f32_16x16x4f32) over the whole
-// K range of the workgroup, so QKV and fc (288 / 384 tiles at M = 128)
-// need no K split and no sum launch. Both operands go global -> LDS
-// (lds_dma16) through a ring of RW_S stages of RW_BK k: the loads of
-// RW_S - 1 stages are in flight while one is multiplied, one wait and one
-// barrier per stage. A stage row is 16 granules of 16 bytes, the granule
-// order XOR-swizzled by the row, so the 16 rows a read instruction touches
-// at one k quad fall in 16 different granules of the 256-byte bank line.
-// K is split over KS workgroups only when the tiles are fewer than the
-// CUs (partials, then the ordered sum of reduce_splits).
-constexpr int RW_BK = 64, RW_S = 5, RW_T = 32;
-constexpr int RW_TILE = RW_T * RW_BK;  // floats per operand per stage
+// A workgroup of four wavefronts owns a 32-row x TN-column tile (TN = 32,
+// 48 or 64: two by TN / 16 blocks of v_mfma_f32_16x16x4f32); each wavefront
+// multiplies the whole tile over a quarter of every stage's k (k quads 4 w
+// .. 4 w + 3), so each LDS granule is read by one wavefront (a split of the
+// tile over the wavefronts reads every row twice), and the four partial
+// tiles are summed through LDS in wavefront order at the end. Both operands
+// go global -> LDS (lds_dma16) through a ring of RQ_S stages of RQ_BK k:
+// one wait and one barrier per stage, the next stage's operands read from
+// LDS while the current stage's products issue. A stage row is 16 granules
+// of 16 bytes, the granule order XOR-swizzled by the row, so the 16 rows a
+// read instruction touches at one k quad fall in 16 different granules of
+// the 256-byte bank line. TN and a K split are chosen so that each CU holds
+// one workgroup where the product allows (rows_plan): a CU holding two
+// workgroups of a launch takes twice as long as the others, so 288 or 384
+// 32 x 32 tiles (GPT-2's QKV and fc at 128 rows) ran at the speed of 512.
+constexpr int RQ_BK = 64, RQ_S = 5, RQ_TM = 32;
 
-template <int EPI>
-__global__ void __launch_bounds__(256, 2) k_rows(GemmArgs a, int tiles_m, int tiles_n, int KR,
+template <int EPI, int TN>
+__global__ void __launch_bounds__(256, 1) k_rows(GemmArgs a, int tiles_m, int tiles_n, int KR,
                                                  int KS) {
-    __shared__ __attribute__((aligned(1024))) float sm[RW_S * 2 * RW_TILE];
+    constexpr int ROWS = RQ_TM + TN;     // stage rows: RQ_TM of X, then TN of W
+    constexpr int NI = ROWS / 16;        // load instructions per wavefront and stage
+    constexpr int STAGE = ROWS * RQ_BK;  // floats per stage
+    constexpr int CB = TN / 16;          // 16-column blocks
+    constexpr int RS = TN + 4;           // row stride of the partial tiles (bank spread)
+    static_assert(ROWS % 16 == 0 && 4 * RQ_TM * RS <= RQ_S * STAGE, "tile shape");
+    __shared__ __attribute__((aligned(1024))) float sm[RQ_S * STAGE];
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     // work id: row tiles fastest, then column tiles, then K splits; ids
     // XCD-contiguous, so the row tiles of a column tile share its W rows in
     // one XCD's L2
     const int p = xcd_order(blockIdx.x, tiles_m * tiles_n * KS);
     const int tm = p % tiles_m, tn = (p / tiles_m) % tiles_n, ks = p / (tiles_m * tiles_n);
-    const int m0 = tm * RW_T, n0 = tn * RW_T;
+    const int m0 = tm * RQ_TM, n0 = tn * TN;
     const int K = a.K, M = a.M, N = a.N;
-    const int kb = ks * KR, nk = (min(K, kb + KR) - kb) / RW_BK;
-    // load instruction i (0, 1) of wavefront w covers stage rows 4 (4 i +
-    // w) .. +3 of each operand: lane -> row 4 (4 i + w) + lane / 16, slot
-    // lane % 16, holding k quad slot ^ (row % 16); rows past M or N read
-    // the last one (finite values; their results are not stored)
-    const float* xs[2];
-    const float* ws[2];
-    int lo[2];
+    const int kb = ks * KR, nk = (min(K, kb + KR) - kb) / RQ_BK;
+    // load instruction i of wavefront w covers stage rows 4 (4 i + w) ..
+    // +3: lane -> row 4 (4 i + w) + lane / 16, slot lane % 16, holding k
+    // quad slot ^ (row % 16); rows past M or N read the last one (finite
+    // values; their results are not stored)
+    const float* src[NI];
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
+    for (int i = 0; i < NI; i++) {
         const int row = 4 * (4 * i + wave) + (lane >> 4), slot = lane & 15;
         const int kq = slot ^ (row & 15);
-        xs[i] = a.X + (long)min(m0 + row, M - 1) * K + kb + 4 * kq;
-        ws[i] = a.W + (long)min(n0 + row, N - 1) * K + kb + 4 * kq;
-        lo[i] = (4 * i + wave) * 64 * 4;  // this instruction's 64 granules in the stage
+        src[i] = row < RQ_TM ? a.X + (long)min(m0 + row, M - 1) * K + kb + 4 * kq
+                             : a.W + (long)min(n0 + row - RQ_TM, N - 1) * K + kb + 4 * kq;
     }
     auto issue = [&](int kt, int st) {
-        float* base = sm + st * 2 * RW_TILE;
+        float* base = sm + st * STAGE;
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
-            lds_dma16(xs[i] + kt * RW_BK, base + lo[i]);
-            lds_dma16(ws[i] + kt * RW_BK, base + RW_TILE + lo[i]);
-        }
+        for (int i = 0; i < NI; i++) lds_dma16(src[i] + kt * RQ_BK, base + (4 * i + wave) * 256);
     };
-    // this wavefront's block: rows 16 (w / 2) .., columns 16 (w % 2) ..;
-    // lane reads row (or column) 16 b + lane % 16, k quad 4 s + lane / 16 of
-    // sub-step s
-    const int lc = lane & 15, g = lane >> 4;
-    const int ra = 16 * (wave >> 1) + lc, rb = 16 * (wave & 1) + lc;
-    int ao[4], bo[4];
+    // lane: row (column) 16 b + lane % 16 of each 16-block, k quad 4 w +
+    // lane / 16; element e of the quad is the k of the e-th product
+    const int lc = lane & 15, g = lane >> 4, q = 4 * wave + g;
+    int ao[2], bo[CB];
 #pragma unroll
-    for (int s4 = 0; s4 < 4; s4++) {
-        const int q = 4 * s4 + g;
-        ao[s4] = ra * RW_BK + 4 * (q ^ (ra & 15));
-        bo[s4] = RW_TILE + rb * RW_BK + 4 * (q ^ (rb & 15));
+    for (int rb = 0; rb < 2; rb++) {
+        const int r = 16 * rb + lc;
+        ao[rb] = r * RQ_BK + 4 * (q ^ (r & 15));
     }
-    // four accumulators (k = 4 j + e of each 16-k sub-step goes to acc[e]),
-    // so consecutive products do not wait for each other's results; added
-    // in a fixed order at the end
-    f32x4 acc4[4];
 #pragma unroll
-    for (int e = 0; e < 4; e++) acc4[e] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int cb = 0; cb < CB; cb++) {
+        const int r = RQ_TM + 16 * cb + lc;
+        bo[cb] = r * RQ_BK + 4 * (q ^ (r & 15));
+    }
+    f32x4 acc[2][CB];
 #pragma unroll
-    for (int st = 0; st < RW_S - 1; st++)
+    for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+        for (int cb = 0; cb < CB; cb++) acc[rb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // operands of a stage, read from LDS one stage ahead of their products
+    // (the reads of stage kt + 1 are in flight while stage kt's products
+    // issue)
+    f32x4 av[2], bv[CB];
+    auto read = [&](int kt) {
+        const float* base = sm + (kt % RQ_S) * STAGE;
+#pragma unroll
+        for (int rb = 0; rb < 2; rb++) av[rb] = *(const f32x4*)&base[ao[rb]];
+#pragma unroll
+        for (int cb = 0; cb < CB; cb++) bv[cb] = *(const f32x4*)&base[bo[cb]];
+    };
+#pragma unroll
+    for (int st = 0; st < RQ_S - 1; st++)
         if (st < nk) issue(st, st);
-    for (int kt = 0; kt < nk; kt++) {
-        // stage kt has landed once at most the later stages' loads (4
-        // instructions each) are in flight
-        if (kt + RW_S - 2 < nk) wait_vmcnt<4 * (RW_S - 2)>();
+    if (nk > 0) {
+        // stage 0 has landed once at most stages 1 .. RQ_S - 2 are in flight
+        if (RQ_S - 2 < nk) wait_vmcnt<NI * (RQ_S - 2)>();
         else wait_vmcnt<0>();
-        // every wavefront's granules of this stage have landed, and every
-        // wavefront is done with the stage the next issue overwrites
         asm volatile("s_barrier" ::: "memory");
-        if (kt + RW_S - 1 < nk) issue(kt + RW_S - 1, (kt + RW_S - 1) % RW_S);
-        const float* base = sm + (kt % RW_S) * 2 * RW_TILE;
+        read(0);
+    }
+    for (int kt = 0; kt < nk; kt++) {
+        const f32x4 a0 = av[0], a1 = av[1];
+        f32x4 bc[CB];
 #pragma unroll
-        for (int s4 = 0; s4 < 4; s4++) {
-            const f32x4 av = *(const f32x4*)&base[ao[s4]];
-            const f32x4 bv = *(const f32x4*)&base[bo[s4]];
+        for (int cb = 0; cb < CB; cb++) bc[cb] = bv[cb];
+        if (kt + 1 < nk) {
+            // stage kt + 1 has landed once at most stages kt + 2 .. kt +
+            // RQ_S - 2 are in flight; past the barrier every wavefront has
+            // landed its part of it and is done reading stage kt - 1 (its
+            // products issued in the previous trip), which the next issue
+            // overwrites
+            if (kt + RQ_S - 2 < nk) wait_vmcnt<NI * (RQ_S - 3)>();
+            else wait_vmcnt<0>();
+            asm volatile("s_barrier" ::: "memory");
+            if (kt + RQ_S - 1 < nk) issue(kt + RQ_S - 1, (kt + RQ_S - 1) % RQ_S);
+            read(kt + 1);
+        }
 #pragma unroll
-            for (int e = 0; e < 4; e++)
-                acc4[e] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[e], bv[e], acc4[e], 0, 0, 0);
+        for (int e = 0; e < 4; e++)
+#pragma unroll
+            for (int cb = 0; cb < CB; cb++) {
+                acc[0][cb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0[e], bc[cb][e], acc[0][cb], 0, 0, 0);
+                acc[1][cb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1[e], bc[cb][e], acc[1][cb], 0, 0, 0);
+            }
+    }
+    // every load has landed (the wait before the last stage's reads was for
+    // all of them) and, past this barrier, every wavefront is done reading
+    // the ring: it holds the partial tiles, [wave][row][RS]
+    __syncthreads();
+#pragma unroll
+    for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+        for (int cb = 0; cb < CB; cb++)
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                sm[(wave * RQ_TM + 16 * rb + 4 * g + r) * RS + 16 * cb + lc] = acc[rb][cb][r];
+    __syncthreads();
+    const long roff = a.row_off + (a.row_off_dev ? *a.row_off_dev : 0);
+#pragma unroll
+    for (int u = 0; u < RQ_TM * TN / 256; u++) {
+        const int idx = tid + 256 * u, row = idx / TN, cl = idx - row * TN;
+        const float* pr = sm + row * RS + cl;
+        const float v = ((pr[0] + pr[RQ_TM * RS]) + pr[2 * RQ_TM * RS]) + pr[3 * RQ_TM * RS];
+        const int gr = m0 + row, gc = n0 + cl;
+        if (gr < M && gc < N) {
+            if (KS == 1) store_out<EPI>(a, roff, gr, gc, v);
+            else a.part[((long)ks * M + gr) * N + gc] = v;
         }
     }
-    const f32x4 acc = (acc4[0] + acc4[1]) + (acc4[2] + acc4[3]);
-    // acc[r]: row m0 + 16 (w / 2) + 4 (lane / 16) + r, column n0 + 16 (w % 2) + lane % 16
-    const int col = n0 + 16 * (wave & 1) + lc;
-    if (col >= N) return;
-    const int r0 = m0 + 16 * (wave >> 1) + 4 * g;
-    if (KS == 1) {
-        const long roff = a.row_off + (a.row_off_dev ? *a.row_off_dev : 0);
-#pragma unroll
-        for (int r = 0; r < 4; r++)
-            if (r0 + r < M) store_out<EPI>(a, roff, r0 + r, col, acc[r]);
-        return;
-    }
-#pragma unroll
-    for (int r = 0; r < 4; r++)
-        if (r0 + r < M) a.part[((long)ks * M + r0 + r) * N + col] = acc[r];
 }
 
 template <int EPI>
@@ -1090,27 +1127,55 @@ hipError_t skinny_epi(const GemmArgs& a, hipStream_t s) {
     return stream_mb<EPI, 8>(a, s);
 }
 
-// k_rows for 64 < M <= 128: K split only while the 32 x 32 tiles are
-// fewer than the CUs, each range at least 4 stages (256 k), the partials
-// within a.part_cap.
-int rows_splits(const GemmArgs& a, int* KR) {
-    const int tiles = ((a.M + RW_T - 1) / RW_T) * ((a.N + RW_T - 1) / RW_T);
-    const int steps = a.K / RW_BK;
-    int KS = a.part && tiles < 256 ? std::min((256 + tiles - 1) / tiles, std::max(1, a.K / 256)) : 1;
-    while (KS > 1 && (long)KS * a.M * a.N > a.part_cap) KS--;
-    *KR = (steps + KS - 1) / KS * RW_BK;
-    return (a.K + *KR - 1) / *KR;
+// k_rows for 64 < M <= 128: the tile width TN and the K split KS with the
+// least estimated time, at most one workgroup per CU where possible. A
+// stage costs about (0.15 + 0.0075 TN) us (measured at 128 rows: 0.39 us
+// for TN = 32, 0.51 for 48); launches over the CU count take whole extra
+// rounds; K is split (ranges of at least 3 stages, partials within
+// a.part_cap) only while the tiles are fewer than half the CUs.
+struct RowsPlan {
+    int TN, KS, KR;
+};
+RowsPlan rows_plan(const GemmArgs& a) {
+    const int steps = a.K / RQ_BK, tiles_m = (a.M + RQ_TM - 1) / RQ_TM;
+    RowsPlan best{32, 1, a.K};
+    double best_t = 1e30;
+    for (const int TN : {32, 48, 64}) {
+        const int tiles = tiles_m * ((a.N + TN - 1) / TN);
+        int KS = 1;
+        if (a.part && 2 * tiles < 256) {
+            KS = std::max(1, std::min(256 / tiles, steps / 3));
+            while (KS > 1 && (long)KS * a.M * a.N > a.part_cap) KS--;
+        }
+        const int per = (steps + KS - 1) / KS;
+        KS = (steps + per - 1) / per;
+        const int rounds = (tiles * KS + 255) / 256;
+        const double t = rounds * per * (0.15 + 0.0075 * TN);
+        if (t < best_t) {
+            best_t = t;
+            best = RowsPlan{TN, KS, per * RQ_BK};
+        }
+    }
+    return best;
+}
+
+int rows_splits(const GemmArgs& a) { return rows_plan(a).KS; }
+
+template <int EPI, int TN>
+hipError_t rows_launch(const GemmArgs& a, const RowsPlan& p, hipStream_t s) {
+    const int tiles_m = (a.M + RQ_TM - 1) / RQ_TM, tiles_n = (a.N + TN - 1) / TN;
+    k_rows<EPI, TN><<<tiles_m * tiles_n * p.KS, 256, 0, s>>>(a, tiles_m, tiles_n, p.KR, p.KS);
+    return hipGetLastError();
 }
 
 template <int EPI>
 hipError_t rows_epi(const GemmArgs& a, hipStream_t s) {
-    const int tiles_m = (a.M + RW_T - 1) / RW_T, tiles_n = (a.N + RW_T - 1) / RW_T;
-    int KR;
-    const int KS = rows_splits(a, &KR);
-    k_rows<EPI><<<tiles_m * tiles_n * KS, 256, 0, s>>>(a, tiles_m, tiles_n, KR, KS);
-    const hipError_t e = hipGetLastError();
+    const RowsPlan p = rows_plan(a);
+    const hipError_t e = p.TN == 32   ? rows_launch<EPI, 32>(a, p, s)
+                         : p.TN == 48 ? rows_launch<EPI, 48>(a, p, s)
+                                      : rows_launch<EPI, 64>(a, p, s);
     if (e != hipSuccess) return e;
-    return KS == 1 ? ln_after(a, s) : reduce_splits<EPI>(a, KS, s);
+    return p.KS == 1 ? ln_after(a, s) : reduce_splits<EPI>(a, p.KS, s);
 }
 
 // The few-row products take M <= SKINNY_MAX_M rows, and up to ST_MAX_M rows
@@ -1132,7 +1197,7 @@ bool use_stream(const GemmArgs& a) {
 // Of those, the ones over more than SKINNY_MAX_M rows with K in whole
 // k_rows stages take k_rows instead of k_stream.
 bool use_rows(const GemmArgs& a) {
-    return a.M > SKINNY_MAX_M && a.K % RW_BK == 0 && use_stream(a);
+    return a.M > SKINNY_MAX_M && a.K % RQ_BK == 0 && use_stream(a);
 }
 
 // Share of the tile slots the last round of a launch fills when `res`
@@ -1317,7 +1382,7 @@ hipError_t launch_pack_w(const float* W, float* Wp, int N, int K, hipStream_t s)
 int launch_gemm_splits(const GemmArgs& a) {
     if (a.M <= 0 || a.N <= 0 || a.K <= 0 || (a.K & 3)) return 1;
     int KR;
-    if (use_rows(a)) return rows_splits(a, &KR);
+    if (use_rows(a)) return rows_splits(a);
     if (use_stream(a)) return stream_splits(a, &KR);
     return tile_splits(a, ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN), &KR);
 }

@@ -237,11 +237,13 @@ def test_softmax_error_bound_dense_grid(kat, kind):
     (0, 130, 81, 1600, 1),    # MFMA tiles, ragged edges, K = 1600 (XL)
     (0, 200, 333, 36, 2),     # register-staged tiles (K not a multiple of 16), GELU
     (0, 257, 129, 768, 3),    # direct-to-LDS BK = 32, residual
-    (0, 128, 2304, 768, 1),   # 32 x 32 tiles over M = 128 rows (k_rows), no K split
-    (0, 100, 3072, 768, 2),   # 32 x 32 tiles, ragged rows, GELU
-    (0, 128, 768, 3072, 3),   # 32 x 32 tiles with K split 3 ways, residual reduce
-    (0, 97, 1000, 1600, 3),   # 32 x 32 tiles, ragged rows and columns, K = 1600 split, residual
+    (0, 128, 2304, 768, 1),   # 32 x 48 tiles over M = 128 rows (k_rows), no K split
+    (0, 100, 3072, 768, 2),   # 32 x 48 tiles, ragged rows, GELU
+    (0, 128, 768, 3072, 3),   # 32 x 48 tiles with K split 4 ways, residual reduce
+    (0, 97, 1000, 1600, 3),   # 32 x 64 tiles, ragged rows and columns, K = 1600 split, residual
     (0, 128, 50, 64, 2),      # 32 x 32 tiles, one 64-k stage, ragged columns, GELU
+    (0, 128, 4096, 1024, 2),  # 32 x 64 tiles, 256 of them, GELU
+    (0, 120, 1024, 4096, 3),  # 32 x 64 tiles with K split 4 ways, ragged rows, residual
     (0, 256, 771, 768, 3),    # two row tiles, ragged columns, K split
     (0, 65, 50, 36, 1),       # register-staged tiles, K = 36, one tile
     (0, 2048, 768, 768, 3),   # tiles with K split (M = 2048), residual reduce
@@ -260,7 +262,7 @@ def test_softmax_error_bound_dense_grid(kat, kind):
     (2, 37, 100, 3072, 3),    # weight-streaming from packed weights, split over K
     (2, 20, 771, 1600, 2),    # packed weights, ragged last column block, GELU
     (2, 100, 333, 36, 1),     # packed, K = 36 (zero-padded last step), 128-row tiles
-    (2, 128, 2304, 768, 1),   # 128 rows: 32 x 32 tiles (the packed copy unused)
+    (2, 128, 2304, 768, 1),   # 128 rows: 32 x 48 tiles (the packed copy unused)
     (1, 2, 771, 1024, 3),     # decode product
 ])
 def test_gemm_error_bound_float64(kat, path, M, N, K, epi):
