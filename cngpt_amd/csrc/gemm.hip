@@ -781,6 +781,169 @@ __global__ void __launch_bounds__(ST_NW * 64) k_stream(GemmArgs a, int tiles_n, 
 }
 
 // Y = epi(sum over the KS partial tiles, in order); one thread per output.
+// k_gemm_wide: TM x TN tiles (TM = 128, one workgroup per CU, or 64, two),
+// whole K, for products whose 128 x 128 tiles leave a round of CUs
+// part-empty (so they ran split-K or stream-K, with partials to sum) while
+// a tile shape makes the tile count a whole number of rounds: at M = 2048
+// (one GPU's share of B=16 T=1024) GPT-2 small's QKV (2304 columns) takes
+// 128 x 144 tiles (256), fc (3072) 64 x 96 (1024), c_proj and proj (768)
+// 64 x 48 (512). Wavefront w owns rows (TM / 4) w .. and every column of
+// the tile: TM / 64 x TN / 16 blocks of v_mfma_f32_16x16x4f32. Both
+// operands go global -> LDS (lds_dma16) through a ring of S stages of 32 k
+// (the stage padded to a multiple of 32 rows, the pad loading clamped W
+// rows that nothing reads); a stage is read in two 16-k halves, each half's
+// operands read while the previous half's products issue, one wait and one
+// barrier per stage between the halves. A stage row is 8 granules of 16
+// bytes, granule slot s of row r holding k quad s ^ ((r / 2) % 8): two rows
+// share a 256-byte bank line, and the 16 rows a read instruction touches at
+// one k quad fall in 16 different 16-byte bank groups.
+constexpr int WD_BK = 32;
+
+template <int TM, int TN>
+constexpr int wd_rows() {
+    return (TM + TN + 31) / 32 * 32;
+}
+
+template <int EPI, int TM, int TN, int S>
+__global__ void __launch_bounds__(256, 128 / TM) k_gemm_wide(GemmArgs a, int tiles_m, int tiles_n) {
+    constexpr int ROWS = wd_rows<TM, TN>();  // stage rows: TM of X, TN of W, pad
+    constexpr int NI = ROWS / 32;        // load instructions per wavefront and stage
+    constexpr int STAGE = ROWS * WD_BK;  // floats per stage
+    constexpr int CB = TN / 16;          // 16-column blocks
+    constexpr int RB = TM / 64;          // 16-row blocks per wavefront
+    static_assert(TN % 16 == 0 && S >= 3 && (TM == 64 || TM == 128), "tile shape");
+    __shared__ __attribute__((aligned(1024))) float sm[S * STAGE];
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    // work id XCD-contiguous, row tiles fastest: the row tiles of a column
+    // tile share its W rows in one XCD's L2
+    const int p = xcd_order(blockIdx.x, tiles_m * tiles_n);
+    const int tm = p % tiles_m, tn = p / tiles_m;
+    const int m0 = tm * TM, n0 = tn * TN;
+    const int K = a.K, M = a.M, N = a.N;
+    const int nk = K / WD_BK;
+    // load instruction i of wavefront w covers stage rows 8 (4 i + w) ..
+    // +7: lane -> row 8 (4 i + w) + lane / 8, slot lane % 8, holding k quad
+    // slot ^ ((row / 2) % 8); rows past M or N (and the pad) read the last
+    // one (finite values; their results are not stored)
+    const float* src[NI];
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        const int row = 8 * (4 * i + wave) + (lane >> 3), slot = lane & 7;
+        const int kq = slot ^ ((row >> 1) & 7);
+        src[i] = row < TM ? a.X + (long)min(m0 + row, M - 1) * K + 4 * kq
+                          : a.W + (long)min(n0 + row - TM, N - 1) * K + 4 * kq;
+    }
+    auto issue = [&](int kt, int st) {
+        float* base = sm + st * STAGE;
+#pragma unroll
+        for (int i = 0; i < NI; i++) lds_dma16(src[i] + kt * WD_BK, base + (4 * i + wave) * 256);
+    };
+    // lane: row (column) 16 b + lane % 16 of each 16-block, k quad 4 h +
+    // lane / 16 of half h; element e of the quad is the k of the e-th
+    // product
+    const int lc = lane & 15, g = lane >> 4;
+    int ao[2][RB], bo[2][CB];
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const int q = 4 * h + g;
+#pragma unroll
+        for (int rb = 0; rb < RB; rb++) {
+            const int r = 16 * RB * wave + 16 * rb + lc;
+            ao[h][rb] = r * WD_BK + 4 * (q ^ ((r >> 1) & 7));
+        }
+#pragma unroll
+        for (int cb = 0; cb < CB; cb++) {
+            const int r = TM + 16 * cb + lc;
+            bo[h][cb] = r * WD_BK + 4 * (q ^ ((r >> 1) & 7));
+        }
+    }
+    f32x4 acc[RB][CB];
+#pragma unroll
+    for (int rb = 0; rb < RB; rb++)
+#pragma unroll
+        for (int cb = 0; cb < CB; cb++) acc[rb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    f32x4 a0[RB], b0[CB], a1[RB], b1[CB];
+    auto read = [&](int kt, int h, f32x4(&av)[RB], f32x4(&bv)[CB]) {
+        const float* base = sm + (kt % S) * STAGE;
+#pragma unroll
+        for (int rb = 0; rb < RB; rb++) av[rb] = *(const f32x4*)&base[ao[h][rb]];
+#pragma unroll
+        for (int cb = 0; cb < CB; cb++) bv[cb] = *(const f32x4*)&base[bo[h][cb]];
+    };
+    auto mul = [&](const f32x4(&av)[RB], const f32x4(&bv)[CB]) {
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+#pragma unroll
+            for (int cb = 0; cb < CB; cb++)
+#pragma unroll
+                for (int rb = 0; rb < RB; rb++)
+                    acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[rb][e], bv[cb][e], acc[rb][cb], 0, 0, 0);
+    };
+#pragma unroll
+    for (int st = 0; st < S - 1; st++)
+        if (st < nk) issue(st, st);
+    if (nk > 0) {
+        // stage 0 has landed once at most stages 1 .. S - 2 are in flight
+        if (S - 2 < nk) wait_vmcnt<NI * (S - 2)>();
+        else wait_vmcnt<0>();
+        asm volatile("s_barrier" ::: "memory");
+        read(0, 0, a0, b0);
+    }
+    for (int kt = 0; kt < nk; kt++) {
+        read(kt, 1, a1, b1);
+        mul(a0, b0);
+        if (kt + 1 < nk) {
+            // stage kt + 1 has landed once at most stages kt + 2 .. kt + S -
+            // 2 are in flight; past the barrier every wavefront has landed
+            // its part of it and is done reading stage kt - 1 (both halves'
+            // products issued before this point), which the next issue
+            // overwrites
+            if (kt + S - 2 < nk) wait_vmcnt<NI * (S - 3)>();
+            else wait_vmcnt<0>();
+            asm volatile("s_barrier" ::: "memory");
+            if (kt + S - 1 < nk) issue(kt + S - 1, (kt + S - 1) % S);
+            read(kt + 1, 0, a0, b0);
+        }
+        mul(a1, b1);
+    }
+    // acc[rb][cb][r]: row m0 + (TM / 4) w + 16 rb + 4 (lane / 16) + r, column n0 +
+    // 16 cb + lane % 16. The bias and the residual are loaded before the
+    // first store: a load after a store would wait for that store too (the
+    // vector-memory counter counts both), one round trip per element.
+    const long roff = a.row_off + (a.row_off_dev ? *a.row_off_dev : 0);
+    long yrow[RB][4];
+#pragma unroll
+    for (int rb = 0; rb < RB; rb++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int row = min(m0 + 16 * RB * wave + 16 * rb + 4 * g + r, M - 1);
+            const long orow = a.seg ? (long)(row / a.seg) * a.seg_stride + row % a.seg : row;
+            yrow[rb][r] = (orow + roff) * a.ldy;
+        }
+    float bj[CB], old[RB][CB][4];
+#pragma unroll
+    for (int cb = 0; cb < CB; cb++) {
+        const int col = min(n0 + 16 * cb + lc, N - 1);
+        bj[cb] = EPI == EPI_STORE ? 0.f : a.bias[col];
+#pragma unroll
+        for (int rb = 0; rb < RB; rb++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) old[rb][cb][r] = EPI == EPI_RESID ? a.Y[yrow[rb][r] + col] : 0.f;
+    }
+#pragma unroll
+    for (int cb = 0; cb < CB; cb++) {
+        const int col = n0 + 16 * cb + lc;
+#pragma unroll
+        for (int rb = 0; rb < RB; rb++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int row = m0 + 16 * RB * wave + 16 * rb + 4 * g + r;
+                if (row < M && col < N)
+                    a.Y[yrow[rb][r] + col] = epi_value<EPI>(acc[rb][cb][r], bj[cb], old[rb][cb][r]);
+            }
+    }
+}
+
 // k_rows: products over 64 < M <= 128 rows whose 128 x 128 tiles would
 // leave most CUs idle (the B=1 T=128 forward: 6-24 such tiles per product).
 // A workgroup of four wavefronts owns a 32-row x TN-column tile (TN = 32,
@@ -1296,6 +1459,64 @@ int sk_workgroups(const GemmArgs& a, int tiles) {
 // whole, 79.2 % with every full round whole.
 int sk_whole_rounds(int tiles, int G) { return tiles / G; }
 
+// k_gemm_wide shapes and the share of fp32 peak each reached on its own in
+// full rounds (M = 2048 and 16384): 128 x 144 0.75, 64 x 96 0.78, 64 x 48
+// 0.64 (128 x 192 and 64 x 144 reached 0.75 and 0.70 and never beat 64 x 96
+// or 128 x 144 on a GPT-2 shape). A product takes the
+// shape with the best estimate (that share times the fraction of the
+// rounds' tile slots its tiles fill, ragged edges counted as waste) when
+// that beats what the 128 x 128 tiles reach (launch_gemm timings, partial
+// sums and LayerNorm included): up to 256 of them (split K) 0.31-0.56, so
+// an estimate of 0.5 is enough; 257-576 (stream-K after whole-tile
+// rounds) 0.61-0.73, so 0.7; beyond that stream-K holds its own (fc at
+// 4096 rows: 154.5 us against 163.4 as 64 x 96 tiles), and so do products
+// whose tiles fill their rounds. CNGPT_HIP_WIDE=0 turns the path off (A/B
+// timing).
+struct WidePlan {
+    int TM, TN;
+};
+WidePlan wide_plan(const GemmArgs& a) {
+    static const bool off = [] {
+        const char* e = getenv("CNGPT_HIP_WIDE");
+        return e && e[0] == '0';
+    }();
+    static const struct {
+        int TM, TN;
+        double f;
+    } cand[] = {{128, 144, 0.75}, {64, 96, 0.78}, {64, 48, 0.64}};
+    WidePlan best{0, 0};
+    if (off || a.km || a.M <= ST_MAX_M || a.K % WD_BK) return best;
+    const long t128 = (long)((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
+    const double fill = t128 <= 256 ? t128 / 256.0 : t128 / (512.0 * ((t128 + 511) / 512));
+    if (fill >= 0.9 || t128 > 576) return best;
+    double best_e = t128 <= 256 ? 0.5 : 0.7;
+    for (const auto& c : cand) {
+        const long tiles = (long)((a.M + c.TM - 1) / c.TM) * ((a.N + c.TN - 1) / c.TN);
+        const long cap = c.TM == 128 ? 256 : 512;
+        const long rounds = (tiles + cap - 1) / cap;
+        const double e = c.f * (double)a.M * a.N / ((double)rounds * cap * c.TM * c.TN);
+        if (e > best_e) {
+            best_e = e;
+            best = WidePlan{c.TM, c.TN};
+        }
+    }
+    return best;
+}
+
+template <int EPI, int TM, int TN, int S>
+hipError_t wide_launch(const GemmArgs& a, hipStream_t s) {
+    const int tiles_m = (a.M + TM - 1) / TM, tiles_n = (a.N + TN - 1) / TN;
+    k_gemm_wide<EPI, TM, TN, S><<<tiles_m * tiles_n, 256, 0, s>>>(a, tiles_m, tiles_n);
+    const hipError_t e = hipGetLastError();
+    return e != hipSuccess ? e : ln_after(a, s);
+}
+
+template <int EPI>
+hipError_t wide_epi(const GemmArgs& a, const WidePlan& w, hipStream_t s) {
+    if (w.TM == 128) return wide_launch<EPI, 128, 144, 4>(a, s);
+    return w.TN == 96 ? wide_launch<EPI, 64, 96, 4>(a, s) : wide_launch<EPI, 64, 48, 4>(a, s);
+}
+
 // K-major operands: both (a.km == 3, the residual epilogue of the dW
 // products) or W only (a.km == 2, the stored epilogue of the dX products,
 // W the weight matrix as stored: row k = output k of the forward product):
@@ -1316,6 +1537,7 @@ template <int EPI>
 hipError_t gemm_epi(const GemmArgs& a, hipStream_t s) {
     const int tiles_m = (a.M + BM - 1) / BM, tiles_n = (a.N + BN - 1) / BN;
     const int tiles = tiles_m * tiles_n, cus = 256;
+    if (const WidePlan w = wide_plan(a); w.TM) return wide_epi<EPI>(a, w, s);
     int KR;
     const int KS = tile_splits(a, tiles, &KR);
     if (KS > 1) {
@@ -1384,6 +1606,7 @@ int launch_gemm_splits(const GemmArgs& a) {
     int KR;
     if (use_rows(a)) return rows_splits(a);
     if (use_stream(a)) return stream_splits(a, &KR);
+    if (wide_plan(a).TM) return 1;
     return tile_splits(a, ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN), &KR);
 }
 

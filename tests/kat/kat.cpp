@@ -103,8 +103,9 @@ int kat_gemm(const float* X, const float* W, const float* bias, float* Y, int M,
 }
 
 // Y[M,N] += X . W^T + bias (launch_gemm), and lnout = LayerNorm(Y rows)
-// with gains lnw and biases lnb, formed by the split sum when K is split;
-// returns the splits (> 1: the sum formed the LayerNorm), -1 on failure.
+// with gains lnw and biases lnb, formed by the split sum when K is split,
+// else by a LayerNorm launch after the product; returns the splits (> 1:
+// the sum formed the LayerNorm), -1 on failure.
 int kat_gemm_ln(const float* X, const float* W, const float* bias, float* Y, const float* lnw,
                 const float* lnb, float* lnout, int M, int N, int K) {
     if (M <= 0 || N <= 0 || K <= 0) return fail("bad shape");
@@ -124,10 +125,8 @@ int kat_gemm_ln(const float* X, const float* W, const float* bias, float* Y, con
     a.M = M; a.N = N; a.K = K; a.ldy = N;
     a.epi = EPI_RESID;
     a.part = part; a.part_cap = 1 << 24;
+    a.ln_w = dlw; a.ln_b = dlb; a.ln_out = dln;
     const int splits = launch_gemm_splits(a);
-    if (splits > 1) {
-        a.ln_w = dlw; a.ln_b = dlb; a.ln_out = dln;
-    }
     TRY(launch_gemm(a, nullptr));
     TRY(hipDeviceSynchronize());
     TRY(hipMemcpy(Y, dy, (size_t)M * N * sizeof(float), hipMemcpyDeviceToHost));

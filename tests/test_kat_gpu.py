@@ -246,9 +246,13 @@ def test_softmax_error_bound_dense_grid(kat, kind):
     (0, 120, 1024, 4096, 3),  # 32 x 64 tiles with K split 4 ways, ragged rows, residual
     (0, 256, 771, 768, 3),    # two row tiles, ragged columns, K split
     (0, 65, 50, 36, 1),       # register-staged tiles, K = 36, one tile
-    (0, 2048, 768, 768, 3),   # tiles with K split (M = 2048), residual reduce
-    (0, 2048, 768, 3072, 3),  # tiles with K split 5 ways (M = 2048), residual reduce
-    (0, 2048, 2304, 768, 1),  # stream-K: 288 tiles over 512 workgroups, fixup
+    (0, 2048, 768, 768, 3),   # 64 x 48 tiles, two per CU (M = 2048), residual
+    (0, 2048, 768, 3072, 3),  # 64 x 48 tiles over K = 3072, residual
+    (0, 2048, 3072, 768, 2),  # 64 x 96 tiles, two rounds at two per CU, GELU
+    (0, 1000, 2304, 768, 1),  # 64 x 96 tiles, ragged rows
+    (0, 4096, 2304, 768, 1),  # 64 x 96 tiles, three rounds at two per CU
+    (0, 1024, 768, 768, 3),   # 128 x 128 tiles with K split (M = 1024), residual reduce
+    (0, 2048, 2304, 768, 1),  # 128 x 144 tiles, one per CU
     (0, 1100, 4000, 1600, 3), # stream-K: 9 x 32 ragged tiles, residual
     (0, 1280, 7680, 256, 3),  # 600 tiles over 256 workgroups: a whole-tile round, then stream-K
     (0, 1000, 19400, 64, 2),  # 8 x 152 ragged tiles over 512 workgroups: whole-tile round, GELU
@@ -323,6 +327,17 @@ def test_gemm_layernorm_in_split_sum(kat, M, N, K):
     (the sum launch over whole rows): the residual stream within the float64
     error bound, and the LayerNorm within 1e-5 of a float64 LayerNorm of the
     float32 rows."""
+    check_gemm_layernorm(kat, M, N, K, split=True)
+
+
+@pytest.mark.parametrize("M,N,K", [(2048, 768, 3072), (2048, 768, 768)])
+def test_gemm_layernorm_after_whole_k(kat, M, N, K):
+    """The same product and LayerNorm where the product runs whole K (64 x 48
+    tiles at 2048 rows) and the LayerNorm is a launch of its own."""
+    check_gemm_layernorm(kat, M, N, K, split=False)
+
+
+def check_gemm_layernorm(kat, M, N, K, split):
     rng = np.random.default_rng(13 * M + N + K)
     X = rng.standard_normal((M, K)).astype(np.float32)
     W = (0.02 * rng.standard_normal((N, K))).astype(np.float32)
@@ -333,7 +348,8 @@ def test_gemm_layernorm_in_split_sum(kat, M, N, K):
     Y = Y0.copy()
     ln = np.zeros((M, N), np.float32)
     splits = kat.kat_gemm_ln(fp(X), fp(W), fp(b), fp(Y), fp(lw), fp(lb), fp(ln), M, N, K)
-    assert splits > 1, kat.kat_error().decode()
+    assert splits > 0, kat.kat_error().decode()
+    assert (splits > 1) == split, splits
     acc = X.astype(np.float64) @ W.astype(np.float64).T
     mag = np.abs(X.astype(np.float64)) @ np.abs(W.astype(np.float64)).T + np.abs(b) + np.abs(Y0)
     assert np.all(np.abs(Y - ((Y0 + acc) + b)) <= (K + 4) * U * mag + TINY)
