@@ -389,6 +389,7 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
     int tok = *a.tok;
     constexpr bool samp = SAMP;  // the greedy instantiation carries no sampling code
     const float tdiv = a.temp > 0.0f ? a.temp : 1.0f;
+    const float scale2 = a.scale * 1.4426950408889634f;
     // Two weight buffers of UPW * U float4 per lane, NJQ * U of them the
     // QKV or fc columns, U the c_proj column, 4U the proj column:
     //   wa[0, 2U): QKV (A), then fc (D)      wa[2U, 4U): proj, first half (E)
@@ -637,9 +638,12 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
                     for (int i = 0; i < 4; i++) d += dot4(qv[i], isnew ? kv4[i] : kq[i]);
                     d += CNGPT_DPP(d, 0xB1);  // the 4 lanes of a key: xor 1, xor 2
                     d += CNGPT_DPP(d, 0x4E);
-                    const float sc = valid ? d * a.scale : -INFINITY;
+                    // scores in base 2 (scale * log2 e folded in), so that
+                    // every exponential of the attention and its merges is
+                    // one v_exp_f32
+                    const float sc = valid ? d * scale2 : -INFINITY;
                     const float m = wave_max_dpp(sc);
-                    const float e = valid ? expf(sc - m) : 0.f;
+                    const float e = valid ? __builtin_amdgcn_exp2f(sc - m) : 0.f;
                     const float ls = wave_sum_dpp(dq == 0 ? e : 0.f);
                     // keys past kw1 have e = 0 (and finite cached values), so
                     // they add exact zeros
@@ -671,7 +675,7 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
                     float Ls = 0.f, O = 0.f;
 #pragma unroll
                     for (int v = 0; v < PW; v++) {
-                        const float f = mv[v] == -INFINITY ? 0.f : expf(mv[v] - M);
+                        const float f = mv[v] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mv[v] - M);
                         Ls += lv[v] * f;
                         O += ov[v] * f;
                     }
@@ -740,7 +744,7 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
                     }
                 }
                 if (!settle(ok)) return;
-                // merge: each head's split weights exp(m_s - M) / L, formed
+                // merge: each head's split weights 2^(m_s - M) / L (m in base 2), formed
                 // once (in place of the m values) by one thread per head,
                 // then every channel the weighted sum of its head's splits
                 if (tid < H) {
@@ -750,10 +754,10 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
                     for (int sp = 0; sp < ns; sp++) M = fmaxf(M, mh[sp]);
                     float Ls = 0.f;
                     for (int sp = 0; sp < ns; sp++)
-                        Ls += lh[sp] * (mh[sp] == -INFINITY ? 0.f : expf(mh[sp] - M));
+                        Ls += lh[sp] * (mh[sp] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mh[sp] - M));
                     const float inv = 1.0f / Ls;
                     for (int sp = 0; sp < ns; sp++)
-                        mh[sp] = (mh[sp] == -INFINITY ? 0.f : expf(mh[sp] - M)) * inv;
+                        mh[sp] = (mh[sp] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mh[sp] - M)) * inv;
                 }
                 __syncthreads();
                 for (int e = tid; e < C; e += PT) {
