@@ -88,6 +88,7 @@ EXPORTS = [
     "cngpt_hip_train_create", "cngpt_hip_train_destroy", "cngpt_hip_train_forward",
     "cngpt_hip_train_backward", "cngpt_hip_train_zero_grad", "cngpt_hip_train_adamw",
     "cngpt_hip_train_read", "cngpt_hip_train_write", "cngpt_hip_train_steps",
+    "cngpt_hip_train_set_dropout",
     "fast_init", "fast_free", "fast_set_threads", "gpt_forward_fast", "gpt_forward_fast_all",
     "fast_params_changed", "fast_last_error",
     "gpt_num_params", "gpt_init", "gpt_init_weights", "gpt_load", "gpt_save", "gpt_free",
@@ -151,6 +152,7 @@ def lib():
     L.cngpt_hip_train_forward.argtypes = [_VP, _I, _I, _F]
     L.cngpt_hip_train_backward.argtypes = [_VP]
     L.cngpt_hip_train_zero_grad.argtypes = [_VP]
+    L.cngpt_hip_train_set_dropout.argtypes = [_VP, ctypes.c_float]
     L.cngpt_hip_train_adamw.argtypes = [_VP] + [ctypes.c_float] * 6 + [_F]
     L.cngpt_hip_train_read.argtypes = [_VP, ctypes.c_int, _F, ctypes.c_long]
     L.cngpt_hip_train_write.argtypes = [_VP, ctypes.c_int, _F, ctypes.c_long]
@@ -493,6 +495,12 @@ class Trainer:
 
     def backward(self) -> None:                         # model.c:634-877
         _check(lib().cngpt_hip_train_backward(self._t), "train_backward")
+
+    def set_dropout(self, p: float) -> None:
+        """GPTConfig.dropout (model.h:43): with p > 0 each forward draws its
+        keep masks with the process's rand() in model.c's order and applies
+        the residual-stream dropout of model.c:471-599 (and its backward)."""
+        _check(lib().cngpt_hip_train_set_dropout(self._t, ctypes.c_float(p)), "train_set_dropout")
 
     def zero_grad(self) -> None:                        # model.c:879-886
         _check(lib().cngpt_hip_train_zero_grad(self._t), "train_zero_grad")

@@ -255,6 +255,10 @@ hipError_t launch_cross_entropy(float* logits, long rows, int V, const int* targ
 // out = gelu(in); d = d * gelu'(x) (n a multiple of 4).
 hipError_t launch_gelu_fwd(const float* in, float* out, long n, hipStream_t s);
 hipError_t launch_gelu_bwd(float* d, const float* x, long n, hipStream_t s);
+// x[i] *= mask[i] ? scale : 0 (dropout_fwd / dropout_bwd's scaling, the
+// bytes of mask 0 or 1; n a multiple of 4, mask 4-byte aligned).
+hipError_t launch_dropout(float* x, const unsigned char* mask, long n, float scale,
+                          hipStream_t s);
 // dst [cols_p][ldd] = src [rows][lds]^T, zero in the padding (rows <= rows_p
 // <= ldd, cols <= cols_p).
 hipError_t launch_transpose(const float* src, long lds, int rows, int cols, float* dst, long ldd,

@@ -24,6 +24,23 @@ __global__ void __launch_bounds__(256) k_gelu_fwd(const f32x4* __restrict__ in,
     out[i] = f32x4{gelu_tanh(v.x), gelu_tanh(v.y), gelu_tanh(v.z), gelu_tanh(v.w)};
 }
 
+// x[i] *= mask[i] ? scale : 0, over n4 groups of 4: dropout_fwd's scaling
+// of the kept values and dropout_bwd's of the gradient (reference
+// ops.c:603-625), the same product in both, with the mask drawn on the host.
+__global__ void __launch_bounds__(256) k_dropout(f32x4* __restrict__ x,
+                                                 const unsigned* __restrict__ mask, long n4,
+                                                 float scale) {
+    const long i = (long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n4) return;
+    const unsigned m = mask[i];  // four mask bytes, element j in byte j
+    f32x4 v = x[i];
+    v.x *= (m & 0xffu) ? scale : 0.0f;
+    v.y *= (m & 0xff00u) ? scale : 0.0f;
+    v.z *= (m & 0xff0000u) ? scale : 0.0f;
+    v.w *= (m & 0xff000000u) ? scale : 0.0f;
+    x[i] = v;
+}
+
 // d gelu / dx of the tanh form (reference ops.c:347-355): 0.5 (1 + t) +
 // 0.5 x (1 - t^2) u'(x), t = tanh(u), u = sqrt(2/pi) (x + 0.044715 x^3).
 __device__ __forceinline__ float gelu_grad(float x) {
@@ -333,6 +350,16 @@ hipError_t launch_gelu_fwd(const float* in, float* out, long n, hipStream_t s) {
     if (n & 3) return hipErrorInvalidValue;
     const long n4 = n >> 2;
     k_gelu_fwd<<<(unsigned)((n4 + 255) / 256), 256, 0, s>>>((const f32x4*)in, (f32x4*)out, n4);
+    return hipGetLastError();
+}
+
+hipError_t launch_dropout(float* x, const unsigned char* mask, long n, float scale,
+                          hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    if (n & 3) return hipErrorInvalidValue;
+    const long n4 = n >> 2;
+    k_dropout<<<(unsigned)((n4 + 255) / 256), 256, 0, s>>>((f32x4*)x, (const unsigned*)mask, n4,
+                                                           scale);
     return hipGetLastError();
 }
 

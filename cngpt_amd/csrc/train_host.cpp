@@ -87,6 +87,14 @@ struct cngpt_hip_train {
     double* nparts = nullptr;
     float *norm = nullptr, *coef = nullptr;
     bool have_fwd = false;
+
+    // GPTConfig.dropout (model.h:43): the keep masks of the last forward,
+    // [1 + 2 L][B T C] bytes (the embedding, then res1 and res2 of each
+    // layer), drawn on the host with rand() in model.c's order
+    float dropout = 0.f;
+    unsigned char* masks = nullptr;
+    std::vector<unsigned char> hmasks;
+    bool dropped = false;
 };
 
 namespace {
@@ -324,7 +332,26 @@ void cngpt_hip_train_destroy(cngpt_hip_train* t) {
     (void)hipSetDevice(t->device);
     (void)hipDeviceSynchronize();
     if (t->arena) (void)hipFree(t->arena);
+    if (t->masks) (void)hipFree(t->masks);
     delete t;
+}
+
+int cngpt_hip_train_set_dropout(cngpt_hip_train* t, float p) {
+    CtxView v;
+    if (view_of(t, &v)) return -1;
+    if (!(p >= 0.f) || !(p < 1.f)) return ctx_fail("dropout rate %g outside [0, 1)", (double)p);
+    if (p > 0.f && !t->masks) {
+        const size_t n = (size_t)(1 + 2 * t->cfg.n_layer) * t->N * t->cfg.n_embd;
+        TRY(hipSetDevice(t->device));
+        if (hipMalloc(&t->masks, n) != hipSuccess) {
+            (void)hipGetLastError();
+            t->masks = nullptr;
+            return ctx_fail("dropout mask allocation of %zu bytes failed", n);
+        }
+        t->hmasks.resize(n);
+    }
+    t->dropout = p;
+    return 0;
 }
 
 int cngpt_hip_train_forward(cngpt_hip_train* t, const int* tokens, const int* targets,
@@ -358,7 +385,27 @@ int cngpt_hip_train_forward(cngpt_hip_train* t, const int* tokens, const int* ta
                        s));
     TRY(hipMemcpyAsync(t->upos, order.data(), N * sizeof(int), hipMemcpyHostToDevice, s));
 
+    // dropout (model.c:450: in every forward with targets when the rate is
+    // set): dropout_fwd's draws (ops.c:603-618), one rand() per element,
+    // kept when it exceeds p * RAND_MAX, for the embedding and then res1
+    // and res2 of each layer; then the keep masks go to the device
+    const float p = t->dropout;
+    const bool drop = p > 0.f;
+    const long NC = N * C;
+    const float dscale = drop ? 1.0f / (1.0f - p) : 1.0f;
+    if (drop) {
+        unsigned char* hm = t->hmasks.data();
+        const size_t n = t->hmasks.size();
+        for (size_t i = 0; i < n; i++) {
+            const unsigned int r = (unsigned int)rand();
+            hm[i] = r > (unsigned int)(p * (float)RAND_MAX) ? 1 : 0;
+        }
+        TRY(hipMemcpyAsync(t->masks, hm, n, hipMemcpyHostToDevice, s));
+    }
+    t->dropped = drop;
+
     TRY(launch_embed(t->tok, v.wte, v.wpe, t->emb, N, T, C, V, 0, nullptr, t->err, nullptr, 0, s));
+    if (drop) TRY(launch_dropout(t->emb, t->masks, NC, dscale, s));   // model.c:471-472
     const float* x = t->emb;
     const size_t xbytes = (size_t)N * C * sizeof(float);
     for (int l = 0; l < c.n_layer; l++) {
@@ -370,12 +417,14 @@ int cngpt_hip_train_forward(cngpt_hip_train* t, const int* tokens, const int* ta
         TRY(launch_attention_causal(a.qkv, T, a.attn_out, B, T, C, H, s, a.lse));
         TRY(hipMemcpyAsync(a.res1, x, xbytes, hipMemcpyDeviceToDevice, s));
         if (gemm(t, s, a.attn_out, w.proj_w, w.proj_b, a.res1, N, C, C, EPI_RESID)) return -1;
+        if (drop) TRY(launch_dropout(a.res1, t->masks + (1 + 2 * l) * NC, NC, dscale, s));
         TRY(launch_layernorm(a.res1, C, w.ln2_w, w.ln2_b, a.ln2_out, C, (int)N, C, s, a.ln2_mean,
                              a.ln2_rstd));
         if (gemm(t, s, a.ln2_out, w.fc_w, w.fc_b, a.fc_out, N, 4 * C, C, EPI_BIAS)) return -1;
         TRY(launch_gelu_fwd(a.fc_out, a.gelu, N * 4 * C, s));
         TRY(hipMemcpyAsync(a.res2, a.res1, xbytes, hipMemcpyDeviceToDevice, s));
         if (gemm(t, s, a.gelu, w.mlp_w, w.mlp_b, a.res2, N, C, 4 * C, EPI_RESID)) return -1;
+        if (drop) TRY(launch_dropout(a.res2, t->masks + (2 + 2 * l) * NC, NC, dscale, s));
         x = a.res2;
     }
     TRY(launch_layernorm(x, C, v.lnf_w, v.lnf_b, t->lnf_out, C, (int)N, C, s, t->lnf_mean,
@@ -406,6 +455,9 @@ int cngpt_hip_train_backward(cngpt_hip_train* t) {
     const long N = t->N;
     hipStream_t s = v.stream;
     const size_t xbytes = (size_t)N * C * sizeof(float);
+    const long NC = N * C;
+    const bool drop = t->dropped;
+    const float dscale = drop ? 1.0f / (1.0f - t->dropout) : 1.0f;
 
     // dlogits = (probs - onehot) / (B T) (model.c:660-666) was formed by the
     // forward's loss pass; the tied lm_head: d ln_f = dlogits . wte,
@@ -424,6 +476,8 @@ int cngpt_hip_train_backward(cngpt_hip_train* t) {
         const LayerW& w = v.layers[l];
         const TrainLayer& a = t->acts[l];
         const float* x_in = l > 0 ? t->acts[l - 1].res2 : t->emb;
+        // dropout_bwd (ops.c:620-625) of res2 (model.c:699-700)
+        if (drop) TRY(launch_dropout(t->d_x, t->masks + (2 + 2 * l) * NC, NC, dscale, s));
         TRY(hipMemcpyAsync(t->d_res1, t->d_x, xbytes, hipMemcpyDeviceToDevice, s));
         // proj: Y = gelu . mlp_w^T + b
         if (linear_dx(t, s, t->d_x, w.mlp_w, t->d_hid, C, 4 * C) ||
@@ -439,6 +493,8 @@ int cngpt_hip_train_backward(cngpt_hip_train* t) {
         TRY(launch_layernorm_bwd(t->d_ln, a.res1, w.ln2_w, a.ln2_mean, a.ln2_rstd, t->d_res1,
                                  grad_of(t, v, w.ln2_w), grad_of(t, v, w.ln2_b), (int)N, C, t->red,
                                  s));
+        // and of res1 (model.c:732-733)
+        if (drop) TRY(launch_dropout(t->d_res1, t->masks + (1 + 2 * l) * NC, NC, dscale, s));
         // c_proj: Y = attn_out . proj_w^T + b
         if (linear_dx(t, s, t->d_res1, w.proj_w, t->d_attn, C, C) ||
             linear_dw(t, s, t->d_res1, C, a.attn_out, grad_of(t, v, w.proj_w),
@@ -456,6 +512,8 @@ int cngpt_hip_train_backward(cngpt_hip_train* t) {
                                  grad_of(t, v, w.ln1_w), grad_of(t, v, w.ln1_b), (int)N, C, t->red,
                                  s));
     }
+    // and of the embedding (model.c:849-850)
+    if (drop) TRY(launch_dropout(t->d_x, t->masks, NC, dscale, s));
     TRY(launch_embed_bwd(t->d_x, B, T, C, grad_of(t, v, v.wpe), grad_of(t, v, v.wte), t->uniq,
                          t->ustart, t->upos, t->nuniq, s));
     TRY(hipGetLastError());

@@ -232,8 +232,9 @@ int  cngpt_hip_init_weights(const cngpt_hip_config *cfg, float *params, unsigned
  * gpt_backward (GPTActivations, src/model.h:86-115, with each attention's
  * log-sum-exp in place of its T x T probabilities), the gradients
  * (GPTGrads) and the AdamW moments (m_buf, v_buf, decay_buf,
- * src/model.h:120-141). Dropout is not supported (the default of
- * `cngpt train`, src/cngpt.c:94): the configuration carries none.
+ * src/model.h:120-141). The configuration carries no dropout rate:
+ * cngpt_hip_train_set_dropout sets GPTConfig.dropout for the trainer (0,
+ * the default of `cngpt train`, src/cngpt.c:94, until then).
  * ------------------------------------------------------------------ */
 typedef struct cngpt_hip_train cngpt_hip_train;
 
@@ -252,6 +253,16 @@ int  cngpt_hip_train_forward(cngpt_hip_train *t, const int *tokens, const int *t
 /* gpt_backward (model.c:634-877) for the last forward: gradients add to
  * the held ones, as in the reference. */
 int  cngpt_hip_train_backward(cngpt_hip_train *t);
+
+/* GPTConfig.dropout (src/model.h:43) for this trainer's forwards, p in
+ * [0, 1): with p > 0 every cngpt_hip_train_forward draws the keep masks of
+ * dropout_fwd (src/ops.c:603-618) with the process's rand(), one call per
+ * element in model.c's order (the embedding, then res1 and res2 of each
+ * layer: model.c:471-472, 572-574, 597-599; (1 + 2 n_layer) B T n_embd
+ * draws), as the reference's gpt_forward with targets does, applies them on
+ * the device, and the backward applies dropout_bwd at model.c:699-700,
+ * 732-733 and 849-850. Allocates the masks' device bytes on first use. */
+int  cngpt_hip_train_set_dropout(cngpt_hip_train *t, float p);
 
 /* gpt_zero_grad (model.c:879-886). */
 int  cngpt_hip_train_zero_grad(cngpt_hip_train *t);

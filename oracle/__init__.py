@@ -128,6 +128,10 @@ def lib():
     L.orc_train_forward.argtypes = [ctypes.c_void_p, _F, _I, _I]
     L.orc_train_forward.restype = ctypes.c_float
     L.orc_train_backward.argtypes = [ctypes.c_void_p, _F, _I, _I, _F]
+    L.orc_train_set_dropout.argtypes = [ctypes.c_void_p, ctypes.c_float]
+    L.orc_train_masks.argtypes = [ctypes.c_void_p]
+    L.orc_train_masks.restype = ctypes.POINTER(ctypes.c_ubyte)
+    L.orc_dropout_fwd.argtypes = [_F, ctypes.POINTER(ctypes.c_ubyte), ctypes.c_long, ctypes.c_float]
     L.orc_adamw.argtypes = [ctypes.POINTER(OrcCfg), _F, _F, _F, _F, i, ctypes.c_float,
                             ctypes.c_float, ctypes.c_float, ctypes.c_float, ctypes.c_float,
                             ctypes.c_float]
@@ -359,11 +363,28 @@ class Trainer:
     def zero_grad(self):                                # model.c:879-886
         self.grads[:] = 0
 
+    def set_dropout(self, p: float) -> None:
+        """GPTConfig.dropout: the residual-stream dropout of the training
+        forwards (model.c:450-472, 572-599), rand() draws in model.c's order."""
+        if lib().orc_train_set_dropout(self._t, p) != 0:
+            raise ValueError(f"dropout rate {p} outside [0, 1)")
+        self.dropout = p
+
+    def masks(self) -> np.ndarray:
+        """The last forward's keep masks, [1 + 2 L, B T C] (the embedding,
+        then res1 and res2 of each layer)."""
+        n = (1 + 2 * self.cfg.n_layer) * self.B * self.T * self.cfg.n_embd
+        return np.ctypeslib.as_array(lib().orc_train_masks(self._t), shape=(n,)).reshape(
+            1 + 2 * self.cfg.n_layer, -1).copy()
+
     def forward(self, tokens, targets) -> float:        # model.c:442-625
+        """The loss, or 0 with targets None (no loss, no dropout)."""
         tokens = np.ascontiguousarray(tokens, np.int32).reshape(-1)
-        targets = np.ascontiguousarray(targets, np.int32).reshape(-1)
+        if targets is not None:
+            targets = np.ascontiguousarray(targets, np.int32).reshape(-1)
         self._tok, self._tgt = tokens, targets
-        return float(lib().orc_train_forward(self._t, _fp(self.params), _ip(tokens), _ip(targets)))
+        tp = _ip(targets) if targets is not None else None
+        return float(lib().orc_train_forward(self._t, _fp(self.params), _ip(tokens), tp))
 
     def backward(self):                                 # model.c:634-877
         lib().orc_train_backward(self._t, _fp(self.params), _ip(self._tok), _ip(self._tgt),

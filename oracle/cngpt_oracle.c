@@ -555,8 +555,29 @@ float orc_cross_entropy(const float *logits, const int *targets, float *probs,
 /* ------------------------------------------------------------------ */
 /* Training: gpt_forward with targets, gpt_backward, gpt_adamw         */
 /* (src/model.c:442-921) and the backward ops of src/ops.c, scalar     */
-/* paths. Dropout 0, the default of `cngpt train` (src/cngpt.c:94).    */
+/* paths, with the residual-stream dropout of model.c:471-472,         */
+/* 572-574, 597-599 when a rate is set (orc_train_set_dropout).        */
 /* ------------------------------------------------------------------ */
+
+/* dropout_fwd (ops.c:603-618): one rand() per element, kept when it
+ * exceeds p * RAND_MAX, kept values scaled by 1 / (1 - p). */
+void orc_dropout_fwd(float *x, unsigned char *mask, long n, float p)
+{
+    const float scale = 1.0f / (1.0f - p);
+    for (long i = 0; i < n; i++) {
+        const unsigned int r = (unsigned int)rand();
+        const unsigned char keep = (r > (unsigned int)(p * (float)RAND_MAX)) ? 1 : 0;
+        mask[i] = keep;
+        x[i] *= keep ? scale : 0.0f;
+    }
+}
+
+/* dropout_bwd (ops.c:620-625). */
+void orc_dropout_bwd(float *dx, const unsigned char *mask, long n, float p)
+{
+    const float scale = 1.0f / (1.0f - p);
+    for (long i = 0; i < n; i++) dx[i] *= mask[i] ? scale : 0.0f;
+}
 
 void orc_linear_bwd_dx(const float *dY, const float *W, float *dX, int M, int K, int N)
 {                                                       /* ops.c:125-133 */
@@ -623,6 +644,9 @@ struct orc_train {
     float *emb, *ln_f_out, *ln_f_mean, *ln_f_rstd, *logits, *probs;
     float **ln1_out, **ln1_mean, **ln1_rstd, **qkv, **attn_probs, **attn_out, **attn_proj;
     float **res1, **ln2_out, **ln2_mean, **ln2_rstd, **fc_out, **gelu, **mlp_out, **res2;
+    float dropout;                   /* GPTConfig.dropout (model.h:43); 0: none */
+    unsigned char *masks;            /* [1 + 2 L][B T C]: emb, then res1, res2 per layer */
+    int dropped;                     /* the last forward applied them */
 };
 
 static float **alloc_layers(int L, size_t n, int *ok)
@@ -651,8 +675,22 @@ void orc_train_free(orc_train *t)
                       t->attn_proj, t->res1, t->ln2_out, t->ln2_mean, t->ln2_rstd, t->fc_out,
                       t->gelu, t->mlp_out, t->res2 };
     for (size_t i = 0; i < sizeof(all) / sizeof(all[0]); i++) free_layers(all[i], L);
+    free(t->masks);
     free(t);
 }
+
+int orc_train_set_dropout(orc_train *t, float p)
+{
+    if (!t || !(p >= 0.0f) || !(p < 1.0f)) return -1;
+    if (p > 0.0f && !t->masks) {
+        const size_t n = (size_t)(1 + 2 * t->c.n_layer) * t->B * t->T * t->c.n_embd;
+        if (!(t->masks = malloc(n))) return -1;
+    }
+    t->dropout = p;
+    return 0;
+}
+
+const unsigned char *orc_train_masks(const orc_train *t) { return t ? t->masks : NULL; }
 
 orc_train *orc_train_new(const orc_cfg *c, int B, int T)
 {                                                       /* model.c:333-440 */
@@ -719,6 +757,11 @@ float orc_train_forward(orc_train *t, const float *params, const int *tokens, co
             float *d = t->emb + ((size_t)b * T + p) * C;
             for (int k = 0; k < C; k++) d[k] = e[k] + q[k];
         }
+    /* model.c:450: dropout only in a forward with targets */
+    const int drop = targets != NULL && t->dropout > 0.0f;
+    const size_t NC = N * (size_t)C;
+    t->dropped = drop;
+    if (drop) orc_dropout_fwd(t->emb, t->masks, (long)NC, t->dropout);   /* model.c:471-472 */
     const float *x = t->emb;
     const float scale = 1.0f / sqrtf((float)hs);
     for (int l = 0; l < L; l++) {
@@ -746,12 +789,16 @@ float orc_train_forward(orc_train *t, const float *params, const int *tokens, co
             }
         linear_seq(t->attn_out[l], params + o[4], params + o[5], t->attn_proj[l], (int)N, C, C);
         for (size_t i = 0; i < N * C; i++) t->res1[l][i] = x[i] + t->attn_proj[l][i];   /* :572-573 */
+        if (drop) orc_dropout_fwd(t->res1[l], t->masks + (1 + 2 * (size_t)l) * NC, (long)NC,
+                                  t->dropout);                              /* :573-574 */
         orc_layernorm(t->res1[l], params + o[6], params + o[7], t->ln2_out[l], t->ln2_mean[l],
                       t->ln2_rstd[l], (int)N, C);
         linear_seq(t->ln2_out[l], params + o[8], params + o[9], t->fc_out[l], (int)N, C, 4 * C);
         orc_gelu(t->fc_out[l], t->gelu[l], (int)(N * 4 * C));
         linear_seq(t->gelu[l], params + o[10], params + o[11], t->mlp_out[l], (int)N, 4 * C, C);
         for (size_t i = 0; i < N * C; i++) t->res2[l][i] = t->res1[l][i] + t->mlp_out[l][i];  /* :597-598 */
+        if (drop) orc_dropout_fwd(t->res2[l], t->masks + (2 + 2 * (size_t)l) * NC, (long)NC,
+                                  t->dropout);                              /* :598-599 */
         x = t->res2[l];
     }
     const long *of = off + 2 + 12 * L;                    /* model.c:608-614 */
@@ -797,6 +844,8 @@ void orc_train_backward(orc_train *t, const float *params, const int *tokens, co
     for (int l = L - 1; l >= 0; l--) {                    /* model.c:690-857 */
         const long *o = off + 2 + 12 * l;
         const float *x_in = l == 0 ? t->emb : t->res2[l - 1];
+        if (t->dropped)                                   /* model.c:699-700 */
+            orc_dropout_bwd(d_x, t->masks + (2 + 2 * (size_t)l) * N * C, (long)(N * C), t->dropout);
         memcpy(d_res1, d_x, N * C * sizeof(float));
         memset(d_gelu, 0, N * 4 * C * sizeof(float));
         orc_linear_bwd_dx(d_x, params + o[10], d_gelu, (int)N, 4 * C, C);
@@ -808,6 +857,9 @@ void orc_train_backward(orc_train *t, const float *params, const int *tokens, co
         orc_linear_bwd_dw(d_mlp4, t->ln2_out[l], grads + o[8], grads + o[9], (int)N, C, 4 * C);
         orc_layernorm_bwd(d_ln2, t->res1[l], params + o[6], t->ln2_mean[l], t->ln2_rstd[l],
                           d_res1, grads + o[6], grads + o[7], (int)N, C);
+        if (t->dropped)                                   /* model.c:732-733 */
+            orc_dropout_bwd(d_res1, t->masks + (1 + 2 * (size_t)l) * N * C, (long)(N * C),
+                            t->dropout);
         memset(d_attn_o, 0, N * C * sizeof(float));
         orc_linear_bwd_dx(d_res1, params + o[4], d_attn_o, (int)N, C, C);
         orc_linear_bwd_dw(d_res1, t->attn_out[l], grads + o[4], grads + o[5], (int)N, C, C);
@@ -857,6 +909,7 @@ void orc_train_backward(orc_train *t, const float *params, const int *tokens, co
                           grads + o[0], grads + o[1], (int)N, C);
         for (size_t i = 0; i < N * C; i++) d_x[i] += d_res1[i];
     }
+    if (t->dropped) orc_dropout_bwd(d_x, t->masks, (long)(N * C), t->dropout);  /* model.c:849-850 */
     for (int b = 0; b < B; b++)                           /* model.c:850-866 */
         for (int p = 0; p < T; p++) {
             const float *dr = d_x + ((size_t)b * T + p) * C;

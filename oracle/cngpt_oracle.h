@@ -112,6 +112,14 @@ float orc_train_forward(orc_train *t, const float *params, const int *tokens, co
  * params). */
 void orc_train_backward(orc_train *t, const float *params, const int *tokens, const int *targets,
                         float *grads);
+/* GPTConfig.dropout for the training forwards (model.c:450): p in [0, 1);
+ * the masks of the last forward, [1 + 2 L][B T C] bytes (the embedding,
+ * then res1 and res2 of each layer), drawn with rand() in model.c's order. */
+int orc_train_set_dropout(orc_train *t, float p);
+const unsigned char *orc_train_masks(const orc_train *t);
+/* dropout_fwd / dropout_bwd (src/ops.c:603-625). */
+void orc_dropout_fwd(float *x, unsigned char *mask, long n, float p);
+void orc_dropout_bwd(float *dx, const unsigned char *mask, long n, float p);
 /* gpt_adamw (src/model.c:888-921) with the step count already advanced:
  * clips grads in place to grad_clip by their global norm (if > 0), then
  * the AdamW update of params, m and v; weight decay on the matrices and

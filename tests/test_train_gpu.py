@@ -257,3 +257,59 @@ def test_errors():
                 tr.forward(tok, bad)
             with pytest.raises(cngpt_amd.CngptError, match="load_params"):
                 tr.write(cngpt_amd.TRAIN_PARAMS, params)
+
+
+@pytest.mark.parametrize("name,p", [("tiny", 0.1), ("hs64", 0.3), ("gpt2_width", 0.1)])
+def test_dropout_vs_oracle(name, p):
+    """GPTConfig.dropout: the same rand() stream (srand before each side)
+    gives the device and the oracle the same keep masks at model.c's three
+    sites; two steps, so the second forward's masks continue the stream."""
+    cfg, B, T = CASES[name]
+    params = randomize(cfg, cngpt_amd.init_weights(cfg, 31), 32)
+    ref = oracle.Trainer(ocfg(cfg), params, B, T)
+    ref.set_dropout(p)
+    batches = [batch(cfg, B, T, 40 + i) for i in range(2)]
+    oracle.srand(2024)
+    ref_losses = []
+    for tok, tgt in batches:
+        ref.zero_grad()
+        ref_losses.append(ref.forward(tok, tgt))
+        ref.backward()
+        ref.adamw(3e-3)
+    with cngpt_amd.Model(cfg, params) as m, cngpt_amd.Trainer(m, B, T) as tr:
+        tr.set_dropout(p)
+        oracle.srand(2024)
+        for i, (tok, tgt) in enumerate(batches):
+            say(f"{name}: dropout {p}, step {i}")
+            tr.zero_grad()
+            loss = tr.forward(tok, tgt)
+            tr.backward()
+            # step 1 starts from weights updated on both sides (Adam may flip
+            # the sign of a near-zero gradient element's step: see above)
+            assert abs(loss - ref_losses[i]) <= (1e-5 if i == 0 else 1e-4) * abs(ref_losses[i]), \
+                (i, loss, ref_losses[i])
+            if i == 0:
+                # the first step's gradients against a fresh oracle step
+                chk = oracle.Trainer(ocfg(cfg), params, B, T)
+                chk.set_dropout(p)
+                oracle.srand(2024)
+                chk.zero_grad()
+                chk.forward(*batches[0])
+                chk.backward()
+                compare_grads(cfg, tr.grads, chk.grads, what=f"{name} dropout {p}")
+                chk.close()   # its forward left the stream where step 0 left it
+            tr.adamw(3e-3)
+        params_dev = tr.params
+    err = np.abs(params_dev - ref.params)
+    assert float(err.max()) <= 2 * 3e-3 * 2
+    assert np.mean(err > 1e-5) < 1e-2
+    ref.close()
+
+
+def test_dropout_rate_outside_range_is_refused():
+    cfg, B, T = CASES["tiny"]
+    with cngpt_amd.Model(cfg, cngpt_amd.init_weights(cfg, 1)) as m, cngpt_amd.Trainer(m, B, T) as tr:
+        for p in (1.0, -0.1, float("nan")):
+            with pytest.raises(cngpt_amd.CngptError):
+                tr.set_dropout(p)
+        tr.set_dropout(0.0)
