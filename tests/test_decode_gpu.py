@@ -407,3 +407,22 @@ def test_profiler_environment_turns_graph_replay_off(monkeypatch, capfd):
         assert np.isfinite(a).all()
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
     say("decode B=6 with the profiler environment: direct launches, bit-identical")
+
+
+def test_prefill_of_four_sequences_on_whole_round_tiles():
+    """A 4 x 300-token prompt (1200 rows): QKV and fc run 64 x 96 tiles
+    that fill whole rounds of CUs, QKV writing each sequence's rows into its
+    part of the KV cache (rows of 300 at a stride of the capacity); the
+    prefill's logits and four greedy steps against the oracle."""
+    cfg = cngpt_amd.Config(2, 12, 768, 50257, 512)
+    params = randomize(cfg, cngpt_amd.init_weights(cfg, 9), 10)
+    prompt = np.random.default_rng(8).integers(0, cfg.vocab_size, size=(4, 300), dtype=np.int32)
+    with cngpt_amd.Model(cfg, params) as m:
+        got = [m.decode_begin(prompt, capacity=310)]
+        for _ in range(4):
+            got.append(m.decode_step(got[-1].argmax(-1).astype(np.int32)))
+    toks = np.stack([g.argmax(-1) for g in got[:-1]], axis=1).astype(np.int32)
+    seq = np.concatenate([prompt, toks], axis=1)
+    ref = oracle.forward(ocfg(cfg), params, seq, oracle.ALL)[:, 299:]
+    say("prefill 4 x 300 (whole-round tiles) + 4 steps")
+    compare(np.stack(got, axis=1), ref, what="B=4 T=300 prefill and steps")
