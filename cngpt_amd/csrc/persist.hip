@@ -63,7 +63,9 @@ constexpr int PW = 7;                  // compute wavefronts per workgroup
 constexpr int PT = (PW + 1) * 64;      // + the control wavefront: 2 per SIMD
 constexpr int PHASES = 5;              // phases per layer
 constexpr int UPW = 4;                 // lm_head columns per wavefront in flight
-constexpr int NJQ = 2;                 // QKV / fc columns per wavefront (4C <= NJQ * 7G)
+constexpr int NJQ = 2;                 // fc columns per wavefront (4C <= NJQ * 7G)
+constexpr int NJA = 3;                 // QKV columns per wavefront of the workgroups
+                                       // after the column owners (3C <= NJA * 7 (G - owners))
 constexpr int KPW = 16;                // attention keys per wavefront
 constexpr int PMAXS = 16;              // attention splits per head
 constexpr long SPIN_LIMIT = 1L << 20;  // polls of one value before giving up
@@ -334,6 +336,15 @@ __device__ __forceinline__ int slot_col(int slot, int N, int CW, int& j, int& q)
     const int c = CW * j + blockIdx.x * PW + q;
     return c < N ? c : -1;
 }
+// The same for the QKV columns, which only the workgroups after the
+// c_proj / proj column owners compute (CWA = PW * (G - owners) wavefronts).
+__device__ __forceinline__ int slot_cola(int slot, int N, int CWA, int owners, int& j, int& q) {
+    j = slot / PW;
+    q = slot - j * PW;
+    if (j >= NJA) return -1;
+    const int c = CWA * j + ((int)blockIdx.x - owners) * PW + q;
+    return c < N ? c : -1;
+}
 
 template <int U, bool SAMP>
 __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
@@ -350,6 +361,14 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
     // register array left unwritten on the control path would stay live
     // across every phase)
     const int cw0 = ctrl ? (1 << 29) : blockIdx.x * PW + wave;
+    // QKV columns: only the workgroups after the c_proj / proj column
+    // owners take them (the owners come to A from publishing E's x, later
+    // than the others, and would hold up every head's q, k, v); the owners
+    // skip A and wait for C's inputs
+    const int owners_ = (a.C + PW - 1) / PW;
+    const bool own = (int)blockIdx.x < owners_;
+    const int cwa0 = (ctrl || own) ? (1 << 29) : ((int)blockIdx.x - owners_) * PW + wave;
+    const int CWA = PW * (G - owners_);
     const int C = a.C, C3 = 3 * C, C4 = 4 * C, H = a.H, V = a.V, L = a.L;
     float* actf = (float*)sm.act;
     const TagLayout tl(C, H);
@@ -390,16 +409,19 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
     constexpr bool samp = SAMP;  // the greedy instantiation carries no sampling code
     const float tdiv = a.temp > 0.0f ? a.temp : 1.0f;
     const float scale2 = a.scale * 1.4426950408889634f;
-    // Two weight buffers of UPW * U float4 per lane, NJQ * U of them the
-    // QKV or fc columns, U the c_proj column, 4U the proj column:
-    //   wa[0, 2U): QKV (A), then fc (D)      wa[2U, 4U): proj, first half (E)
+    // Two weight buffers of UPW * U float4 per lane. On the c_proj / proj
+    // column owners NJQ * U of them hold the fc columns, U the c_proj
+    // column, 4U the proj column:
+    //   wa[0, 2U): fc (D)                    wa[2U, 4U): proj, first half (E)
     //   wb[0, U):  c_proj (C)                wb[U, 3U):  proj, second half (E)
+    // on the other workgroups NJA * U the QKV columns, then the fc columns:
+    //   wa[0, 3U): QKV (A), then fc in wa[0, 2U) (D)
     // Loads are issued after a phase's publish into the slots it freed:
     // after A fc and all of proj (the c_proj / proj column owners have no
-    // work in B, which leaves the longest time for their largest loads),
-    // after D the next QKV (the lm_head's first two rounds after the last
-    // layer), after E the next c_proj (and the lm_head's rounds 2 and 3).
-    // The lm_head streams UPW rounds through all of wa.
+    // work in A and B, which leaves the longest time for their largest
+    // loads), after D the next QKV (the lm_head's first two rounds after
+    // the last layer), after E the next c_proj (and the lm_head's rounds 2
+    // and 3). The lm_head streams UPW rounds through all of wa.
     f32x4 wa[NW], wb[NW];
     f32x4 kq[4];             // attention prefetch: K, 16 dims of one key
     float vr[KPW];           // V of 16 keys, one dim
@@ -472,16 +494,22 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
         int j, q;
         return ldg(b + max(slot_col(opaque_v(lane), N, CW, j, q), 0));
     };
+    auto slot_bias_a = [&](const float* b, int N) -> float {
+        int j, q;
+        return ldg(b + max(slot_cola(opaque_v(lane), N, CWA, owners_, j, q), 0));
+    };
 
     const LayerW* layers = a.layers;
-    load_cols<NJQ, U>(wa, layers[0].attn_w, C3, C, cw0, CW, lane);
-    ln_params(layers[0].ln1_w, layers[0].ln1_b);
+    if (!own) {
+        load_cols<NJA, U>(wa, layers[0].attn_w, C3, C, cwa0, CWA, lane);
+        ln_params(layers[0].ln1_w, layers[0].ln1_b);
+    }
     load_cols<1, U>(wb, layers[0].proj_w, C, C, cw0, CW, lane);
-    bo = slot_bias(layers[0].attn_b, C3);
+    bo = own ? 0.f : slot_bias_a(layers[0].attn_b, C3);
 
     for (int step = 0; step < a.n_steps; step++, t++) {
         // opaque copies per iteration (see opaque_s)
-        const int lane1 = opaque_v(lane), cw1 = opaque_s(cw0);
+        const int lane1 = opaque_v(lane), cw1 = opaque_s(cw0), cwa1 = opaque_s(cwa0);
         const int cw = cw1;
         const unsigned sbase = a.tag0 + (unsigned)step * per_step;
         // ---------------- embedding x = wte[tok] + wpe[t] (fast.c:245-254)
@@ -492,7 +520,7 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
         if (blockIdx.x == 0 && tid == 0) a.hist[t] = tok;
 
         for (int l = 0; l < L; l++) {
-            const int lane = opaque_v(lane1), cw = opaque_s(cw1);
+            const int lane = opaque_v(lane1), cw = opaque_s(cw1), cwa = opaque_s(cwa1);
             const LayerW P = layers[l];
             const LayerW PN = layers[min(l + 1, L - 1)];
             float* kvl = a.cache + (long)l * a.cap * C3;
@@ -503,8 +531,9 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
             const unsigned TA = sbase + PHASES * l + 1, TB = TA + 1, TC = TA + 2, TD = TA + 3,
                            TE = TA + 4, TXIN = TA - 1;
 
-            // ---------------- phase A: LayerNorm 1 + QKV into row t
-            if (!fetch_ln(TXIN, l == 0, tok, t)) return;
+            // ---------------- phase A: LayerNorm 1 + QKV into row t (not
+            // on the column owners)
+            if (!own && !fetch_ln(TXIN, l == 0, tok, t)) return;
             // attention split layout for keys 0..t
             const int nk = t + 1;
             // The (head, split) items go to the workgroups after the c_proj /
@@ -557,34 +586,33 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
 #pragma unroll
                 for (int jj = 0; jj < KPW; jj++) vr[jj] = 0.f;
             }
-            if (!ctrl) {
-                float acc[UPW];
-                col_dots<NJQ, U>(acc, wa, sm.act, C3, C, cw, CW, lane);
-                if (lane == 0)
+            if (!own) {
+                if (!ctrl) {
+                    float acc[UPW];
+                    col_dots<NJA, U>(acc, wa, sm.act, C3, C, cwa, CWA, lane);
+                    if (lane == 0)
 #pragma unroll
-                    for (int j = 0; j < UPW; j++) sm.red[j][wave] = acc[j];
-            }
-            __syncthreads();
-            {
-                const float bn = slot_bias(P.proj_b, C);
+                        for (int j = 0; j < UPW; j++) sm.red[j][wave] = acc[j];
+                }
+                __syncthreads();
                 if (ctrl) {
                     int j, q;
-                    const int c = slot_col(lane, C3, CW, j, q);
+                    const int c = slot_cola(lane, C3, CWA, owners_, j, q);
                     if (c >= 0) {
                         const float v = sm.red[j][q] + bo;
                         put(tq + c, v, TA);
                         st_sc(rowt + c, v);  // the cache row, for later steps
                     }
                 }
-                bo = bn;
+                // Weight loads are issued after the phase's publish (the
+                // barrier puts them behind its stores): queued ahead of the
+                // stores they delayed the publish, and a wait the compiler
+                // places for them inside the phase delayed its products.
+                __syncthreads();
             }
-            // Weight loads are issued after the phase's publish (the barrier
-            // puts them behind its stores): queued ahead of the stores they
-            // delayed the publish, and a wait the compiler places for them
-            // inside the phase delayed its products. fc with LayerNorm 2's
-            // gains, and this wavefront's proj column (depth 4C) in wa[2U,
-            // 4U) and wb[U, 3U).
-            __syncthreads();
+            bo = slot_bias(P.proj_b, C);
+            // fc with LayerNorm 2's gains, and, on the column owners, this
+            // wavefront's proj column (depth 4C) in wa[2U, 4U) and wb[U, 3U)
             load_cols<NJQ, U>(wa, P.fc_w, C4, C, cw, CW, lane);
             ln_params(P.ln2_w, P.ln2_b);
             {
@@ -803,8 +831,10 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
             // final LayerNorm's
             __syncthreads();
             if (l + 1 < L) {
-                load_cols<NJQ, U>(wa, PN.attn_w, C3, C, cw, CW, lane);
-                ln_params(PN.ln1_w, PN.ln1_b);
+                if (!own) {
+                    load_cols<NJA, U>(wa, PN.attn_w, C3, C, cwa, CWA, lane);
+                    ln_params(PN.ln1_w, PN.ln1_b);
+                }
             } else {
                 load_cols<2, U>(wa, a.wte, V, C, cw, CW, lane);
                 ln_params(a.lnf_w, a.lnf_b);
@@ -877,7 +907,7 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
             // the last layer, then also the lm_head's rounds 2 and 3)
             load_cols<1, U>(wb, layers[l + 1 < L ? l + 1 : 0].proj_w, C, C, cw, CW, lane);
             if (l + 1 == L) load_cols<2, U, 2 * U>(wa, a.wte, V, C, cw + 2 * CW, CW, lane);
-            bo = slot_bias(PN.attn_b, C3);
+            bo = own ? 0.f : slot_bias_a(PN.attn_b, C3);
         }
 
         // ---------------- phase F: final LayerNorm, lm_head (tied wte), argmax partials
@@ -928,7 +958,7 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
             }
         }
         __syncthreads();
-        bo = slot_bias(layers[0].attn_b, C3);
+        bo = own ? 0.f : slot_bias_a(layers[0].attn_b, C3);
         // sampling: the workgroup's scaled logits (wavefront w holds the
         // first rounds_w of sx[w][.]), their max m_g and sum of expf(x - m_g)
         auto own_logit = [&](bool& have, int& col) -> float {
@@ -959,8 +989,8 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
             put_all(tam + 2 * blockIdx.x, tl.as, b, TF);
             put_all(tam + 2 * blockIdx.x + 1, tl.as, __int_as_float(bi), TF);
         }
-        if (step + 1 < a.n_steps) {
-            load_cols<NJQ, U>(wa, layers[0].attn_w, C3, C, cw, CW, lane1);
+        if (step + 1 < a.n_steps && !own) {
+            load_cols<NJA, U>(wa, layers[0].attn_w, C3, C, cwa1, CWA, lane1);
             ln_params(layers[0].ln1_w, layers[0].ln1_b);
         }
 
@@ -1207,8 +1237,9 @@ bool persist_supported(int C, int H, int V, int cap, int G) {
     // columns per wavefront: QKV and fc at most NJQ, c_proj and proj one
     if (4L * C > NJQ * CW || C > CW || V < 1) return false;
     // attention: H * splits workgroups after the c_proj / proj column
-    // owners, at most PW * KPW keys per split
+    // owners, at most PW * KPW keys per split; QKV on those workgroups
     const int owners = (C + PW - 1) / PW;
+    if (owners >= G || 3L * C > (long)NJA * PW * (G - owners)) return false;
     const int ns = std::min((G - owners) / H, PMAXS);
     if (ns < 1 || (long)ns * PW * KPW < cap) return false;
     return true;
