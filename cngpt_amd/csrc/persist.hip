@@ -64,8 +64,8 @@ constexpr int PT = (PW + 1) * 64;      // + the control wavefront: 2 per SIMD
 constexpr int PHASES = 5;              // phases per layer
 constexpr int UPW = 4;                 // lm_head columns per wavefront in flight
 constexpr int NJQ = 2;                 // fc columns per wavefront (4C <= NJQ * 7G)
-constexpr int NJA = 3;                 // QKV columns per wavefront of the workgroups
-                                       // after the column owners (3C <= NJA * 7 (G - owners))
+constexpr int NJA = 4;                 // QKV columns per wavefront of the QKV workgroups
+                                       // (3C <= NJA * 7 * their count)
 constexpr int KPW = 16;                // attention keys per wavefront
 constexpr int PMAXS = 16;              // attention splits per head
 constexpr long SPIN_LIMIT = 1L << 20;  // polls of one value before giving up
@@ -336,14 +336,33 @@ __device__ __forceinline__ int slot_col(int slot, int N, int CW, int& j, int& q)
     const int c = CW * j + blockIdx.x * PW + q;
     return c < N ? c : -1;
 }
-// The same for the QKV columns, which only the workgroups after the
-// c_proj / proj column owners compute (CWA = PW * (G - owners) wavefronts).
-__device__ __forceinline__ int slot_cola(int slot, int N, int CWA, int owners, int& j, int& q) {
+// The same for the QKV columns, which only workgroups q0 .. G - 1 compute
+// (CWA = PW * (G - q0) wavefronts).
+__device__ __forceinline__ int slot_cola(int slot, int N, int CWA, int q0, int& j, int& q) {
     j = slot / PW;
     q = slot - j * PW;
     if (j >= NJA) return -1;
-    const int c = CWA * j + ((int)blockIdx.x - owners) * PW + q;
+    const int c = CWA * j + ((int)blockIdx.x - q0) * PW + q;
     return c < N ? c : -1;
+}
+
+// Key splits of the attention at position t (nk = t + 1 keys): as few as
+// the workgroup's PW * KPW keys allow, within the workgroups after the
+// c_proj / proj column owners and PMAXS.
+__device__ __forceinline__ int attn_splits(int t, int owners, int G, int H) {
+    const int ns = (t + 1 + PW * KPW - 1) / (PW * KPW);
+    return min(ns, min((G - owners) / H, PMAXS));
+}
+
+// First QKV workgroup of a step at position t: the workgroups after the
+// column owners and the step's (head, split) attention items, as long as
+// they hold NJA columns per wavefront of all 3C; else as many of the last
+// workgroups as do (some of them then also attention items).
+__device__ __forceinline__ int qkv_first(int t, int C, int H, int G) {
+    const int owners = (C + PW - 1) / PW;
+    const int nmin = (3 * C + NJA * PW - 1) / (NJA * PW);
+    const int q0 = owners + H * attn_splits(t, owners, G, H);
+    return max(owners, min(q0, G - nmin));
 }
 
 template <int U, bool SAMP>
@@ -361,14 +380,17 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
     // register array left unwritten on the control path would stay live
     // across every phase)
     const int cw0 = ctrl ? (1 << 29) : blockIdx.x * PW + wave;
-    // QKV columns: only the workgroups after the c_proj / proj column
-    // owners take them (the owners come to A from publishing E's x, later
-    // than the others, and would hold up every head's q, k, v); the owners
-    // skip A and wait for C's inputs
-    const int owners_ = (a.C + PW - 1) / PW;
-    const bool own = (int)blockIdx.x < owners_;
-    const int cwa0 = (ctrl || own) ? (1 << 29) : ((int)blockIdx.x - owners_) * PW + wave;
-    const int CWA = PW * (G - owners_);
+    // QKV columns: only workgroups q0 .. G - 1 of a step take them, those
+    // after the c_proj / proj column owners and the attention items where
+    // they fit (an owner comes to A from publishing E's x, an item from
+    // staging the next layer's keys, both later than the others, and would
+    // hold up every head's q, k, v); the other workgroups skip A. q0 moves
+    // with the step's key splits, so the mapping is formed per step (and
+    // for the next step where its weights are loaded ahead).
+    int q0 = qkv_first(*a.pos, a.C, a.H, G);
+    auto qkv_wave = [&](int first) {
+        return (ctrl || (int)blockIdx.x < first) ? (1 << 29) : ((int)blockIdx.x - first) * PW + wave;
+    };
     const int C = a.C, C3 = 3 * C, C4 = 4 * C, H = a.H, V = a.V, L = a.L;
     float* actf = (float*)sm.act;
     const TagLayout tl(C, H);
@@ -494,22 +516,26 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
         int j, q;
         return ldg(b + max(slot_col(opaque_v(lane), N, CW, j, q), 0));
     };
-    auto slot_bias_a = [&](const float* b, int N) -> float {
+    auto slot_bias_a = [&](const float* b, int N, int first) -> float {
         int j, q;
-        return ldg(b + max(slot_cola(opaque_v(lane), N, CWA, owners_, j, q), 0));
+        return ldg(b + max(slot_cola(opaque_v(lane), N, PW * (G - first), first, j, q), 0));
     };
 
     const LayerW* layers = a.layers;
-    if (!own) {
-        load_cols<NJA, U>(wa, layers[0].attn_w, C3, C, cwa0, CWA, lane);
+    if ((int)blockIdx.x >= q0) {
+        load_cols<NJA, U>(wa, layers[0].attn_w, C3, C, qkv_wave(q0), PW * (G - q0), lane);
         ln_params(layers[0].ln1_w, layers[0].ln1_b);
     }
     load_cols<1, U>(wb, layers[0].proj_w, C, C, cw0, CW, lane);
-    bo = own ? 0.f : slot_bias_a(layers[0].attn_b, C3);
+    bo = (int)blockIdx.x >= q0 ? slot_bias_a(layers[0].attn_b, C3, q0) : 0.f;
 
     for (int step = 0; step < a.n_steps; step++, t++) {
         // opaque copies per iteration (see opaque_s)
-        const int lane1 = opaque_v(lane), cw1 = opaque_s(cw0), cwa1 = opaque_s(cwa0);
+        const int lane1 = opaque_v(lane), cw1 = opaque_s(cw0);
+        // this step's QKV workgroups
+        const int qf = opaque_s(q0);
+        const bool inq = (int)blockIdx.x >= qf;
+        const int CWA = PW * (G - qf);
         const int cw = cw1;
         const unsigned sbase = a.tag0 + (unsigned)step * per_step;
         // ---------------- embedding x = wte[tok] + wpe[t] (fast.c:245-254)
@@ -520,7 +546,7 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
         if (blockIdx.x == 0 && tid == 0) a.hist[t] = tok;
 
         for (int l = 0; l < L; l++) {
-            const int lane = opaque_v(lane1), cw = opaque_s(cw1), cwa = opaque_s(cwa1);
+            const int lane = opaque_v(lane1), cw = opaque_s(cw1), cwa = opaque_s(qkv_wave(qf));
             const LayerW P = layers[l];
             const LayerW PN = layers[min(l + 1, L - 1)];
             float* kvl = a.cache + (long)l * a.cap * C3;
@@ -533,7 +559,7 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
 
             // ---------------- phase A: LayerNorm 1 + QKV into row t (not
             // on the column owners)
-            if (!own && !fetch_ln(TXIN, l == 0, tok, t)) return;
+            if (inq && !fetch_ln(TXIN, l == 0, tok, t)) return;
             // attention split layout for keys 0..t
             const int nk = t + 1;
             // The (head, split) items go to the workgroups after the c_proj /
@@ -544,8 +570,7 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
             // As few splits as the workgroup's PW * KPW keys allow (fewer
             // partials to exchange).
             const int owners = (C + PW - 1) / PW;
-            int ns = (nk + PW * KPW - 1) / (PW * KPW);
-            ns = min(ns, min((G - owners) / H, PMAXS));
+            const int ns = attn_splits(t, owners, G, H);
             const int kps = (nk + ns - 1) / ns;
             const int kpw = (kps + PW - 1) / PW;
             const int item = (int)blockIdx.x - owners;
@@ -586,7 +611,7 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
 #pragma unroll
                 for (int jj = 0; jj < KPW; jj++) vr[jj] = 0.f;
             }
-            if (!own) {
+            if (inq) {
                 if (!ctrl) {
                     float acc[UPW];
                     col_dots<NJA, U>(acc, wa, sm.act, C3, C, cwa, CWA, lane);
@@ -597,7 +622,7 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
                 __syncthreads();
                 if (ctrl) {
                     int j, q;
-                    const int c = slot_cola(lane, C3, CWA, owners_, j, q);
+                    const int c = slot_cola(lane, C3, CWA, qf, j, q);
                     if (c >= 0) {
                         const float v = sm.red[j][q] + bo;
                         put(tq + c, v, TA);
@@ -831,7 +856,7 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
             // final LayerNorm's
             __syncthreads();
             if (l + 1 < L) {
-                if (!own) {
+                if (inq) {
                     load_cols<NJA, U>(wa, PN.attn_w, C3, C, cwa, CWA, lane);
                     ln_params(PN.ln1_w, PN.ln1_b);
                 }
@@ -907,7 +932,7 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
             // the last layer, then also the lm_head's rounds 2 and 3)
             load_cols<1, U>(wb, layers[l + 1 < L ? l + 1 : 0].proj_w, C, C, cw, CW, lane);
             if (l + 1 == L) load_cols<2, U, 2 * U>(wa, a.wte, V, C, cw + 2 * CW, CW, lane);
-            bo = own ? 0.f : slot_bias_a(PN.attn_b, C3);
+            bo = inq ? slot_bias_a(PN.attn_b, C3, qf) : 0.f;
         }
 
         // ---------------- phase F: final LayerNorm, lm_head (tied wte), argmax partials
@@ -958,7 +983,9 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
             }
         }
         __syncthreads();
-        bo = own ? 0.f : slot_bias_a(layers[0].attn_b, C3);
+        // the next step's QKV workgroups (its position is t + 1)
+        q0 = qkv_first(t + 1, C, H, G);
+        bo = (int)blockIdx.x >= q0 ? slot_bias_a(layers[0].attn_b, C3, q0) : 0.f;
         // sampling: the workgroup's scaled logits (wavefront w holds the
         // first rounds_w of sx[w][.]), their max m_g and sum of expf(x - m_g)
         auto own_logit = [&](bool& have, int& col) -> float {
@@ -989,8 +1016,8 @@ __global__ void __launch_bounds__(PT, 1) k_decode_persist(PersistArgs a) {
             put_all(tam + 2 * blockIdx.x, tl.as, b, TF);
             put_all(tam + 2 * blockIdx.x + 1, tl.as, __int_as_float(bi), TF);
         }
-        if (step + 1 < a.n_steps && !own) {
-            load_cols<NJA, U>(wa, layers[0].attn_w, C3, C, cwa1, CWA, lane1);
+        if (step + 1 < a.n_steps && (int)blockIdx.x >= q0) {
+            load_cols<NJA, U>(wa, layers[0].attn_w, C3, C, qkv_wave(q0), PW * (G - q0), lane1);
             ln_params(layers[0].ln1_w, layers[0].ln1_b);
         }
 
@@ -1239,7 +1266,7 @@ bool persist_supported(int C, int H, int V, int cap, int G) {
     // attention: H * splits workgroups after the c_proj / proj column
     // owners, at most PW * KPW keys per split; QKV on those workgroups
     const int owners = (C + PW - 1) / PW;
-    if (owners >= G || 3L * C > (long)NJA * PW * (G - owners)) return false;
+    if (owners >= G || 3L * C > (long)NJA * PW * (G - owners)) return false;   // (qkv_first)
     const int ns = std::min((G - owners) / H, PMAXS);
     if (ns < 1 || (long)ns * PW * KPW < cap) return false;
     return true;
