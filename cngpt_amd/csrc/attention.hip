@@ -210,23 +210,57 @@ __global__ void __launch_bounds__(256, 2)
 // running max m, sum l and O^T as above; the four are merged through LDS
 // in wavefront order (O = sum_w 2^(m_w - M) O_w / sum_w 2^(m_w - M) l_w,
 // M = max_w m_w; a wavefront with no block has m = -inf and adds zero).
-template <int HS>
+//
+// With CB > 0 (HS = 64) the workgroup also applies its head's share of the
+// c_proj product (reference fast.c:299-303: the head outputs are the k
+// range h * 64 .. +63 of that product's inner dimension): a launch has
+// C / (64 CB) workgroups per (query block, sequence, head), workgroup slice
+// sl owning output columns n0 = 64 CB sl .. +64 CB (16 CB per wavefront);
+// it multiplies its merged 32 x 64 head output by W[n0 .. ][h * 64 .. +63]
+// (streamed global -> LDS when the workgroup starts, under the attention)
+// and writes the partial sums part[(h * rows + row) * C + n] for the rows
+// of x (row = b * T + t); the sum over heads in head order, the bias, the
+// residual and the next LayerNorm follow in one launch (launch_sum_heads).
+template <int HS, int CB>
 __global__ void __launch_bounds__(256, 2)
     k_attn_ks(const float* __restrict__ qkv, long seq_stride, float* __restrict__ out, int B,
-              int T, int C, int H, int nqb, float scale, float* __restrict__ lse) {
+              int T, int C, int H, int nqb, float scale, float* __restrict__ lse,
+              const float* __restrict__ W, float* __restrict__ part) {
     constexpr int HALF = HS / 2;
     constexpr int NDB = (HS + 31) / 32;
     constexpr int OS = NDB * 32 + 1;  // LDS row of a merged query
+    static_assert(CB == 0 || HS == 64, "the fused c_proj takes 64-wide heads");
+    constexpr int PS = 68;            // LDS row of a normalised query (fused c_proj)
     __shared__ float om[4][32], ol[4][32];
     __shared__ float oo[4][32 * OS];
+    // fused c_proj: this wavefront's CB blocks of 16 weight rows (columns of
+    // the output) x 64 k, granule q of row c at slot q ^ c; the normalised
+    // head output of the 32 queries
+    __shared__ __attribute__((aligned(16))) float wsl[CB ? 4 * CB : 1][CB ? 16 * 64 : 1];
+    __shared__ __attribute__((aligned(16))) float on[CB ? 32 * PS : 1];
 
     const int BH = B * H;
-    const int qb = nqb - 1 - (int)(blockIdx.x / BH);  // longest query blocks first
+    const int NSL = CB ? C / (64 * CB) : 1;  // column slices per (query block, sequence, head)
+    const int qb = nqb - 1 - (int)(blockIdx.x / (BH * NSL));  // longest query blocks first
     const int bh = blockIdx.x % BH;
+    const int sl = CB ? (int)(blockIdx.x / BH) % NSL : 0;
     const int b = bh / H, h = bh % H;
     const long C3 = 3L * C;
     const float* base = qkv + (long)b * seq_stride * C3;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    if constexpr (CB > 0) {
+        // instruction j of block cb: lane i writes row 4 j + i / 16, slot
+        // i % 16, which holds granule (i % 16) ^ row of that weight row
+        const int wv = __builtin_amdgcn_readfirstlane(wave);
+#pragma unroll
+        for (int cb = 0; cb < CB; cb++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int r = 4 * j + (lane >> 4), q = (lane & 15) ^ r;
+                const int n = 64 * CB * sl + 16 * (CB * wv + cb) + r;
+                lds_dma16(W + (long)n * C + h * 64 + 4 * q, &wsl[CB * wv + cb][256 * j]);
+            }
+    }
     const int lr = lane & 31, lh = lane >> 5;
     const int q0 = qb * 32, qi = q0 + lr;
     const int nkb = min(q0 + 31, T - 1) / 32 + 1;  // key blocks up to the diagonal
@@ -336,7 +370,12 @@ __global__ void __launch_bounds__(256, 2)
     __syncthreads();
     for (int i = tid; i < 32 * HS; i += 256) {
         const int q = i / HS, d = i % HS;
-        if (q0 + q >= T) break;
+        if (q0 + q >= T) {
+            // (fused c_proj: rows past T multiply zeros; their sums are not stored)
+            if (CB) on[q * PS + d] = 0.f;
+            if (CB) continue;
+            break;
+        }
         const float mx = fmaxf(fmaxf(om[0][q], om[1][q]), fmaxf(om[2][q], om[3][q]));
         float l = 0.f, v = 0.f;
 #pragma unroll
@@ -345,8 +384,59 @@ __global__ void __launch_bounds__(256, 2)
             l += f * ol[w][q];
             v += f * oo[w][q * OS + d];
         }
-        out[((long)b * T + q0 + q) * C + h * HS + d] = v / l;
-        if (lse && d == 0) lse[((long)b * H + h) * T + q0 + q] = mx + log2f(l);
+        if (CB) {
+            on[q * PS + d] = v / l;
+        } else {
+            out[((long)b * T + q0 + q) * C + h * HS + d] = v / l;
+            if (lse && d == 0) lse[((long)b * H + h) * T + q0 + q] = mx + log2f(l);
+        }
+    }
+    if constexpr (CB > 0) {
+        // the weights have landed (the only loads left in flight) and every
+        // wavefront's normalised rows are in LDS
+        wait_vmcnt<0>();
+        __syncthreads();
+        // 2 x CB blocks of v_mfma_f32_16x16x4f32: lane (c = lane % 16, g =
+        // lane / 16) supplies query row 16 rb + c and weight row 16 cb + c
+        // at k = 16 g + 4 t + e of granule step t
+        const int lc = lane & 15, g = lane >> 4;
+        f32x4 acc[2][CB];
+#pragma unroll
+        for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+            for (int cb = 0; cb < CB; cb++) acc[rb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            f32x4 av[2], bv[CB];
+#pragma unroll
+            for (int rb = 0; rb < 2; rb++)
+                av[rb] = *(const f32x4*)&on[(16 * rb + lc) * PS + 16 * g + 4 * t];
+#pragma unroll
+            for (int cb = 0; cb < CB; cb++)
+                bv[cb] = *(const f32x4*)&wsl[CB * wave + cb][lc * 64 + 4 * ((4 * g + t) ^ lc)];
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+#pragma unroll
+                for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+                    for (int cb = 0; cb < CB; cb++)
+                        acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[rb][e], bv[cb][e],
+                                                                            acc[rb][cb], 0, 0, 0);
+        }
+        // acc[rb][cb][r]: query row 16 rb + 4 g + r, output column 16 cb + lc
+        // of this wavefront's
+        const long rows = (long)B * T;
+#pragma unroll
+        for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int t = q0 + 16 * rb + 4 * g + r;
+                if (t >= T) continue;
+                float* pr = part + ((long)h * rows + (long)b * T + t) * C + 64 * CB * sl +
+                            16 * CB * wave + lc;
+#pragma unroll
+                for (int cb = 0; cb < CB; cb++) pr[16 * cb] = acc[rb][cb][r];
+            }
     }
 }
 
@@ -362,8 +452,8 @@ hipError_t causal_hs(const float* qkv, long seq_stride, float* out, int B, int T
         // key split, B=8 T=1024 (768 blocks) 1.609 -> 1.973 ms
         if ((long)nqb * B * H < 512) {
             const int nqb32 = (T + 31) / 32;
-            k_attn_ks<HS><<<nqb32 * B * H, 256, 0, s>>>(qkv, seq_stride, out, B, T, C, H, nqb32,
-                                                         scale, lse);
+            k_attn_ks<HS, 0><<<nqb32 * B * H, 256, 0, s>>>(qkv, seq_stride, out, B, T, C, H,
+                                                            nqb32, scale, lse, nullptr, nullptr);
             return hipGetLastError();
         }
     }
@@ -385,4 +475,36 @@ hipError_t launch_attention_causal(const float* qkv, long seq_stride, float* out
         case 128: return causal_hs<128>(qkv, seq_stride, out, B, T, C, H, lse, s);
     }
     return hipErrorInvalidValue;
+}
+
+int attention_proj_cb(int B, int T, int C, int H) {
+    if (H <= 0 || C != 64 * H || B <= 0 || T <= 0) return 0;
+    // 16 CB output columns per wavefront: the narrowest of 2, 3 and 4 that
+    // divides C into slices and keeps the launch within one workgroup per
+    // CU, else the widest within two
+    const long qblocks = (long)((T + 31) / 32) * B * H;
+    for (int cb = 2; cb <= 4; cb++)
+        if (C % (64 * cb) == 0 && qblocks * (C / (64 * cb)) <= 256) return cb;
+    for (int cb = 4; cb >= 2; cb--)
+        if (C % (64 * cb) == 0 && qblocks * (C / (64 * cb)) <= 512) return cb;
+    return 0;
+}
+
+hipError_t launch_attention_proj(const float* qkv, long seq_stride, const float* W, float* part,
+                                 int B, int T, int C, int H, int CB, hipStream_t s) {
+    if (B <= 0 || T <= 0) return hipSuccess;
+    if (C != 64 * H || CB < 2 || CB > 4 || C % (64 * CB)) return hipErrorInvalidValue;
+    const int nqb32 = (T + 31) / 32;
+    const unsigned grid = (unsigned)(nqb32 * B * H * (C / (64 * CB)));
+    const float scale = 1.0f / sqrtf(64.0f);
+    if (CB == 4)
+        k_attn_ks<64, 4><<<grid, 256, 0, s>>>(qkv, seq_stride, nullptr, B, T, C, H, nqb32, scale,
+                                              nullptr, W, part);
+    else if (CB == 3)
+        k_attn_ks<64, 3><<<grid, 256, 0, s>>>(qkv, seq_stride, nullptr, B, T, C, H, nqb32, scale,
+                                              nullptr, W, part);
+    else
+        k_attn_ks<64, 2><<<grid, 256, 0, s>>>(qkv, seq_stride, nullptr, B, T, C, H, nqb32, scale,
+                                              nullptr, W, part);
+    return hipGetLastError();
 }

@@ -151,6 +151,9 @@ struct cngpt_hip_ctx {
     };
     bool use_packed = true;
     bool packed_fresh = false;
+    // short prefills: c_proj applied per head inside the attention launch
+    bool use_attn_proj = true;
+    int attn_proj_cb = 0;
     std::vector<Packed> packs;
     std::unordered_map<const float*, const float*> packed_of;
 
@@ -590,6 +593,19 @@ int ensure_arena(cngpt_hip_ctx* h, int B, int T, int all, int kv) {
     return 0;
 }
 
+// Wavefront column blocks of the attention launch with c_proj per head (0:
+// attention and c_proj as two launches). For short prefills (at most 128
+// rows of 64-wide heads), where the c_proj product is a split-K launch of
+// its own whose partials are summed anyway.
+int attn_proj_cb(const cngpt_hip_ctx* h, int B, int T) {
+    const int C = h->cfg.n_embd, H = h->cfg.n_head;
+    const long rows = (long)B * T;
+    if (!h->use_attn_proj || rows <= SKINNY_MAX_M || rows > 128 || C > 2048) return 0;
+    if ((long)H * rows * C > GEMM_PART_FLOATS) return 0;
+    const int cb = attention_proj_cb(B, T, C, H);
+    return cb && h->attn_proj_cb && C % (64 * h->attn_proj_cb) == 0 ? h->attn_proj_cb : cb;
+}
+
 int check_tokens(const cngpt_hip_ctx* h, const int* tokens, long n) {
     for (long i = 0; i < n; i++)
         if (tokens[i] < 0 || tokens[i] >= h->cfg.vocab_size)
@@ -622,20 +638,42 @@ int enqueue_forward(cngpt_hip_ctx* h, int B, int T, int mode, bool kv, bool want
                      kv ? T : 0, seq_stride, 3L * C))
             return -1;
         if (!last) {
-            {
-                double fl = 2.0 * C * (double)T * (T + 1) * B;
-                double by = 4.0 * rows * C * 4;  // q,k,v read + out written
-                Timed t(h, CNGPT_K_ATTN, fl, by);
-                HIP_TRY(launch_attention_causal(qkv, seq_stride, h->aout, B, T, C, H, h->stream));
-            }
             // the next LayerNorm after the MLP: layer l+1's first, or the
             // final one (only in ALL mode, where the last layer is not pruned)
             const bool end = l + 1 == L;
             const float* nw = end ? h->lnf_w : h->layers[l + 1].ln1_w;
             const float* nb = end ? h->lnf_b : h->layers[l + 1].ln1_b;
-            if (run_gemm(h, h->aout, w.proj_w, w.proj_b, h->x, (int)rows, C, C, EPI_RESID, 0, 0,
-                         -1, 0, nullptr, w.ln2_w, w.ln2_b, h->ln) ||
-                run_gemm(h, h->ln, w.fc_w, w.fc_b, h->hid, (int)rows, 4 * C, C, EPI_BIAS_GELU) ||
+            if (const int cb = attn_proj_cb(h, B, T)) {
+                // attention with each head's share of c_proj, then the
+                // sum over heads with the bias, the residual and LayerNorm 2
+                {
+                    double fl = 2.0 * C * (double)T * (T + 1) * B + 2.0 * rows * C * C;
+                    double by = 4.0 * (rows * C * 4 + (double)C * C + (double)H * rows * C);
+                    Timed t(h, CNGPT_K_ATTN, fl, by);
+                    HIP_TRY(launch_attention_proj(qkv, seq_stride, w.proj_w, h->gemm_part, B, T,
+                                                  C, H, cb, h->stream));
+                }
+                GemmArgs a{};
+                a.M = (int)rows; a.N = C; a.K = C;
+                a.bias = w.proj_b; a.Y = h->x; a.ldy = C;
+                a.part = h->gemm_part; a.part_cap = GEMM_PART_FLOATS;
+                a.ln_w = w.ln2_w; a.ln_b = w.ln2_b; a.ln_out = h->ln;
+                a.epi = EPI_RESID;
+                Timed t(h, CNGPT_K_LAYERNORM, 0.0, 4.0 * rows * C * (H + 3));
+                HIP_TRY(launch_sum_heads(a, H, h->stream));
+            } else {
+                {
+                    double fl = 2.0 * C * (double)T * (T + 1) * B;
+                    double by = 4.0 * rows * C * 4;  // q,k,v read + out written
+                    Timed t(h, CNGPT_K_ATTN, fl, by);
+                    HIP_TRY(launch_attention_causal(qkv, seq_stride, h->aout, B, T, C, H,
+                                                    h->stream));
+                }
+                if (run_gemm(h, h->aout, w.proj_w, w.proj_b, h->x, (int)rows, C, C, EPI_RESID, 0,
+                             0, -1, 0, nullptr, w.ln2_w, w.ln2_b, h->ln))
+                    return -1;
+            }
+            if (run_gemm(h, h->ln, w.fc_w, w.fc_b, h->hid, (int)rows, 4 * C, C, EPI_BIAS_GELU) ||
                 run_gemm(h, h->hid, w.mlp_w, w.mlp_b, h->x, (int)rows, C, 4 * C, EPI_RESID, 0, 0,
                          -1, 0, nullptr, nw, nb, h->ln))
                 return -1;
@@ -1326,6 +1364,10 @@ int cngpt_hip_create(int device, cngpt_hip_ctx** out) {
     if (pp && pp[0] == '0') h->decode_path = CNGPT_DECODE_KERNELS;
     const char* pk = getenv("CNGPT_HIP_PACK");
     h->use_packed = !(pk && pk[0] == '0');
+    const char* ap = getenv("CNGPT_HIP_ATTNPROJ");
+    h->use_attn_proj = !(ap && ap[0] == '0');
+    // 2, 3 or 4: that many column blocks per wavefront where they divide C
+    if (ap && ap[0] >= '2' && ap[0] <= '4') h->attn_proj_cb = ap[0] - '0';
     if (hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking) != hipSuccess) {
         delete h;
         return fail("hipStreamCreate failed");

@@ -1601,6 +1601,13 @@ hipError_t launch_pack_w(const float* W, float* Wp, int N, int K, hipStream_t s)
     return hipGetLastError();
 }
 
+hipError_t launch_sum_heads(const GemmArgs& a, int KS, hipStream_t s) {
+    if (a.M <= 0) return hipSuccess;
+    if (KS < 1 || (long)KS * a.M * a.N > a.part_cap || (a.N & 3) || (a.ln_out && a.N > 2048))
+        return hipErrorInvalidValue;
+    return reduce_splits<EPI_RESID>(a, KS, s);
+}
+
 int launch_gemm_splits(const GemmArgs& a) {
     if (a.M <= 0 || a.N <= 0 || a.K <= 0 || (a.K & 3)) return 1;
     int KR;

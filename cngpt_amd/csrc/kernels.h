@@ -58,6 +58,10 @@ hipError_t launch_gemm(const GemmArgs& a, hipStream_t s);
 // Number of K splits launch_gemm uses for a (1: none; then a LayerNorm
 // asked for with ln_out is a launch of its own after the product).
 int launch_gemm_splits(const GemmArgs& a);
+// Y = Y + bias + the sum of KS partial products a.part[ks][M][N] in ks order
+// (the residual epilogue), with the LayerNorm of each row into a.ln_out when
+// it is set (N <= 2048).
+hipError_t launch_sum_heads(const GemmArgs& a, int KS, hipStream_t s);
 // Floats of the packed copy of an [N][K] weight matrix, and the launch
 // that writes it (K a multiple of 4).
 size_t packed_w_floats(int N, int K);
@@ -238,6 +242,16 @@ hipError_t launch_decode_persist(const PersistArgs& a, int G, hipStream_t s);
 // attention backward uses to recompute the probabilities.
 hipError_t launch_attention_causal(const float* qkv, long seq_stride, float* out, int B, int T,
                                    int C, int H, hipStream_t s, float* lse = nullptr);
+// The same attention (64-wide heads, keys split over a workgroup's
+// wavefronts) with each head's share of the c_proj product applied in the
+// launch: part[(h * B * T + row) * C + n] = sum over d of out[row][h * 64 +
+// d] * W[n][h * 64 + d], W the [C][C] c_proj weights; CB (2..4, from
+// attention_proj_cb, 0 = this form does not apply) sets 16 CB output
+// columns per wavefront. launch_sum_heads (gemm.hip) then adds the H
+// partials in head order with the bias and residual, and the LayerNorm.
+int attention_proj_cb(int B, int T, int C, int H);
+hipError_t launch_attention_proj(const float* qkv, long seq_stride, const float* W, float* part,
+                                 int B, int T, int C, int H, int CB, hipStream_t s);
 
 // loss.hip
 // Cross-entropy of rows x V logits against targets [rows]: row_loss[r] =

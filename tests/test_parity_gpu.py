@@ -181,6 +181,31 @@ def test_gpt2_small_split_k_shapes(small):
                 what=f"B={B} T={T} ALL")
 
 
+def test_short_prefills_with_cproj_in_attention(small):
+    """65 to 128 rows of 64-wide heads: the attention launch applies each
+    head's 64 rows of the c_proj inner dimension to its output and writes
+    per-head partials, which one launch sums in head order with the bias,
+    the residual and LayerNorm 2. Ragged query blocks (T not a multiple of
+    32), several sequences, both modes; GPT-2 medium's width (C = 1024, 16
+    heads: 4 column blocks per wavefront) on one layer."""
+    cfg, params, m = small
+    V = cfg.vocab_size
+    for B, T, seed in ((1, 100, 11), (2, 50, 12), (4, 32, 13), (1, 65, 14)):
+        tk = oracle.lcg_tokens(B * T, V, seed=seed).reshape(B, T)
+        say(f"small B={B} T={T} LAST and ALL")
+        compare(m.forward(tk, cngpt_amd.LAST), oracle.forward(ocfg(cfg), params, tk),
+                what=f"B={B} T={T} LAST")
+        compare(m.forward(tk, cngpt_amd.ALL)[-1:],
+                oracle.forward(ocfg(cfg), params, tk[-1:], oracle.ALL), what=f"B={B} T={T} ALL")
+    mcfg = cngpt_amd.Config(1, 16, 1024, 5000, 128)
+    mp = randomize(mcfg, cngpt_amd.init_weights(mcfg, 77), 5)
+    with cngpt_amd.Model(mcfg, mp) as mm:
+        tk = oracle.lcg_tokens(128, mcfg.vocab_size, seed=15).reshape(1, 128)
+        say("C=1024 H=16 B=1 T=128 ALL")
+        compare(mm.forward(tk, cngpt_amd.ALL),
+                oracle.forward(ocfg(mcfg), mp, tk, oracle.ALL), what="C=1024 ALL")
+
+
 def test_gpt2_small_b17_t512(small):
     """8704 rows: 68 row tiles leave the last round of the QKV (1224 tiles)
     and fc (1632 tiles) products under 90 % full at 4 and at 3 workgroups
