@@ -56,6 +56,23 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (7 << 4) | (0xF << 8));
 }
 
+// wait_vmcnt<n>() for 0 <= n < N <= 8 where n is a constant only once the
+// caller's loop is unrolled (the switch then folds to the one wait)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_dyn(int n) {
+    static_assert(N <= 8, "counts up to 7");
+    switch (n) {
+        case 0: wait_vmcnt<0>(); break;
+        case 1: wait_vmcnt<1>(); break;
+        case 2: wait_vmcnt<2>(); break;
+        case 3: wait_vmcnt<3>(); break;
+        case 4: wait_vmcnt<4>(); break;
+        case 5: wait_vmcnt<5>(); break;
+        case 6: wait_vmcnt<6>(); break;
+        default: wait_vmcnt<7>(); break;
+    }
+}
+
 // 16 bytes per lane from global memory into LDS at lds + 16 * lane
 // (global_load_lds_dwordx4, lds wavefront-uniform), issued as assembly so
 // that the compiler tracks neither the load nor the LDS it writes: it would

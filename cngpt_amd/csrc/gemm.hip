@@ -28,10 +28,15 @@
 // step k+1 while step k is multiplied, then into a padded LDS double buffer;
 // the last step zero-fills past K.
 //
-// k_stream: up to 128 rows (64 < M <= 128 when 128 x 128 tiles would be
-// too few), weights streamed once (from their packed copy when the caller
-// has one), input rows through LDS, K split over workgroups when the column
-// tiles are few, or over the wavefronts of narrower tiles up to 32 rows.
+// k_stream: up to 128 rows (32 < M <= 128 when 128 x 128 tiles would be
+// too few and K is not a multiple of 64; k_rows otherwise), weights
+// streamed once (from their packed copy when the caller has one), input
+// rows through LDS, K split over workgroups when the column tiles are few,
+// or over the wavefronts of narrower tiles up to 32 rows.
+//
+// k_rows: 32 < M <= 128 rows, 32-row tiles, both operands through an LDS
+// ring, the four wavefronts splitting every stage's k.
+//
 // Products over M <= 2 rows (single-sequence decode) are k_dgemv in
 // decode.hip.
 #include <algorithm>
@@ -690,36 +695,17 @@ __global__ void __launch_bounds__(ST_NW * 64) k_stream(GemmArgs a, int tiles_n, 
         asm volatile("s_barrier" ::: "memory");
         if (!LAST) issue_x(c + 1, xs[(c + 1) & 1]);
         const float* xb = xs[c & 1];
-#pragma unroll
-        for (int j = 0; j < ST_PF; j++) {
-            const int s = c * ST_PF + j;
-            // step s has landed once at most the later ring loads and the
-            // next chunk are in flight (in the last chunk: the later ring
-            // loads only)
-            if (LAST) {
-                // (j is a constant once the loop is unrolled)
-                switch (ST_PF - 1 - j) {
-                    case 0: wait_vmcnt<0>(); break;
-                    case 1: wait_vmcnt<1>(); break;
-                    case 2: wait_vmcnt<2>(); break;
-                    case 3: wait_vmcnt<3>(); break;
-                    case 4: wait_vmcnt<4>(); break;
-                    case 5: wait_vmcnt<5>(); break;
-                    case 6: wait_vmcnt<6>(); break;
-                    default: wait_vmcnt<7>(); break;
-                }
-            } else {
-                wait_vmcnt<ST_PF - 1 + XI>();
-            }
-            asm volatile("" ::: "memory");
-            const bool kok = kb + 16 * (s * WPB + ph) + g4 < ke;
-            const f32x4 w = *(const f32x4*)&ws[wave][j][4 * lane];
-            f32x4 xf[MB];
+        // the operands of step j: this lane's weight quad and input quads
+        auto read_step = [&](int j, f32x4& w, f32x4 (&xf)[MB]) {
+            w = *(const f32x4*)&ws[wave][j][4 * lane];
 #pragma unroll
             for (int mb = 0; mb < MB; mb++) {
                 const int r = 16 * mb + lc, q = 4 * (j * WPB + ph) + (lane >> 4);
                 xf[mb] = *(const f32x4*)&xb[r * ST_KC + 4 * (q ^ (r & 15))];
             }
+        };
+        auto products = [&](int s, const f32x4& w, const f32x4 (&xf)[MB]) {
+            const bool kok = kb + 16 * (s * WPB + ph) + g4 < ke;
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 const float we = kok ? w[e] : 0.f;
@@ -727,10 +713,66 @@ __global__ void __launch_bounds__(ST_NW * 64) k_stream(GemmArgs a, int tiles_n, 
                 for (int mb = 0; mb < MB; mb++)
                     acc[mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(xf[mb][e], we, acc[mb], 0, 0, 0);
             }
-            if (!LAST) {
-                // the slot is refilled only after its values are in registers
-                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-                issue_w(s + ST_PF);
+        };
+        if constexpr (MB == 1) {
+#pragma unroll
+            for (int j = 0; j < ST_PF; j++) {
+                const int s = c * ST_PF + j;
+                // step s has landed once at most the later ring loads and
+                // the next chunk are in flight (in the last chunk: the later
+                // ring loads only)
+                if (LAST) wait_vmcnt_dyn<ST_PF>(ST_PF - 1 - j);
+                else wait_vmcnt<ST_PF - 1 + XI>();
+                asm volatile("" ::: "memory");
+                f32x4 w, xf[MB];
+                read_step(j, w, xf);
+                products(s, w, xf);
+                if (!LAST) {
+                    // the slot is refilled only after its values are in registers
+                    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                    issue_w(s + ST_PF);
+                }
+            }
+        } else {
+            // two or more row blocks: each step's operands are read while the
+            // previous step's products run (read right before its own
+            // products, the LDS latency sat between every two steps; at one
+            // row block the read-ahead measured no faster). Step jj has
+            // landed once at most the ring loads after it, the next chunk's
+            // input and the refills of the steps before jj - 1 are in
+            // flight: ST_PF - 2 + XI whenever it is waited for, one step
+            // ahead of its products (in the last chunk ST_PF - 1 - jj).
+            auto wait_step = [&](int jj) {
+                if (LAST) wait_vmcnt_dyn<ST_PF>(ST_PF - 1 - jj);
+                else wait_vmcnt<ST_PF - 2 + XI>();
+                asm volatile("" ::: "memory");
+            };
+            f32x4 wc, xc[MB];
+            wait_step(1);
+            read_step(0, wc, xc);
+#pragma unroll
+            for (int j = 0; j < ST_PF; j++) {
+                const int s = c * ST_PF + j;
+                f32x4 wn, xn[MB];
+                if (j + 1 < ST_PF) {
+                    if (j > 0) wait_step(j + 1);
+                    read_step(j + 1, wn, xn);
+                    // (the scheduler would otherwise sink the reads to their use)
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                products(s, wc, xc);
+                if (!LAST) {
+                    // slot j is refilled only after its values are in
+                    // registers: an empty statement that reads them makes the
+                    // compiler wait for their LDS read (and not for step j + 1's)
+                    asm volatile("" ::"v"(wc[0]), "v"(wc[1]), "v"(wc[2]), "v"(wc[3]) : "memory");
+                    issue_w(s + ST_PF);
+                }
+                if (j + 1 < ST_PF) {
+                    wc = wn;
+#pragma unroll
+                    for (int mb = 0; mb < MB; mb++) xc[mb] = xn[mb];
+                }
             }
         }
     };
@@ -944,7 +986,7 @@ __global__ void __launch_bounds__(256, 128 / TM) k_gemm_wide(GemmArgs a, int til
     }
 }
 
-// k_rows: products over 64 < M <= 128 rows whose 128 x 128 tiles would
+// k_rows: products over 32 < M <= 128 rows whose 128 x 128 tiles would
 // leave most CUs idle (the B=1 T=128 forward: 6-24 such tiles per product).
 // A workgroup of four wavefronts owns a 32-row x TN-column tile (TN = 32,
 // 48 or 64: two by TN / 16 blocks of v_mfma_f32_16x16x4f32); each wavefront
@@ -1290,7 +1332,7 @@ hipError_t skinny_epi(const GemmArgs& a, hipStream_t s) {
     return stream_mb<EPI, 8>(a, s);
 }
 
-// k_rows for 64 < M <= 128: the tile width TN and the K split KS with the
+// k_rows for 32 < M <= 128: the tile width TN and the K split KS with the
 // least estimated time, at most one workgroup per CU where possible. A
 // stage costs about (0.15 + 0.0075 TN) us (measured at 128 rows: 0.39 us
 // for TN = 32, 0.51 for 48); launches over the CU count take whole extra
@@ -1345,7 +1387,7 @@ hipError_t rows_epi(const GemmArgs& a, hipStream_t s) {
 // of products whose 128 x 128 tiles would be too few for the CUs (the
 // reference's own B=1 T=128 forward: 6-24 tiles per product), with
 // row-major operands. CNGPT_HIP_STREAM128=0 / 1 forces the choice for
-// 64 < M <= 128 (A/B timing of the two paths).
+// 64 < M <= 128 (A/B timing against the 128 x 128 tiles).
 bool use_stream(const GemmArgs& a) {
     if (a.M <= SKINNY_MAX_M) return true;
     if (a.M > ST_MAX_M || a.km) return false;
@@ -1357,10 +1399,16 @@ bool use_stream(const GemmArgs& a) {
     return (long)((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN) < 256;
 }
 
-// Of those, the ones over more than SKINNY_MAX_M rows with K in whole
-// k_rows stages take k_rows instead of k_stream.
+// Of those, the ones over more than ROWS_MIN_M rows with K in whole k_rows
+// stages take k_rows instead of k_stream. Measured at 33-64 rows (GPT-2
+// small forwards through the host API, final-position logits): B=1 T=64
+// 0.713 -> 0.680 ms per forward, B=2 T=32 0.728 -> 0.695 ms; at 17-32 rows
+// k_stream stays ahead (B=1 T=32 0.593 vs 0.635 ms, GPT-2 XL decode at
+// B=32 3.42 vs 3.53 ms per step).
+constexpr int ROWS_MIN_M = 32;
 bool use_rows(const GemmArgs& a) {
-    return a.M > SKINNY_MAX_M && a.K % RQ_BK == 0 && use_stream(a);
+    return a.M > ROWS_MIN_M && a.M <= ST_MAX_M && !a.km && a.K % RQ_BK == 0 &&
+           (a.M <= SKINNY_MAX_M || use_stream(a));
 }
 
 // Share of the tile slots the last round of a launch fills when `res`

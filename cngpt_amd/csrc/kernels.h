@@ -51,7 +51,8 @@ struct GemmArgs {
     int km;
     long ldx, ldw;
 };
-// M <= SKINNY_MAX_M rows take the weight-streaming k_stream, larger M the
+// M <= SKINNY_MAX_M rows take the weight-streaming k_stream (32 < M <= 128
+// rows the 32-row k_rows tiles where K is a multiple of 64), larger M the
 // 128 x 128 MFMA tiles.
 constexpr int SKINNY_MAX_M = 64;
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t s);

@@ -354,6 +354,34 @@ def test_generate_sampling_gpt2_small_rand_stream():
     say(f"generate sampled small: {n} tokens")
 
 
+def test_generate_sampling_gpt2_small_512_steps_teacher_forced():
+    """The sampled decode leg as measured: GPT-2 small, the 32-token LCG
+    prompt, 513 tokens at temp 0.8 / top-k 40 in one generate call (the
+    whole run inside one persistent launch), fixed uniform draws. Every
+    token is checked against sample_top_k over the oracle's logits of the
+    sequence the device generated (teacher forcing: one oracle forward over
+    all 544 positions), so a draw at a CDF boundary does not end the check."""
+    cfg = cngpt_amd.GPT2_SMALL
+    params = cngpt_amd.init_weights(cfg, 1234)
+    prompt = oracle.lcg_tokens(32, cfg.vocab_size, 777).reshape(1, 32)
+    n = 513
+    draws = np.random.default_rng(7).random(n).astype(np.float32)
+    with cngpt_amd.Model(cfg, params) as m:
+        m.decode_begin(prompt, capacity=32 + n - 1)
+        gen = m.generate(n, 0.8, 40, draws)[0]
+    seq = np.concatenate([prompt[0], gen[:-1]]).reshape(1, -1)
+    ref = oracle.forward(ocfg(cfg), params, seq, oracle.ALL)[0, 31:]
+    near = 0
+    for i in range(n):
+        want = oracle.sample_top_k(ref[i], 0.8, 40, float(draws[i]))
+        if want != gen[i]:
+            # the device logits differ from the oracle's by <= 1e-3
+            assert cdf_gap(ref[i], 0.8, 40, float(draws[i])) < 1e-3, (i, gen[i], want)
+            near += 1
+    say(f"generate sampled small: {n} tokens, {near} at a CDF boundary")
+    assert near <= 3
+
+
 def test_packed_weights_bit_identical_to_row_major(monkeypatch):
     """A handle made with CNGPT_HIP_PACK=0 streams the row-major weights in
     its few-row products instead of their packed copy: the same values in

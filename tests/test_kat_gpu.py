@@ -256,14 +256,17 @@ def test_softmax_error_bound_dense_grid(kat, kind):
     (0, 1100, 4000, 1600, 3), # stream-K: 9 x 32 ragged tiles, residual
     (0, 1280, 7680, 256, 3),  # 600 tiles over 256 workgroups: a whole-tile round, then stream-K
     (0, 1000, 19400, 64, 2),  # 8 x 152 ragged tiles over 512 workgroups: whole-tile round, GELU
-    (0, 37, 100, 3072, 3),    # weight-streaming product, split over K
+    (0, 37, 100, 3072, 3),    # 37 rows: 32 x 32 tiles (k_rows), a one-tile-wide K split, residual
+    (0, 33, 768, 768, 3),     # 33 rows: a second row tile of one row, K split, residual
+    (0, 64, 2304, 768, 1),    # 64 rows: two row tiles of k_rows
+    (0, 37, 100, 3040, 3),    # 37 rows, K not a multiple of 64: weight-streaming, split over K
     (0, 5, 2304, 768, 1),     # weight-streaming, QKV width
     (0, 8, 3072, 1024, 1),    # weight-streaming, four wavefronts per column block, no K split
     (0, 13, 4100, 1000, 2),   # two phases per block, ragged columns and K, GELU
     (0, 30, 6400, 1600, 3),   # two phases per block at 30 rows, residual
     (0, 16, 3200, 36, 1),     # four phases per block, K = 36 (one step, three phases empty)
     (2, 8, 4096, 1024, 2),    # packed weights, four phases per block
-    (2, 37, 100, 3072, 3),    # weight-streaming from packed weights, split over K
+    (2, 37, 100, 3040, 3),    # weight-streaming from packed weights, split over K
     (2, 20, 771, 1600, 2),    # packed weights, ragged last column block, GELU
     (2, 100, 333, 36, 1),     # packed, K = 36 (zero-padded last step), 128-row tiles
     (2, 128, 2304, 768, 1),   # 128 rows: 32 x 48 tiles (the packed copy unused)
@@ -301,7 +304,7 @@ def test_gemm_error_bound_float64(kat, path, M, N, K, epi):
 
 
 @pytest.mark.parametrize("M,N,K,epi", [
-    (3, 2304, 768, 1), (24, 3200, 800, 2), (40, 1600, 6400, 3), (64, 50257, 64, 0),
+    (3, 2304, 768, 1), (24, 3200, 800, 2), (40, 1600, 6432, 3), (64, 50257, 96, 0),
     (100, 333, 36, 3), (128, 771, 1280, 1), (8, 3072, 1024, 1), (32, 6400, 1600, 2),
 ])
 def test_gemm_packed_weights_bitwise(kat, M, N, K, epi):

@@ -182,15 +182,17 @@ def test_gpt2_small_split_k_shapes(small):
 
 
 def test_short_prefills_with_cproj_in_attention(small):
-    """65 to 128 rows of 64-wide heads: the attention launch applies each
+    """17 to 128 rows of 64-wide heads: the attention launch applies each
     head's 64 rows of the c_proj inner dimension to its output and writes
     per-head partials, which one launch sums in head order with the bias,
     the residual and LayerNorm 2. Ragged query blocks (T not a multiple of
-    32), several sequences, both modes; GPT-2 medium's width (C = 1024, 16
-    heads: 4 column blocks per wavefront) on one layer."""
+    32), several sequences, both modes, the products on 32-row tiles (33 to
+    128 rows) or weight-streaming (up to 32); GPT-2 medium's width (C =
+    1024, 16 heads: 4 column blocks per wavefront) on one layer."""
     cfg, params, m = small
     V = cfg.vocab_size
-    for B, T, seed in ((1, 100, 11), (2, 50, 12), (4, 32, 13), (1, 65, 14)):
+    for B, T, seed in ((1, 100, 11), (2, 50, 12), (4, 32, 13), (1, 65, 14), (1, 40, 16),
+                       (3, 7, 17), (1, 17, 18), (2, 20, 19)):
         tk = oracle.lcg_tokens(B * T, V, seed=seed).reshape(B, T)
         say(f"small B={B} T={T} LAST and ALL")
         compare(m.forward(tk, cngpt_amd.LAST), oracle.forward(ocfg(cfg), params, tk),
