@@ -15,6 +15,9 @@ logits [16, 1024, 50257] left in HBM. Prints one JSON line:
   decode    greedy single-token steps with the KV cache (B=1: all steps in
             one persistent launch; otherwise one replayed HIP graph per
             step), tok/s and algorithmic HBM bytes / time;
+  batched_decode  the decode halves of the GPT-2 medium (B=8 after a
+            768-token prompt) and XL (B=32 after 32 tokens) workloads,
+            each on a handle of its own, the same figures;
   cpu_baseline  the oracle (C restatement of the reference's fast path with
             OpenBLAS) timed on this host on a bounded sample.
 --workload medium / xl measures GPT-2 medium (prefill B=8, decode B=8 after a
@@ -27,6 +30,7 @@ import json
 import os
 import sys
 import time
+from concurrent.futures import ThreadPoolExecutor
 
 import numpy as np
 
@@ -61,13 +65,25 @@ def lcg_tokens(n: int, vocab: int, seed: int) -> np.ndarray:
 def weights(name: str, cfg):
     """GPT-2 small: the reference's seeded init (srand(1234), the draw order of
     gpt_init_weights). Medium / XL: N(0, 0.02) from numpy's generator (the
-    rand() stream would take minutes for 0.35-1.5 G values)."""
+    rand() stream would take minutes for 0.35-1.5 G values), 64 PCG64
+    streams spawned from the seed, filled by a thread pool."""
     if name == "small":
         return cngpt_amd.init_weights(cfg, SEED), \
             "seeded N(0,0.02) weights (srand 1234, gpt_init_weights order)"
-    p = np.random.default_rng(SEED).standard_normal(cngpt_amd.num_params(cfg), dtype=np.float32)
-    p *= np.float32(0.02)
-    return p, "N(0,0.02) weights from numpy PCG64 seed 1234"
+    n = cngpt_amd.num_params(cfg)
+    p = np.empty(n, np.float32)
+    streams = np.random.SeedSequence(SEED).spawn(64)
+    cuts = np.linspace(0, n, len(streams) + 1).astype(np.int64)
+
+    def fill(i):
+        part = p[cuts[i]:cuts[i + 1]]
+        np.random.Generator(np.random.PCG64(streams[i])).standard_normal(out=part,
+                                                                         dtype=np.float32)
+        part *= np.float32(0.02)
+
+    with ThreadPoolExecutor(min(16, os.cpu_count() or 1)) as ex:
+        list(ex.map(fill, range(len(streams))))
+    return p, "N(0,0.02) weights from 64 numpy PCG64 streams spawned from seed 1234"
 
 
 def prefill(m: cngpt_amd.Model, cfg, B: int, T: int, steps: int, warmup: int,
@@ -232,6 +248,28 @@ def decode(m: cngpt_amd.Model, cfg, B: int, prompt_len: int, steps: int, draws=N
     t0 = time.perf_counter()
     m.generate(steps + 1, **kw)
     return time.perf_counter() - t0, PATHS.get(m.decode_path(), "none")
+
+
+def batched_decode():
+    """The decode halves of the GPT-2 medium and XL workloads, each on a
+    handle of its own: greedy steps of B sequences after a prompt (medium
+    B=8, 256 steps after 768 tokens; XL B=32, 128 steps after 32 tokens),
+    one generate call timed after a warm-up one; HBM fraction of the
+    algorithmic bytes per step (every weight, the cached keys and values)."""
+    out = {}
+    for wname in ("medium", "xl"):
+        wcfg, _, _, dB, prompt, steps = WORKLOADS[wname]
+        p, _ = weights(wname, wcfg)
+        mm = cngpt_amd.Model(wcfg, p)
+        dt, path = decode(mm, wcfg, dB, prompt, steps)
+        nbytes = decode_bytes(wcfg, p.size, dB, prompt, steps)
+        mm.close()
+        del p
+        out[f"{wname}_b{dB}"] = {"model": NAMES[wname], "B": dB, "prompt": prompt,
+                                 "steps": steps, "ms_per_step": round(dt * 1e3 / steps, 4),
+                                 "tok_s": round(steps * dB / dt, 1),
+                                 "hbm_frac": round(nbytes / dt / PEAK_HBM, 4), "path": path}
+    return out
 
 
 def reference_shape(m: cngpt_amd.Model, iters: int = 100, warmup: int = 10):
@@ -438,6 +476,7 @@ def main():
     # training steps on the device at `cngpt train`'s default batch (4 x 1024)
     train = train_leg(m, cfg, 4, 1024, 5, 2) if name == "small" else None
     m.close()
+    bdec = batched_decode() if name == "small" else None
 
     # HBM-side bytes per GEMM launch from the committed rocprofv3 --pmc
     # summary of this workload (FETCH_SIZE + WRITE_SIZE, calibrated).
@@ -515,6 +554,8 @@ def main():
         line["reference_shape"] = ref_shape
     if share:
         line["dp_share"] = share
+    if bdec:
+        line["batched_decode"] = bdec
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(name, cfg, params, args.cpu_budget, B, T)
     if args.copy_calibration:
