@@ -154,6 +154,8 @@ struct cngpt_hip_ctx {
     // short prefills: c_proj applied per head inside the attention launch
     bool use_attn_proj = true;
     int attn_proj_cb = 0;
+    // batched decode: the QKV product's K-split sum inside the attention
+    bool use_qkv_fold = true;
     std::vector<Packed> packs;
     std::unordered_map<const float*, const float*> packed_of;
 
@@ -279,7 +281,7 @@ int run_ln(cngpt_hip_ctx* h, const float* x, long in_stride, const float* w, con
 int run_gemm(cngpt_hip_ctx* h, const float* X, const float* W, const float* bias, float* Y, int M,
              int N, int K, int epi, int seg = 0, long seg_stride = 0, long ldy = -1,
              int row_off = 0, const int* row_off_dev = nullptr, const float* lnw = nullptr,
-             const float* lnb = nullptr, float* lnout = nullptr) {
+             const float* lnb = nullptr, float* lnout = nullptr, int* left_partials = nullptr) {
     const double flops = 2.0 * M * N * K;
     const double bytes =
         4.0 * ((double)M * K + (double)N * K + (double)M * N * (epi == EPI_RESID ? 2 : 1));
@@ -314,6 +316,13 @@ int run_gemm(cngpt_hip_ctx* h, const float* X, const float* W, const float* bias
     const bool ln_in_sum = lnout && launch_gemm_splits(a) > 1;
     if (ln_in_sum) {
         a.ln_w = lnw; a.ln_b = lnb; a.ln_out = lnout;
+    }
+    // left_partials: where the product splits K, its partials stay in
+    // gemm_part for the caller's next kernel to sum (*left_partials = the
+    // splits; 0 where the product writes Y itself)
+    if (left_partials) {
+        *left_partials = lnout ? 0 : launch_gemm_partials(a);
+        a.partials_only = *left_partials > 0;
     }
     {
         Timed t(h, CNGPT_K_GEMM, flops, bytes);
@@ -406,7 +415,7 @@ int run_lm_head(cngpt_hip_ctx* h, const float* x, int M, bool want_tok, int* pos
 int run_attn_row_proj(cngpt_hip_ctx* h, const float* qkv, long seq_stride, int B, int q_pos,
                       const int* pos_dev, int max_keys, const LayerW& w, float* xres,
                       const float* lnw = nullptr, const float* lnb = nullptr,
-                      float* lnout = nullptr) {
+                      float* lnout = nullptr, int qkv_ks = 0) {
     const cngpt_hip_config& c = h->cfg;
     const int C = c.n_embd, hs = C / c.n_head;
     AttnDecArgs a{};
@@ -419,7 +428,12 @@ int run_attn_row_proj(cngpt_hip_ctx* h, const float* qkv, long seq_stride, int B
     a.err = h->dev_err;
     const double keys = pos_dev ? 0.5 * max_keys : q_pos + 1.0;
     if (B > SKINNY && attention_dec_one_pass(B, c.n_head)) {
-        // many (sequence, head) pairs: one pass, rows straight to c_proj's input
+        // many (sequence, head) pairs: one pass, rows straight to c_proj's
+        // input; with qkv_ks the QKV product's partials are summed here
+        if (qkv_ks) {
+            a.qkv_part = h->gemm_part; a.qkv_bias = w.attn_b;
+            a.qkv_ks = qkv_ks; a.qkv_rows = B;
+        }
         {
             Timed t(h, CNGPT_K_ATTN_ROW, 4.0 * C * keys * B,
                     4.0 * ((double)B * keys * 2 * C + (double)B * C));
@@ -428,6 +442,7 @@ int run_attn_row_proj(cngpt_hip_ctx* h, const float* qkv, long seq_stride, int B
         return run_gemm(h, h->aoutc, w.proj_w, w.proj_b, xres, B, C, C, EPI_RESID, 0, 0, -1, 0,
                         nullptr, lnw, lnb, lnout);
     }
+    if (qkv_ks) return fail("QKV partials left for an attention form that does not sum them");
     {
         Timed t(h, CNGPT_K_ATTN_ROW, 4.0 * C * keys * B,
                 4.0 * ((double)B * keys * 2 * C + (double)B * C));
@@ -758,9 +773,11 @@ int enqueue_decode_step(cngpt_hip_ctx* h) {
         HIP_TRY(launch_embed(h->next_tok, h->wte, h->wpe, h->xc, B, 1, C, c.vocab_size, 0, h->pos,
                              h->dev_err, h->hist, cap, h->stream));
     }
+    const bool fold_qkv = fuse_ln && attention_dec_one_pass(B, c.n_head) && h->use_qkv_fold;
     for (int l = 0; l < L; l++) {
         const LayerW& w = h->layers[l];
         float* kvl = h->qkv + (size_t)l * B * cap * 3 * C;
+        int qkv_ks = 0;
         if (l == 0 && fused_embed) {
             // x = wte[token] + wpe[pos] is built inside layer 0's QKV product
             DecGemvArgs d{};
@@ -775,10 +792,13 @@ int enqueue_decode_step(cngpt_hip_ctx* h) {
             Timed t(h, CNGPT_K_GEMV, 2.0 * B * 3 * C * C,
                     4.0 * (3.0 * C * C + 3.0 * B * C + 2.0 * B * C));
             HIP_TRY(launch_dgemv(d, h->stream));
-        } else if (fuse_ln && l > 0) {
-            // LayerNorm 1 was formed with the previous layer's residual
+        } else if (fuse_ln) {
+            // LayerNorm 1 was formed with the previous layer's residual (in
+            // layer 0: here); where the one-pass attention follows and the
+            // product splits K, the attention sums its partials
+            if (l == 0 && run_ln(h, h->xc, C, w.ln1_w, w.ln1_b, h->lnc, B)) return -1;
             if (run_gemm(h, h->lnc, w.attn_w, w.attn_b, kvl, B, 3 * C, C, EPI_BIAS, 1, cap, 3L * C,
-                         0, h->pos))
+                         0, h->pos, nullptr, nullptr, nullptr, fold_qkv ? &qkv_ks : nullptr))
                 return -1;
         } else if (run_ln_gemm(h, h->xc, w.ln1_w, w.ln1_b, h->lnc, w.attn_w, w.attn_b, kvl, B,
                                3 * C, EPI_BIAS, 1, cap, 3L * C, h->pos)) {
@@ -790,7 +810,7 @@ int enqueue_decode_step(cngpt_hip_ctx* h) {
             const bool last = l + 1 == L;
             const LayerW& wn = h->layers[last ? l : l + 1];
             if (run_attn_row_proj(h, kvl, cap, B, 0, h->pos, (int)cap, w, h->xc, w.ln2_w,
-                                  w.ln2_b, h->lnc) ||
+                                  w.ln2_b, h->lnc, qkv_ks) ||
                 run_gemm(h, h->lnc, w.fc_w, w.fc_b, h->hidc, B, 4 * C, C, EPI_BIAS_GELU) ||
                 run_gemm(h, h->hidc, w.mlp_w, w.mlp_b, h->xc, B, C, 4 * C, EPI_RESID, 0, 0, -1, 0,
                          nullptr, last ? h->lnf_w : wn.ln1_w, last ? h->lnf_b : wn.ln1_b,
@@ -1370,6 +1390,8 @@ int cngpt_hip_create(int device, cngpt_hip_ctx** out) {
     h->use_attn_proj = !(ap && ap[0] == '0');
     // 2, 3 or 4: that many column blocks per wavefront where they divide C
     if (ap && ap[0] >= '2' && ap[0] <= '4') h->attn_proj_cb = ap[0] - '0';
+    const char* qf = getenv("CNGPT_HIP_QKVFOLD");
+    h->use_qkv_fold = !(qf && qf[0] == '0');
     if (hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking) != hipSuccess) {
         delete h;
         return fail("hipStreamCreate failed");

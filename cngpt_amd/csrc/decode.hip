@@ -434,8 +434,31 @@ __global__ void __launch_bounds__(NW * 64) k_attn_dec1(AttnDecArgs a, float* __r
     const int kb = (int)((long)half * nk / SPL), nks = (int)((long)(half + 1) * nk / SPL) - kb;
     const int k0 = kb + (int)((long)wave * nks / NW), k1 = kb + (int)((long)(wave + 1) * nks / NW);
     const int npass = (k1 - k0 + KPW - 1) / KPW;
-    const f32x4 q =
-        *(const f32x4*)(base + (long)t * C3 + d4 * 4) * (a.scale * 1.4426950408889634f);
+    // With qkv_part the QKV product left its K-split partials: this head's
+    // q, k and v of row t are their sum in split order plus the bias (the
+    // arithmetic of the split-K sum launch), formed here into LDS, written
+    // to row t of the cache for the later steps (by the first workgroup of
+    // the pair), and taken from LDS for the query and for key t.
+    __shared__ f32x4 cur[3][LPK];
+    const bool fold = a.qkv_part != nullptr;
+    if (fold) {
+        static_assert(NW * 64 >= 3 * HS, "one thread per value of the row");
+        if (tid < 3 * HS) {
+            const int which = tid / HS, d = tid - which * HS;
+            const long c = (long)which * a.C + h * HS + d;
+            const long slab = (long)a.qkv_rows * C3;
+            const float* pp = a.qkv_part + (long)b * C3 + c;
+            float v = 0.f;
+            for (int ks = 0; ks < a.qkv_ks; ks++) v += pp[ks * slab];
+            v = v + a.qkv_bias[c];
+            ((float*)cur)[which * HS + d] = v;
+        }
+        __syncthreads();
+    }
+    const f32x4 q = (fold ? cur[0][d4] : *(const f32x4*)(base + (long)t * C3 + d4 * 4)) *
+                    (a.scale * 1.4426950408889634f);
+    const f32x4 kt = fold ? cur[1][d4] : f32x4{0.f, 0.f, 0.f, 0.f};
+    const f32x4 vt = fold ? cur[2][d4] : f32x4{0.f, 0.f, 0.f, 0.f};
 
     // Rounds of PD passes: every load of a round is issued first (keys
     // past the range re-read its last one; an empty range runs no round),
@@ -448,9 +471,15 @@ __global__ void __launch_bounds__(NW * 64) k_attn_dec1(AttnDecArgs a, float* __r
         f32x4 kr[PD], vr[PD];
 #pragma unroll
         for (int j = 0; j < PD; j++) {
-            const float* rp = base + (long)min(k0 + (p0 + j) * KPW + kl, k1 - 1) * C3 + d4 * 4;
+            const int key = min(k0 + (p0 + j) * KPW + kl, k1 - 1);
+            const float* rp = base + (long)key * C3 + d4 * 4;
             kr[j] = *(const f32x4*)(rp + a.C);
             vr[j] = *(const f32x4*)(rp + 2 * a.C);
+            // (key t's row is not in the cache yet in the folded form: its
+            // values from LDS, by selects, not a branch around the loads)
+            const bool newest = fold && key == t;
+            kr[j] = newest ? kt : kr[j];
+            vr[j] = newest ? vt : vr[j];
         }
         // all of them before the first use (the scheduler would otherwise
         // spread them out to save registers)
@@ -471,6 +500,15 @@ __global__ void __launch_bounds__(NW * 64) k_attn_dec1(AttnDecArgs a, float* __r
             o = in ? on : o;
             m = in ? mn : m;
         }
+    }
+    // (folded form) row t into the cache for the later steps, after this
+    // step's loads so that no wait for it precedes them; the cache is the
+    // caller's writable buffer and row t is this step's, which the product
+    // would otherwise have written
+    if (fold && half == 0 && tid < 3 * HS) {
+        const int which = tid / HS, d = tid - which * HS;
+        const_cast<float*>(base)[(long)t * C3 + (long)which * a.C + d] =
+            ((const float*)cur)[which * HS + d];
     }
     // merge the key groups of a wavefront (a group with no key has m = -inf)
 #pragma unroll
@@ -765,6 +803,7 @@ hipError_t launch_attention_dec_rows(const AttnDecArgs& a, int B, float* out, lo
                                      hipStream_t s) {
     if (B <= 0) return hipSuccess;
     if (!attention_dec_one_pass(B, a.H) || (ldo & 3)) return hipErrorInvalidValue;
+    if (a.qkv_part && (a.qkv_ks < 1 || a.qkv_rows != B || !a.qkv_bias)) return hipErrorInvalidValue;
     switch (a.C / a.H) {
         case 8: return attn_dec1_hs<8>(a, B, out, ldo, s);
         case 16: return attn_dec1_hs<16>(a, B, out, ldo, s);

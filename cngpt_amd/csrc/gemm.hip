@@ -1319,7 +1319,7 @@ hipError_t stream_mb(const GemmArgs& a, hipStream_t s) {
     }
     if (wpb == 1) stream_launch<EPI, MB, 1>(a, tiles_n, KR, KS, s);
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    if (e != hipSuccess || (KS > 1 && a.partials_only)) return e;
     return KS == 1 ? ln_after(a, s) : reduce_splits<EPI>(a, KS, s);
 }
 
@@ -1379,7 +1379,7 @@ hipError_t rows_epi(const GemmArgs& a, hipStream_t s) {
     const hipError_t e = p.TN == 32   ? rows_launch<EPI, 32>(a, p, s)
                          : p.TN == 48 ? rows_launch<EPI, 48>(a, p, s)
                                       : rows_launch<EPI, 64>(a, p, s);
-    if (e != hipSuccess) return e;
+    if (e != hipSuccess || (p.KS > 1 && a.partials_only)) return e;
     return p.KS == 1 ? ln_after(a, s) : reduce_splits<EPI>(a, p.KS, s);
 }
 
@@ -1656,6 +1656,13 @@ hipError_t launch_sum_heads(const GemmArgs& a, int KS, hipStream_t s) {
     return reduce_splits<EPI_RESID>(a, KS, s);
 }
 
+int launch_gemm_partials(const GemmArgs& a) {
+    if (a.M <= 0 || a.N <= 0 || a.K <= 0 || (a.K & 3) || a.ln_out || a.km) return 0;
+    if (!(use_rows(a) || use_stream(a))) return 0;
+    const int KS = launch_gemm_splits(a);
+    return KS > 1 ? KS : 0;
+}
+
 int launch_gemm_splits(const GemmArgs& a) {
     if (a.M <= 0 || a.N <= 0 || a.K <= 0 || (a.K & 3)) return 1;
     int KR;
@@ -1684,6 +1691,9 @@ hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
             return hipErrorInvalidValue;
         return both ? gemm_km<EPI_RESID, 3>(a, s) : gemm_km<EPI_STORE, 2>(a, s);
     }
+    // partials left unsummed: the few-row paths only, without a LayerNorm
+    if (a.partials_only && (a.ln_out || !(use_rows(a) || use_stream(a))))
+        return hipErrorInvalidValue;
     if (use_rows(a)) {
         switch (a.epi) {
             case EPI_STORE: return rows_epi<EPI_STORE>(a, s);

@@ -50,6 +50,10 @@ struct GemmArgs {
     // least M and N rounded up to 4. 0: both K-contiguous, rows of K floats.
     int km;
     long ldx, ldw;
+    // Optional: where K is split (launch_gemm_splits > 1) the launch leaves
+    // the partials in part[ks][M][N] and does not sum them (the caller's
+    // next kernel does: the decode attention folds the QKV sum in).
+    int partials_only;
 };
 // M <= SKINNY_MAX_M rows take the weight-streaming k_stream (32 < M <= 128
 // rows the 32-row k_rows tiles where K is a multiple of 64), larger M the
@@ -59,6 +63,9 @@ hipError_t launch_gemm(const GemmArgs& a, hipStream_t s);
 // Number of K splits launch_gemm uses for a (1: none; then a LayerNorm
 // asked for with ln_out is a launch of its own after the product).
 int launch_gemm_splits(const GemmArgs& a);
+// K splits whose partials a launch with partials_only leaves unsummed (the
+// few-row products with K split, no LayerNorm), 0 where it would not.
+int launch_gemm_partials(const GemmArgs& a);
 // Y = Y + bias + the sum of KS partial products a.part[ks][M][N] in ks order
 // (the residual epilogue), with the LayerNorm of each row into a.ln_out when
 // it is set (N <= 2048).
@@ -157,6 +164,15 @@ struct AttnDecArgs {
     // Optional: a wait of the split form that gives up (its row is then
     // NaN) ORs ATTN_DEC_TIMEOUT into *err.
     int* err;
+    // Optional (launch_attention_dec_rows): the current row's q, k and v are
+    // the sum of qkv_ks partial products qkv_part[ks][b][3 C] (qkv_rows = B
+    // rows per split) in ks order plus qkv_bias (the QKV product launched
+    // with partials_only); each (sequence, head) workgroup forms its head's
+    // 3 * hs values, uses them for the query and the newest key, and writes
+    // them to row t of the cache.
+    const float* qkv_part;
+    const float* qkv_bias;
+    int qkv_ks, qkv_rows;
 };
 constexpr int ATTN_DEC_TIMEOUT = 8;
 size_t attn_dec1_tag_words(int pairs, int hs);

@@ -405,6 +405,34 @@ def test_packed_weights_bit_identical_to_row_major(monkeypatch):
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
+def test_qkv_split_sum_in_attention_bit_identical(monkeypatch):
+    """Batched decode steps whose QKV product splits K and whose attention
+    runs one pass per (sequence, head): the attention sums the QKV partials
+    of its head in split order plus the bias (the arithmetic of the sum
+    launch it replaces) and writes row t of the cache, so every step's
+    logits equal those of a handle made with CNGPT_HIP_QKVFOLD=0 bit for
+    bit. GPT-2 small's width: B=12 (two workgroups per pair, the first
+    writes the row) and B=24 (one per pair)."""
+    cfg = cngpt_amd.Config(2, 12, 768, 1000, 128)
+    params = randomize(cfg, cngpt_amd.init_weights(cfg, 8), 9)
+    for B in (12, 24):
+        prompt = oracle.lcg_tokens(B * 9, cfg.vocab_size).reshape(B, 9) % cfg.vocab_size
+        runs = []
+        for fold in ("1", "0"):
+            monkeypatch.setenv("CNGPT_HIP_QKVFOLD", fold)
+            with cngpt_amd.Model(cfg, params) as m:
+                got = [m.decode_begin(prompt, capacity=24)]
+                toks = got[-1].argmax(-1).astype(np.int32)
+                for _ in range(10):
+                    got.append(m.decode_step(toks))
+                    toks = got[-1].argmax(-1).astype(np.int32)
+            runs.append(got)
+        for a, b in zip(*runs):
+            assert np.isfinite(a).all()
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), B
+        say(f"QKV sum in the attention, B={B}: 10 steps bit-identical")
+
+
 def test_profiler_environment_turns_graph_replay_off(monkeypatch, capfd):
     """In rocprofv3's environment (it exports ROCPROF_OUTPUT_PATH to the
     program it profiles) a handle launches the batched decode step's kernels
