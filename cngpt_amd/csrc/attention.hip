@@ -371,10 +371,13 @@ __global__ void __launch_bounds__(256, 2)
     for (int i = tid; i < 32 * HS; i += 256) {
         const int q = i / HS, d = i % HS;
         if (q0 + q >= T) {
-            // (fused c_proj: rows past T multiply zeros; their sums are not stored)
-            if (CB) on[q * PS + d] = 0.f;
-            if (CB) continue;
-            break;
+            if constexpr (CB > 0) {
+                // rows past T multiply zeros (their sums are not stored)
+                on[q * PS + d] = 0.f;
+                continue;
+            } else {
+                break;
+            }
         }
         const float mx = fmaxf(fmaxf(om[0][q], om[1][q]), fmaxf(om[2][q], om[3][q]));
         float l = 0.f, v = 0.f;
@@ -384,7 +387,7 @@ __global__ void __launch_bounds__(256, 2)
             l += f * ol[w][q];
             v += f * oo[w][q * OS + d];
         }
-        if (CB) {
+        if constexpr (CB > 0) {
             on[q * PS + d] = v / l;
         } else {
             out[((long)b * T + q0 + q) * C + h * HS + d] = v / l;
@@ -424,7 +427,7 @@ __global__ void __launch_bounds__(256, 2)
                                                                             acc[rb][cb], 0, 0, 0);
         }
         // acc[rb][cb][r]: query row 16 rb + 4 g + r, output column 16 cb + lc
-        // of this wavefront's
+        // of this wavefront's 16 CB columns of the slice
         const long rows = (long)B * T;
 #pragma unroll
         for (int rb = 0; rb < 2; rb++)
