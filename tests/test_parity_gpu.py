@@ -187,8 +187,8 @@ def test_short_prefills_with_cproj_in_attention(small):
     per-head partials, which one launch sums in head order with the bias,
     the residual and LayerNorm 2. Ragged query blocks (T not a multiple of
     32), several sequences, both modes, the products on 32-row tiles (33 to
-    128 rows) or weight-streaming (up to 32); GPT-2 medium's width (C =
-    1024, 16 heads: 4 column blocks per wavefront) on one layer."""
+    128 rows) or weight-streaming (up to 32); GPT-2 medium's and large's
+    widths (C = 1024 and 1280) on one layer."""
     cfg, params, m = small
     V = cfg.vocab_size
     for B, T, seed in ((1, 100, 11), (2, 50, 12), (4, 32, 13), (1, 65, 14), (1, 40, 16),
@@ -199,13 +199,16 @@ def test_short_prefills_with_cproj_in_attention(small):
                 what=f"B={B} T={T} LAST")
         compare(m.forward(tk, cngpt_amd.ALL)[-1:],
                 oracle.forward(ocfg(cfg), params, tk[-1:], oracle.ALL), what=f"B={B} T={T} ALL")
-    mcfg = cngpt_amd.Config(1, 16, 1024, 5000, 128)
-    mp = randomize(mcfg, cngpt_amd.init_weights(mcfg, 77), 5)
-    with cngpt_amd.Model(mcfg, mp) as mm:
-        tk = oracle.lcg_tokens(128, mcfg.vocab_size, seed=15).reshape(1, 128)
-        say("C=1024 H=16 B=1 T=128 ALL")
-        compare(mm.forward(tk, cngpt_amd.ALL),
-                oracle.forward(ocfg(mcfg), mp, tk, oracle.ALL), what="C=1024 ALL")
+    # C = 1280, 20 heads (GPT-2 large's width): 80 query blocks take 4 column
+    # blocks per wavefront over 5 slices, 400 workgroups at two per CU
+    for C, H in ((1024, 16), (1280, 20)):
+        mcfg = cngpt_amd.Config(1, H, C, 5000, 128)
+        mp = randomize(mcfg, cngpt_amd.init_weights(mcfg, 77), 5)
+        with cngpt_amd.Model(mcfg, mp) as mm:
+            tk = oracle.lcg_tokens(128, mcfg.vocab_size, seed=15).reshape(1, 128)
+            say(f"C={C} H={H} B=1 T=128 ALL")
+            compare(mm.forward(tk, cngpt_amd.ALL),
+                    oracle.forward(ocfg(mcfg), mp, tk, oracle.ALL), what=f"C={C} ALL")
 
 
 def test_gpt2_small_b17_t512(small):
