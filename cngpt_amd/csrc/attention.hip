@@ -217,7 +217,9 @@ __global__ void __launch_bounds__(256, 2)
 // C / (64 CB) workgroups per (query block, sequence, head), workgroup slice
 // sl owning output columns n0 = 64 CB sl .. +64 CB (16 CB per wavefront);
 // it multiplies its merged 32 x 64 head output by W[n0 .. ][h * 64 .. +63]
-// (streamed global -> LDS when the workgroup starts, under the attention)
+// (streamed global -> LDS once the key loop is done, under the merge of the
+// wavefronts: issued at the start, those loads came before the attention's
+// own in the wait counter's order, so every early wait waited for them too)
 // and writes the partial sums part[(h * rows + row) * C + n] for the rows
 // of x (row = b * T + t); the sum over heads in head order, the bias, the
 // residual and the next LayerNorm follow in one launch (launch_sum_heads).
@@ -248,19 +250,6 @@ __global__ void __launch_bounds__(256, 2)
     const long C3 = 3L * C;
     const float* base = qkv + (long)b * seq_stride * C3;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    if constexpr (CB > 0) {
-        // instruction j of block cb: lane i writes row 4 j + i / 16, slot
-        // i % 16, which holds granule (i % 16) ^ row of that weight row
-        const int wv = __builtin_amdgcn_readfirstlane(wave);
-#pragma unroll
-        for (int cb = 0; cb < CB; cb++)
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int r = 4 * j + (lane >> 4), q = (lane & 15) ^ r;
-                const int n = 64 * CB * sl + 16 * (CB * wv + cb) + r;
-                lds_dma16(W + (long)n * C + h * 64 + 4 * q, &wsl[CB * wv + cb][256 * j]);
-            }
-    }
     const int lr = lane & 31, lh = lane >> 5;
     const int q0 = qb * 32, qi = q0 + lr;
     const int nkb = min(q0 + 31, T - 1) / 32 + 1;  // key blocks up to the diagonal
@@ -355,6 +344,19 @@ __global__ void __launch_bounds__(256, 2)
             }
     }
 
+    if constexpr (CB > 0) {
+        // instruction j of block cb: lane i writes row 4 j + i / 16, slot
+        // i % 16, which holds granule (i % 16) ^ row of that weight row
+        const int wv = __builtin_amdgcn_readfirstlane(wave);
+#pragma unroll
+        for (int cb = 0; cb < CB; cb++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int r = 4 * j + (lane >> 4), q = (lane & 15) ^ r;
+                const int n = 64 * CB * sl + 16 * (CB * wv + cb) + r;
+                lds_dma16(W + (long)n * C + h * 64 + 4 * q, &wsl[CB * wv + cb][256 * j]);
+            }
+    }
     // o[j][r] = O^T[d = 32 j + 8 (r/4) + 4 lh + r%4][query lr]
     if (lh == 0) {
         om[wave][lr] = m_run;
