@@ -42,8 +42,7 @@ __device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
 // accumulated online, the splits read in batches of MB whose loads are in
 // flight together.
 template <int MB>
-__device__ void merge_rows(const MergeArgs& g, int M, f32x4* xs) {
-    const int t = g.pos_dev ? *g.pos_dev : g.q_pos;
+__device__ void merge_rows(const MergeArgs& g, int M, f32x4* xs, int t) {
     const int ns = (t + g.kps) / g.kps;  // splits over keys 0..t
     const int rs = g.hs + 4, h4 = g.hs / 4;
     const int C4 = g.H * h4;
@@ -138,7 +137,15 @@ __global__ void __launch_bounds__(256) k_dgemv(DecGemvArgs a) {
     }
     const f32x4* w4 = (const f32x4*)(a.W + (long)nn * a.K);
 
-    // 1. Weights first: they do not depend on any earlier kernel.
+    // 0. The position the merge of the attention splits needs goes ahead
+    // of the weights: the memory counter completes loads in issue order, so
+    // a wait for a load issued after the weights also waits for all of them.
+    // (The LayerNorm's input rows stay behind the weights: held in
+    // registers across the weight loads they cost a workgroup per CU.)
+    int t_merge = 0;
+    if (SRC == SRC_MERGE) t_merge = a.merge.pos_dev ? *a.merge.pos_dev : a.merge.q_pos;
+
+    // 1. Weights: they do not depend on any earlier kernel.
     f32x4 wp[PRE];
 #pragma unroll
     for (int i = 0; i < PRE; i++) {
@@ -198,7 +205,7 @@ __global__ void __launch_bounds__(256) k_dgemv(DecGemvArgs a) {
         }
         __syncthreads();
     } else if (SRC == SRC_MERGE) {
-        merge_rows<4>(a.merge, M, xs);
+        merge_rows<4>(a.merge, M, xs, t_merge);
     }
 
     // 3. Dot products over this wavefront's K range.
@@ -638,8 +645,8 @@ __global__ void __launch_bounds__(256) k_attn_merge(MergeArgs g, float* __restri
     // every split of a row in one batch, or batches of 4 while the splits
     // are few (a batch past the last split re-reads it)
     const int t = g.pos_dev ? *g.pos_dev : g.q_pos;
-    if ((t + g.kps) / g.kps > 4) merge_rows<MAXS>(gr, 1, xs);
-    else merge_rows<4>(gr, 1, xs);
+    if ((t + g.kps) / g.kps > 4) merge_rows<MAXS>(gr, 1, xs, t);
+    else merge_rows<4>(gr, 1, xs, t);
     const int C4 = g.H * g.hs / 4;
     f32x4* o = (f32x4*)(out + (long)blockIdx.x * ldo);
     for (int c = threadIdx.x; c < C4; c += blockDim.x) o[c] = xs[c];
