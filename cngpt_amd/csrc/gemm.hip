@@ -1427,18 +1427,20 @@ double round_fill(int tiles, int res) {
 }
 
 // Variant choice, from kernel traces of the GPT-2 small / medium / XL
-// forwards (M = 16384 / 8192 / 4096 rows). K a multiple of 32 (every GPT-2
-// width): k_gemm_dl with BK = 32, two stages (64 KB, 2 workgroups per CU),
-// the fastest direct-load variant on every product but one and 1-15 %
-// above k_gemm; the exception is a second round of tiles left part-empty
-// when one round at 4 per CU would hold them all (GPT-2 small's c_proj and
-// proj, 768 tiles: 187 / 611 us with BK = 16 in two 32 KB stages at 4 per
-// CU against 209 / 620 us). K a multiple of 16: BK = 16, three stages (48
-// KB, 3 per CU). Otherwise k_gemm: BK = 16 with rows padded by 4 floats (40
-// KB, 4 per CU) when its tiles fit one round or fill its last round; else
-// BK = 16 at 3 per CU when that fills its last round; else BK = 32 at 2
-// per CU, whose longer K steps hold up best when a round is left
-// part-empty.
+// forwards (M = 16384 / 8192 / 4096 rows). Whole tiles with K a multiple
+// of 16 (every GPT-2 width): k_gemm_dl with BK = 16 in two 32 KB stages, 4
+// workgroups per CU. With each step's products at raised priority (dl_tile)
+// it is at least as fast as BK = 32 in two 64 KB stages at 2 per CU on every
+// product measured (GPT-2 small B=16: fc 593.5 -> 579.5 us, lm_head 9400 ->
+// 9322 us, QKV, c_proj and proj unchanged; GEMM class 83.8 -> 84.1 %;
+// medium B=8 84.3 -> 84.6 %; XL's lm_head and the B=2 share's the same);
+// three 48 KB stages at 3 per CU were slower (82.6-82.9 %). Before the
+// priority BK = 32 at 2 per CU was the faster on every product but GPT-2
+// small's 768-tile c_proj and proj. Otherwise k_gemm: BK = 16 with rows
+// padded by 4 floats (40 KB, 4 per CU) when its tiles fit one round or
+// fill its last round; else BK = 16 at 3 per CU when that fills its last
+// round; else BK = 32 at 2 per CU, whose longer K steps hold up best when
+// a round is left part-empty.
 //
 // Launches of at most 256 tiles (M up to ~2048 rows: short prefills, the
 // reference's own B=1 T=128 shape, one GPU's share of a batch, the
@@ -1613,12 +1615,8 @@ hipError_t gemm_epi(const GemmArgs& a, hipStream_t s) {
         }
         return e != hipSuccess ? e : ln_after(a, s);
     }
-    if (a.K % 32 == 0 && tiles > 2 * cus && tiles <= 4 * cus && round_fill(tiles, 2 * cus) < 0.9)
+    if (a.K % 16 == 0)
         k_gemm_dl<EPI, 16, 2, 4><<<tiles, NTHREADS, 0, s>>>(a, tiles_m, tiles_n, a.K, 1);
-    else if (a.K % 32 == 0)
-        k_gemm_dl<EPI, 32, 2, 2><<<tiles, NTHREADS, 0, s>>>(a, tiles_m, tiles_n, a.K, 1);
-    else if (a.K % 16 == 0)
-        k_gemm_dl<EPI, 16, 3, 3><<<tiles, NTHREADS, 0, s>>>(a, tiles_m, tiles_n, a.K, 1);
     else if (tiles <= 4 * cus || round_fill(tiles, 4 * cus) >= 0.9)
         k_gemm<EPI, 16, 4, 4><<<tiles, NTHREADS, 0, s>>>(a, tiles_m, tiles_n);
     else if (round_fill(tiles, 3 * cus) >= 0.9)
