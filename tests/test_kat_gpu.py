@@ -246,6 +246,9 @@ def test_softmax_error_bound_dense_grid(kat, kind):
     (0, 120, 1024, 4096, 3),  # 32 x 64 tiles with K split 4 ways, ragged rows, residual
     (0, 256, 771, 768, 3),    # two row tiles, ragged columns, K split
     (0, 65, 50, 36, 1),       # register-staged tiles, K = 36, one tile
+    (0, 300, 200, 48, 1),     # whole 128 x 128 tiles at BK = 16 (K = 48: three steps)
+    (0, 2000, 1000, 80, 3),   # whole tiles at BK = 16, K = 80, residual
+    (0, 4100, 1100, 112, 2),  # whole tiles at BK = 16 over more than 256 tiles, GELU
     (0, 2048, 768, 768, 3),   # 64 x 48 tiles, two per CU (M = 2048), residual
     (0, 2048, 768, 3072, 3),  # 64 x 48 tiles over K = 3072, residual
     (0, 2048, 3072, 768, 2),  # 64 x 96 tiles, two rounds at two per CU, GELU
