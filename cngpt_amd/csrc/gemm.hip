@@ -263,12 +263,13 @@ __device__ __forceinline__ void dl_tile(const GemmArgs& a, int m0, int n0, int k
         asm volatile("s_barrier" ::: "memory");
         if (kt + S - 1 < nk) issue(kt + S - 1, (kt + S - 1) % S);
         const float* base = sm + (kt % S) * 2 * TILE;
-        // The two workgroups on a CU run the same step sequence: at raised
-        // priority for its products, a wavefront keeps the SIMD's matrix
-        // unit fed while the other workgroup's wavefront, at the normal
-        // priority, waits, passes its barrier and issues its loads, so the
-        // two drift apart instead of stalling the unit together (GPT-2
-        // small B=16 T=1024 GEMM class 83.0 -> 84.2 % of peak).
+        // The workgroups sharing a CU (two or four) run the same step
+        // sequence: at raised priority for its products, a wavefront keeps
+        // the SIMD's matrix unit fed while another workgroup's wavefront, at
+        // the normal priority, waits, passes its barrier and issues its
+        // loads, so they drift apart instead of stalling the unit together
+        // (GPT-2 small B=16 T=1024 GEMM class 83.0 -> 84.2 % of peak at two
+        // per CU).
         __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int g = 0; g < NG; g++) {
