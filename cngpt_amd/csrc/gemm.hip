@@ -434,8 +434,11 @@ __global__ void __launch_bounds__(256) k_sk_fixup(GemmArgs a, int tiles_m, int t
     group_coords(t0 + t, tiles_m, tiles_n, tm, tn);
     const long roff = a.row_off + (a.row_off_dev ? *a.row_off_dev : 0);
     // float4 c4 = tid + 256 i of this workgroup's SK_RPW rows: row
-    // rb * SK_RPW + c4 / 32, columns 4 (c4 % 32) ..
+    // rb * SK_RPW + c4 / 32, columns 4 (c4 % 32) ..; the residual and the
+    // bias as float4 where the four columns are inside the output and its
+    // rows are 16-byte aligned, else one by one
     constexpr int NI = SK_RPW * BN / 4 / 256;
+    const bool vec = (a.ldy & 3) == 0 && ((size_t)a.Y & 15) == 0;
     // the residual and bias are loaded with the partials: a load after the
     // first store would wait for that store too (the vector-memory counter
     // counts both), one round trip per element
@@ -455,12 +458,20 @@ __global__ void __launch_bounds__(256) k_sk_fixup(GemmArgs a, int tiles_m, int t
         const int rr = min(row[i], a.M - 1);
         long orow = a.seg ? (long)(rr / a.seg) * a.seg_stride + rr % a.seg : rr;
         yo[i] = (orow + roff) * a.ldy;
-        if (EPI == EPI_RESID)
+        const bool whole = vec && col[i] + 3 < a.N;
+        if (EPI == EPI_RESID) {
+            if (whole) old[i] = *(const f32x4*)(a.Y + yo[i] + col[i]);
+            else
 #pragma unroll
-            for (int e = 0; e < 4; e++) old[i][e] = a.Y[yo[i] + min(col[i] + e, a.N - 1)];
-        if (EPI != EPI_STORE)
+                for (int e = 0; e < 4; e++) old[i][e] = a.Y[yo[i] + min(col[i] + e, a.N - 1)];
+        }
+        if (EPI != EPI_STORE) {
+            if (col[i] + 3 < a.N) bb[i] = f32x4{a.bias[col[i]], a.bias[col[i] + 1], a.bias[col[i] + 2],
+                                                a.bias[col[i] + 3]};
+            else
 #pragma unroll
-            for (int e = 0; e < 4; e++) bb[i][e] = a.bias[min(col[i] + e, a.N - 1)];
+                for (int e = 0; e < 4; e++) bb[i][e] = a.bias[min(col[i] + e, a.N - 1)];
+        }
     }
 #pragma unroll
     for (int i = 0; i < NI; i++) {
@@ -475,16 +486,20 @@ __global__ void __launch_bounds__(256) k_sk_fixup(GemmArgs a, int tiles_m, int t
                                  (c4 & 31) * 4);
         }
         if (row[i] >= a.M) continue;
+        f32x4 y;
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-            const int c = col[i] + e;
-            if (c < a.N) {
-                float y = v[e];
-                if (EPI == EPI_BIAS) y += bb[i][e];
-                else if (EPI == EPI_BIAS_GELU) y = gelu_tanh(y + bb[i][e]);
-                else if (EPI == EPI_RESID) y = (old[i][e] + y) + bb[i][e];
-                a.Y[yo[i] + c] = y;
-            }
+            y[e] = v[e];
+            if (EPI == EPI_BIAS) y[e] += bb[i][e];
+            else if (EPI == EPI_BIAS_GELU) y[e] = gelu_tanh(y[e] + bb[i][e]);
+            else if (EPI == EPI_RESID) y[e] = (old[i][e] + y[e]) + bb[i][e];
+        }
+        if (vec && col[i] + 3 < a.N) {
+            *(f32x4*)(a.Y + yo[i] + col[i]) = y;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                if (col[i] + e < a.N) a.Y[yo[i] + col[i] + e] = y[e];
         }
     }
 }
