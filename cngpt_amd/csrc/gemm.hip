@@ -1595,14 +1595,16 @@ hipError_t wide_epi(const GemmArgs& a, const WidePlan& w, hipStream_t s) {
 // products) or W only (a.km == 2, the stored epilogue of the dX products,
 // W the weight matrix as stored: row k = output k of the forward product):
 // whole 128 x 128 tiles, or K split over the CUs when the tiles are too few
-// (no stream-K).
+// (no stream-K); K is a multiple of 32 (checked by the caller), so every
+// split covers whole steps of 16, four workgroups per CU as for the row-major
+// whole tiles.
 template <int EPI, int KM>
 hipError_t gemm_km(const GemmArgs& a, hipStream_t s) {
     const int tiles_m = (a.M + BM - 1) / BM, tiles_n = (a.N + BN - 1) / BN;
     const int tiles = tiles_m * tiles_n;
     int KR;
     const int KS = tile_splits(a, tiles, &KR);
-    k_gemm_dl<EPI, 32, 2, 2, KM><<<tiles * KS, NTHREADS, 0, s>>>(a, tiles_m, tiles_n, KS > 1 ? KR : a.K, KS);
+    k_gemm_dl<EPI, 16, 2, 4, KM><<<tiles * KS, NTHREADS, 0, s>>>(a, tiles_m, tiles_n, KR, KS);
     const hipError_t e = hipGetLastError();
     return e != hipSuccess || KS == 1 ? e : reduce_splits<EPI>(a, KS, s);
 }
